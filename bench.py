@@ -1,0 +1,280 @@
+#!/usr/bin/env python
+"""FP8-KV paged decode attention on one MI355X: KV-read HBM GB/s (% of peak) and µs/call.
+
+One step = one paged decode-attention call (split kernel + split-K combine) over the Qwen3-1.7B-shaped
+FP8 workload (32 sequences, ragged contexts U[256, 4096], pages scattered over a 2x pool), with inputs
+resident in HBM and the L2 / Infinity Cache evicted by a 1 GiB streaming read before every call (outside
+the timed events). `value` = algorithmic KV bytes read per call / mean event-timed call duration.
+
+Also reported: the dominant kernel's roofline (HBM-bound; algorithmic bytes / its event-timed duration
+against 8 TB/s), the oracle timed on the host CPU over a bounded sample of the same workload, and
+µs/call + GB/s for all five measured shapes. Prints ONE JSON line.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "bytes-per-token_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "KV-read HBM GB/s (% of peak) + µs/call, FP8-KV paged decode attention"
+PEAK_GBPS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def timed_calls(call, flush, steps: int, warmup: int):
+    """Warmup, then `steps` cold calls: (total ms per call, split-kernel ms per call, wall seconds)."""
+    import torch
+
+    for _ in range(warmup):
+        call(None)
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    mids = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    for e in mids:
+        e.record()  # create the HIP events whose handles the library records between its kernels
+    torch.cuda.synchronize()  # barrier: one rank, so the synchronize is the barrier
+    t0 = time.perf_counter()
+    for i in range(steps):
+        flush.run()
+        starts[i].record()
+        call(mids[i])
+        ends[i].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    total = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    split = [s.elapsed_time(m) for s, m in zip(starts, mids)]
+    return total, split, wall
+
+
+def measure_workload(name: str, flush, iters: int, warmup: int) -> dict:
+    import torch
+
+    from bpt_amd import measure, paged_decode_attention, quantize_append, workloads
+
+    w = workloads.make(name, device="cuda:0", seed=0)
+    out = torch.empty(tuple(w.q.shape), dtype=torch.bfloat16, device="cuda:0")
+    args, kw = w.args(), w.kwargs()
+
+    def call(ev):
+        paged_decode_attention(*args, **kw, out=out, mid_event=ev)
+
+    total, split, _ = timed_calls(call, flush, iters, warmup)
+    graph = measure.graph_time_ms(lambda: call(None), calls=10, warmup=2, iters=10)
+    nbytes = w.kv_bytes()
+    med = statistics.median(total)
+    row = {
+        "us_per_call": round(med * 1e3, 2),
+        "split_kernel_us": round(statistics.median(split) * 1e3, 2),
+        "graph_warm_us_per_call": round(statistics.median(graph) * 1e3, 2),
+        "kv_bytes": nbytes,
+        "gbps": round(nbytes / (med * 1e-3) / 1e9, 1),
+        "pct_of_peak": round(100 * nbytes / (med * 1e-3) / 1e9 / PEAK_GBPS, 1),
+        "batch": w.shape.batch,
+        "queries": w.shape.queries,
+        "q_heads": w.shape.q_heads,
+        "kv_heads": w.shape.kv_heads,
+        "kv_format": w.shape.kv_format,
+        "scales": w.shape.scales,
+        "sum_context": sum(w.lengths),
+    }
+    if w.unique_tokens != sum(w.lengths):
+        ub = w.kv_bytes(unique=True)
+        row["unique_kv_bytes"] = ub
+        row["unique_gbps"] = round(ub / (med * 1e-3) / 1e9, 1)
+    if name == "qwen3-1.7b-int8":
+        # The step's quantize-on-write: one new row per sequence into slot 15 of its last page.
+        b, hkv = w.shape.batch, w.shape.kv_heads
+        g = torch.Generator(device="cuda:0").manual_seed(5)
+        k_new = torch.randn((b, 1, hkv, 128), generator=g, device="cuda:0").to(torch.bfloat16)
+        v_new = torch.randn((b, 1, hkv, 128), generator=g, device="cuda:0").to(torch.bfloat16)
+        last = torch.tensor([row_[-1] for row_ in w.extra["tables"]], dtype=torch.int32, device="cuda:0").view(b, 1)
+        offs = torch.full((b, 1), 15, dtype=torch.int32, device="cuda:0")
+
+        def write(ev=None):
+            quantize_append(k_new, v_new, w.k_cache, w.v_cache, w.k_scale, w.v_scale, last, offs)
+
+        wt, _, _ = timed_calls(write, flush, iters, warmup)
+        wg = measure.graph_time_ms(write, calls=20, warmup=2, iters=10)
+        row["append_us_per_call"] = round(statistics.median(wt) * 1e3, 2)
+        row["append_graph_us_per_call"] = round(statistics.median(wg) * 1e3, 2)
+        row["append_bytes"] = {"read": b * hkv * 128 * 2 * 2, "written": b * hkv * (128 + 4) * 2}
+    del w, out
+    torch.cuda.empty_cache()
+    return row
+
+
+def cpu_baseline(name: str, budget_s: float) -> dict:
+    """The oracle (numpy float32) on the host over the first sequences of the same workload."""
+    import numpy as np
+
+    from bpt_amd import workloads
+    from oracle import attention
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
+    except Exception:  # threadpoolctl missing: numpy's BLAS thread count is unknown
+        threads = os.cpu_count() or 1
+    w = workloads.make(name, device="cuda:0", seed=0)
+    o = workloads.to_oracle(w)
+    lengths = w.lengths
+
+    def run(n):
+        t = time.perf_counter()
+        attention.paged_decode(o["q"][:n], o["k_pool"], o["v_pool"], o["block_table"][:n], o["context_lens"][:n],
+                               o["k_scale"], o["v_scale"], o["kv_format"], o["scale"])
+        return time.perf_counter() - t
+
+    n = min(4, len(lengths))
+    first = run(n)
+    per_seq = first / n
+    n = max(1, min(len(lengths), int(budget_s / 4 / max(per_seq, 1e-6))))
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 10):
+        times.append(run(n))
+    med = statistics.median(times)
+    hkv = w.shape.kv_heads
+    elem = 2 if w.shape.kv_format == "bf16" else 1
+    nbytes = sum(lengths[:n]) * hkv * 128 * 2 * elem
+    del w, o
+    return {
+        "value": round(nbytes / med / 1e9, 3),
+        "unit": "GB/s",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"oracle paged_decode (numpy float32, BLAS threads={threads}) over the first {n} of the "
+        f"{len(lengths)} sequences ({sum(lengths[:n])} tokens), median of {len(times)} runs: "
+        f"{med * 1e3:.1f} ms per run",
+        "us_per_call_full_workload_est": round(med / sum(lengths[:n]) * sum(lengths) * 1e6, 1),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="qwen3-1.7b-fp8")
+    ap.add_argument("--flush-bytes", type=int, default=1 << 30)
+    ap.add_argument("--no-configs", action="store_true", help="skip the five-shape table")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(
+            "bench.py measures one GPU: the decode path is sharded by sequence or KV head with no exchange, "
+            "and multi-GPU runs are not part of this build (run with --gpus 1)",
+            file=sys.stderr,
+        )
+        return 2
+
+    import torch
+
+    from bpt_amd import measure, paged_decode_attention, workloads
+
+    torch.cuda.set_device(0)
+    log(f"workload {args.workload}: building")
+    w = workloads.make(args.workload, device="cuda:0", seed=0)
+    flush = measure.ReadProbe(args.flush_bytes)
+    out = torch.empty(tuple(w.q.shape), dtype=torch.bfloat16, device="cuda:0")
+    pargs, kw = w.args(), w.kwargs()
+
+    def call(ev):
+        paged_decode_attention(*pargs, **kw, out=out, mid_event=ev)
+
+    log(f"timing {args.steps} cold steps after {args.warmup} warmup")
+    total, split, wall = timed_calls(call, flush, args.steps, args.warmup)
+    nbytes = w.kv_bytes()
+    ms_per_step = statistics.fmean(total)
+    split_ms = statistics.fmean(split)
+    value = nbytes / (ms_per_step * 1e-3) / 1e9
+    achieved = nbytes / (split_ms * 1e-3) / 1e9
+    log(f"{ms_per_step * 1e3:.1f} us/call ({value:.0f} GB/s), split kernel {split_ms * 1e3:.1f} us")
+
+    read_gbps = measure.measured_read_gbps(4 << 30)
+    log(f"read probe: {read_gbps:.0f} GB/s")
+    from bpt_amd import decode_plan
+
+    splits, split_tokens, _ = decode_plan(*pargs, **kw)
+    result = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": args.workload,
+            "batch": w.shape.batch,
+            "queries_per_seq": w.shape.queries,
+            "q_heads": w.shape.q_heads,
+            "kv_heads": w.shape.kv_heads,
+            "head_dim": 128,
+            "page_size": 16,
+            "kv_dtype": "float8_e4m3fn" if w.shape.kv_format == "fp8" else w.shape.kv_format,
+            "scales": w.shape.scales,
+            "sum_context": sum(w.lengths),
+            "kv_bytes_per_call": nbytes,
+            "num_splits": splits,
+            "split_tokens": split_tokens,
+            "timing": f"HIP events around each call, {args.flush_bytes >> 20} MiB read flush before each (untimed)",
+        },
+        "us_per_call": round(ms_per_step * 1e3, 2),
+        "us_per_call_median": round(statistics.median(total) * 1e3, 2),
+        "pct_of_peak": round(100 * value / PEAK_GBPS, 1),
+        "pct_of_measured_read": round(100 * value / read_gbps, 1),
+        "measured_read_gbps": round(read_gbps, 1),
+        "wall_s_timed_region": round(wall, 4),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "decode_split_kernel",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_GBPS, 4),
+            "kernel_us": round(split_ms * 1e3, 2),
+            "traffic": None,
+        },
+    }
+    del w, out, pargs, kw
+    torch.cuda.empty_cache()
+
+    if not args.no_configs:
+        table = {}
+        for name in workloads.SHAPES:
+            log(f"shape {name}")
+            table[name] = measure_workload(name, flush, iters=20, warmup=5)
+        result["configs"] = table
+    if not args.no_cpu_baseline:
+        log("cpu baseline")
+        result["cpu_baseline"] = cpu_baseline(args.workload, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

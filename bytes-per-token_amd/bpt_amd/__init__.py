@@ -1,0 +1,11 @@
+"""bpt_amd — MI355X (gfx950) paged decode attention over FP8 / INT8 / BF16 KV caches.
+
+The decode hot path of fastserve (kernels/kv_attention.py, engine/kv_cache.py, integration/kv_cache.py),
+re-implemented as hand-written HIP kernels behind a C ABI (include/bpt_amd.h, built into libbpt_amd.so)
+with a thin PyTorch-ROCm host layer. Importing needs no GPU; the library loads on first use and raises if
+it has not been built.
+"""
+
+from .paged_attention import decode_plan, kv_read_bytes, paged_decode_attention, quantize_append
+
+__all__ = ["decode_plan", "kv_read_bytes", "paged_decode_attention", "quantize_append"]

@@ -1,0 +1,78 @@
+"""Build the HIP library `libbpt_amd.so` for gfx950 from `csrc/`, in-tree, with hipcc.
+
+Every `.hip` file under `csrc/` is compiled to an object (in parallel), then linked into one shared library
+next to this file, where `_lib.py` loads it. The build always recompiles: it is cheap (seconds per file)
+and it is the "does it build" check.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+CSRC = PKG_DIR.parent / "csrc"
+INCLUDE = PKG_DIR.parent.parent / "include"
+BUILD_DIR = PKG_DIR.parent / "_build"
+LIB_PATH = PKG_DIR / "libbpt_amd.so"
+ARCH = "gfx950"
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-function",
+    # Packed FP32 (v_pk_fma_f32 and friends) stays off: plain float code is compiled to scalar VALU ops.
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+]
+
+
+def hipcc() -> str:
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(path).exists():
+        raise RuntimeError("hipcc not found: the ROCm toolchain is needed to build libbpt_amd.so")
+    return path
+
+
+def _compile(src: Path, obj: Path) -> None:
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src.name}:\n{proc.stderr}")
+    noise = "is not a recognized feature for this target"
+    for line in proc.stderr.splitlines():
+        if line.strip() and noise not in line:
+            print(line)
+
+
+def build(verbose: bool = True) -> Path:
+    """Compile every csrc/*.hip for gfx950 and link libbpt_amd.so. Returns the library path."""
+    BUILD_DIR.mkdir(exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+    if not sources:
+        raise RuntimeError(f"no HIP sources under {CSRC}")
+    objects = [BUILD_DIR / (s.stem + ".o") for s in sources]
+    workers = min(len(sources), int(os.environ.get("MAX_JOBS", "8")), 16)
+    with ThreadPoolExecutor(max_workers=max(workers, 1)) as pool:
+        list(pool.map(_compile, sources, objects))
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"linking libbpt_amd.so failed:\n{proc.stderr}")
+    os.replace(tmp, LIB_PATH)
+    if verbose:
+        print(f"built {LIB_PATH} from {len(sources)} sources for {ARCH}")
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    build()

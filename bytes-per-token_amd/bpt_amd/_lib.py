@@ -1,0 +1,156 @@
+"""ctypes binding of `libbpt_amd.so` (declared in include/bpt_amd.h).
+
+The structures below mirror the C structs field for field; `struct_size` lets the library refuse a binding
+that went stale. Loading fails loudly when the library has not been built: there is no fallback path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import functools
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libbpt_amd.so"
+
+BPT_OK = 0
+BPT_ERR_INVALID_ARGUMENT = 1
+BPT_ERR_HIP = 2
+
+KV_BF16, KV_FP8_E4M3FN, KV_INT8 = 0, 1, 2
+SCALE_NONE, SCALE_PER_HEAD, SCALE_PER_TOKEN_HEAD = 0, 1, 2
+F_BF16, F_F16, F_F32 = 0, 1, 2
+IDX_I32, IDX_I64 = 0, 1
+
+_vp = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+
+
+class DecodeArgs(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("kv_dtype", _i32),
+        ("scale_kind", _i32),
+        ("q_dtype", _i32),
+        ("out_dtype", _i32),
+        ("table_dtype", _i32),
+        ("batch", _i32),
+        ("num_queries", _i32),
+        ("num_q_heads", _i32),
+        ("num_kv_heads", _i32),
+        ("head_dim", _i32),
+        ("page_size", _i32),
+        ("num_blocks", _i32),
+        ("max_blocks_per_seq", _i32),
+        ("max_context", _i32),
+        ("num_splits", _i32),
+        ("split_tokens", _i32),
+        ("sm_scale", ctypes.c_float),
+        ("q", _vp),
+        ("q_stride_b", _i64),
+        ("q_stride_q", _i64),
+        ("q_stride_h", _i64),
+        ("k_cache", _vp),
+        ("v_cache", _vp),
+        ("kv_stride_block", _i64),
+        ("kv_stride_token", _i64),
+        ("kv_stride_head", _i64),
+        ("k_scale", _vp),
+        ("v_scale", _vp),
+        ("scale_stride_block", _i64),
+        ("scale_stride_token", _i64),
+        ("scale_stride_head", _i64),
+        ("block_table", _vp),
+        ("table_stride_b", _i64),
+        ("context_lens", _vp),
+        ("out", _vp),
+        ("out_stride_b", _i64),
+        ("out_stride_q", _i64),
+        ("out_stride_h", _i64),
+        ("workspace", _vp),
+        ("workspace_bytes", ctypes.c_size_t),
+        ("mid_event", _vp),
+    ]
+
+
+class AppendArgs(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("kv_dtype", _i32),
+        ("scale_kind", _i32),
+        ("src_dtype", _i32),
+        ("slot_dtype", _i32),
+        ("batch", _i32),
+        ("num_queries", _i32),
+        ("num_kv_heads", _i32),
+        ("head_dim", _i32),
+        ("page_size", _i32),
+        ("num_blocks", _i32),
+        ("k", _vp),
+        ("v", _vp),
+        ("new_stride_b", _i64),
+        ("new_stride_q", _i64),
+        ("new_stride_h", _i64),
+        ("write_blocks", _vp),
+        ("write_offsets", _vp),
+        ("slot_stride_b", _i64),
+        ("slot_stride_q", _i64),
+        ("k_cache", _vp),
+        ("v_cache", _vp),
+        ("kv_stride_block", _i64),
+        ("kv_stride_token", _i64),
+        ("kv_stride_head", _i64),
+        ("k_scale", _vp),
+        ("v_scale", _vp),
+        ("scale_stride_block", _i64),
+        ("scale_stride_token", _i64),
+        ("scale_stride_head", _i64),
+    ]
+
+
+# Every symbol include/bpt_amd.h declares, with its ctypes signature.
+SIGNATURES = {
+    "bpt_decode_plan": (_i32, [ctypes.POINTER(DecodeArgs), ctypes.POINTER(ctypes.c_size_t)]),
+    "bpt_paged_decode": (_i32, [ctypes.POINTER(DecodeArgs), _vp]),
+    "bpt_quant_append": (_i32, [ctypes.POINTER(AppendArgs), _vp]),
+    "bpt_last_error": (ctypes.c_char_p, []),
+    "bpt_abi_version": (_i32, []),
+    "bpt_fp8_decode_table": (_i32, [_vp, _vp]),
+    "bpt_fp8_encode": (_i32, [_vp, ctypes.c_float, _vp, _i64, _vp]),
+    "bpt_read_probe": (_i32, [_vp, ctypes.c_uint64, _vp, ctypes.POINTER(_i64), _vp]),
+    "bpt_copy_probe": (_i32, [_vp, _vp, ctypes.c_uint64, _vp]),
+}
+
+ABI_VERSION = 1
+
+
+class BptError(RuntimeError):
+    """A HIP runtime error reported by the library."""
+
+
+@functools.cache
+def lib() -> ctypes.CDLL:
+    """The loaded library. Raises if it was never built: the kernels have no fallback."""
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"{LIB_PATH} is not built: run `python __graft_entry__.py` (build()) or "
+            "`python bytes-per-token_amd/bpt_amd/_build.py` first"
+        )
+    handle = ctypes.CDLL(str(LIB_PATH))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = res
+        fn.argtypes = args
+    if handle.bpt_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"libbpt_amd.so ABI {handle.bpt_abi_version()} != binding {ABI_VERSION}: rebuild")
+    return handle
+
+
+def check(rc: int) -> None:
+    """Turn a return code into the exception the reference's callers expect (ValueError for bad args)."""
+    if rc == BPT_OK:
+        return
+    msg = lib().bpt_last_error().decode()
+    if rc == BPT_ERR_INVALID_ARGUMENT:
+        raise ValueError(msg)
+    raise BptError(msg)

@@ -1,0 +1,295 @@
+// The C ABI (include/bpt_amd.h): argument checks, the split-K plan, kernel dispatch, error reporting.
+//
+// Argument checks run on the host before anything is launched and report BPT_ERR_INVALID_ARGUMENT with a
+// message; nothing here reads device memory, so every call stays asynchronous and graph-capturable.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/bpt_amd.h"
+#include "bpt_device.h"
+#include "bpt_internal.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+int hip_fail(const char* where, hipError_t e) {
+  return fail(BPT_ERR_HIP, "%s: HIP error %d (%s)", where, (int)e, hipGetErrorString(e));
+}
+
+bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
+int log2i(int64_t x) {
+  int r = 0;
+  while ((int64_t(1) << r) < x) ++r;
+  return r;
+}
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+int float_bytes(int dt) { return dt == BPT_F_F32 ? 4 : 2; }
+
+// Workgroups the auto plan aims for: enough to keep every CU of a 256-CU MI355X streaming several splits.
+constexpr int64_t kTargetGroups = 2048;
+
+struct Plan {
+  int rows, rows_per_group, n_rg, chunk, split_tokens, num_splits, len_cap;
+  size_t workspace;
+};
+
+int make_plan(const bpt_decode_args* a, Plan* pl) {
+  const char* fn = "bpt_decode_plan";
+  if (!a) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: args is NULL", fn);
+  if (a->struct_size != sizeof(bpt_decode_args))
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: struct_size %u != %zu (stale binding)", fn, a->struct_size,
+                sizeof(bpt_decode_args));
+  if (a->kv_dtype < BPT_KV_BF16 || a->kv_dtype > BPT_KV_INT8)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: unknown kv_dtype %d", fn, a->kv_dtype);
+  if (a->kv_dtype == BPT_KV_BF16 && a->scale_kind != BPT_SCALE_NONE)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: a bf16 cache takes no scales", fn);
+  if (a->kv_dtype != BPT_KV_BF16 && a->scale_kind != BPT_SCALE_PER_HEAD && a->scale_kind != BPT_SCALE_PER_TOKEN_HEAD)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: a quantized cache needs per-head or per-token-head scales", fn);
+  if (a->q_dtype < BPT_F_BF16 || a->q_dtype > BPT_F_F32 || a->out_dtype < BPT_F_BF16 || a->out_dtype > BPT_F_F32)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: q_dtype/out_dtype must be bf16, f16 or f32", fn);
+  if (a->table_dtype != BPT_IDX_I32 && a->table_dtype != BPT_IDX_I64)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: block table must be int32 or int64", fn);
+  if (a->batch < 0 || a->num_queries < 1 || a->num_q_heads < 1 || a->num_kv_heads < 1)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: batch >= 0, num_queries, num_q_heads, num_kv_heads >= 1", fn);
+  if (a->num_q_heads % a->num_kv_heads)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: %d query heads are not a multiple of %d KV heads", fn,
+                a->num_q_heads, a->num_kv_heads);
+  if (a->head_dim != 128) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: head_dim %d not supported (128)", fn, a->head_dim);
+  if (!is_pow2(a->page_size) || a->page_size > 1024)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: page_size %d must be a power of two <= 1024", fn, a->page_size);
+  if (a->num_blocks < 1 || a->max_blocks_per_seq < 1 || a->max_context < 0)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: num_blocks, max_blocks_per_seq >= 1 and max_context >= 0", fn);
+  if (a->num_splits < 0) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: num_splits must be >= 0", fn);
+  if (!std::isfinite(a->sm_scale)) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: sm_scale must be finite", fn);
+  if (a->batch > 65535) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: batch %d exceeds 65535", fn, a->batch);
+
+  const int G = a->num_q_heads / a->num_kv_heads;
+  pl->rows = a->num_queries * G;
+  pl->rows_per_group = pl->rows <= 1 ? 1 : (pl->rows <= 2 ? 2 : 4);
+  pl->n_rg = (pl->rows + pl->rows_per_group - 1) / pl->rows_per_group;
+  if ((int64_t)a->num_kv_heads * pl->n_rg > 65535)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: too many KV heads x row groups", fn);
+  pl->chunk = bpt::decode_chunk_tokens(a->kv_dtype, a->head_dim);
+
+  // Splits never straddle a chunk, and a split's pages must fit the LDS page table.
+  const int64_t max_split = ((int64_t)(bpt::kMaxSplitPages - 1) * a->page_size / pl->chunk) * pl->chunk;
+  const int64_t ctx = a->max_context > 0 ? a->max_context : 1;
+  int64_t split;
+  if (a->num_splits > 0) {
+    split = (ctx + a->num_splits - 1) / a->num_splits;
+    split = (split + pl->chunk - 1) / pl->chunk * pl->chunk;
+  } else {
+    const int64_t units = (int64_t)a->batch * a->num_kv_heads * pl->n_rg;
+    int64_t ideal = units * ctx / kTargetGroups;
+    const int64_t floor_tokens = (int64_t)pl->chunk * bpt::kDecodeWaves;
+    if (ideal < floor_tokens) ideal = floor_tokens;
+    split = 1;
+    while (split * 2 <= ideal) split *= 2;
+    if (split < pl->chunk) split = pl->chunk;
+  }
+  if (split > max_split) split = max_split;
+  if (split < pl->chunk) split = pl->chunk;
+  pl->split_tokens = (int)split;
+  pl->num_splits = (int)((ctx + split - 1) / split);
+  const int64_t table_cap = (int64_t)a->max_blocks_per_seq * a->page_size;
+  pl->len_cap = (int)(a->max_context < table_cap ? a->max_context : table_cap);
+  if (pl->num_splits > 1) {
+    const size_t rows_total = (size_t)a->batch * a->num_queries * a->num_q_heads * pl->num_splits;
+    pl->workspace = rows_total * (size_t)(a->head_dim + 1) * sizeof(float);
+  } else {
+    pl->workspace = 0;
+  }
+  return BPT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* bpt_last_error(void) { return g_error.c_str(); }
+
+int bpt_abi_version(void) { return BPT_ABI_VERSION; }
+
+int bpt_decode_plan(bpt_decode_args* args, size_t* workspace_bytes) {
+  Plan pl;
+  int rc = make_plan(args, &pl);
+  if (rc) return rc;
+  args->num_splits = pl.num_splits;
+  args->split_tokens = pl.split_tokens;
+  if (workspace_bytes) *workspace_bytes = pl.workspace;
+  return BPT_OK;
+}
+
+int bpt_paged_decode(const bpt_decode_args* a, void* stream) {
+  const char* fn = "bpt_paged_decode";
+  Plan pl;
+  int rc = make_plan(a, &pl);
+  if (rc) return rc;
+  if (a->batch == 0) return BPT_OK;
+  if (!a->q || !a->k_cache || !a->v_cache || !a->block_table || !a->context_lens || !a->out)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: q, caches, block_table, context_lens and out must be non-NULL", fn);
+  if (a->kv_dtype != BPT_KV_BF16 && (!a->k_scale || !a->v_scale))
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: k_scale and v_scale are required for a quantized cache", fn);
+  const int eb = a->kv_dtype == BPT_KV_BF16 ? 2 : 1;
+  if (!aligned16(a->k_cache) || !aligned16(a->v_cache) || (a->kv_stride_block * eb) % 16 ||
+      (a->kv_stride_token * eb) % 16 || (a->kv_stride_head * eb) % 16)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: cache pointers and strides must be 16-byte aligned", fn);
+  if (pl.num_splits > 1 && (!a->workspace || a->workspace_bytes < pl.workspace || ((uintptr_t)a->workspace & 3u)))
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: workspace of %zu bytes required for %d splits (got %zu)", fn,
+                pl.workspace, pl.num_splits, a->workspace_bytes);
+
+  bpt::DecodeParams p;
+  p.q = a->q;
+  p.q_sb = a->q_stride_b;
+  p.q_sq = a->q_stride_q;
+  p.q_sh = a->q_stride_h;
+  p.k = (const uint8_t*)a->k_cache;
+  p.v = (const uint8_t*)a->v_cache;
+  p.kv_sblk = a->kv_stride_block * eb;
+  p.kv_stok = a->kv_stride_token * eb;
+  p.kv_shead = a->kv_stride_head * eb;
+  p.ks = a->k_scale;
+  p.vs = a->v_scale;
+  p.sc_sblk = a->scale_stride_block;
+  p.sc_stok = a->scale_stride_token;
+  p.sc_shead = a->scale_stride_head;
+  p.table = a->block_table;
+  p.table_sb = a->table_stride_b;
+  p.lens = a->context_lens;
+  p.out = a->out;
+  p.o_sb = a->out_stride_b;
+  p.o_sq = a->out_stride_q;
+  p.o_sh = a->out_stride_h;
+  p.part_out = (float*)a->workspace;
+  const size_t rows_total = (size_t)a->batch * a->num_queries * a->num_q_heads * pl.num_splits;
+  p.part_lse = pl.num_splits > 1 ? (float*)a->workspace + rows_total * a->head_dim : nullptr;
+  p.B = a->batch;
+  p.Q = a->num_queries;
+  p.Hq = a->num_q_heads;
+  p.Hkv = a->num_kv_heads;
+  p.G = a->num_q_heads / a->num_kv_heads;
+  p.P = a->page_size;
+  p.logP = log2i(a->page_size);
+  p.num_blocks = a->num_blocks;
+  p.max_blocks = a->max_blocks_per_seq;
+  p.S = pl.num_splits;
+  p.split_tokens = pl.split_tokens;
+  p.n_rg = pl.n_rg;
+  p.len_cap = pl.len_cap;
+  p.qscale = a->sm_scale * bpt::kLog2e;
+  p.q_dtype = a->q_dtype;
+  p.out_dtype = a->out_dtype;
+  p.table_i64 = a->table_dtype == BPT_IDX_I64;
+  hipError_t e = bpt::launch_decode(p, a->kv_dtype, a->scale_kind, a->head_dim, pl.rows_per_group,
+                                    (hipStream_t)stream, (hipEvent_t)a->mid_event);
+  if (e != hipSuccess) return hip_fail(fn, e);
+  return BPT_OK;
+}
+
+int bpt_quant_append(const bpt_append_args* a, void* stream) {
+  const char* fn = "bpt_quant_append";
+  if (!a) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: args is NULL", fn);
+  if (a->struct_size != sizeof(bpt_append_args))
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: struct_size %u != %zu (stale binding)", fn, a->struct_size,
+                sizeof(bpt_append_args));
+  if (a->kv_dtype < BPT_KV_BF16 || a->kv_dtype > BPT_KV_INT8)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: unknown kv_dtype %d", fn, a->kv_dtype);
+  if (a->kv_dtype == BPT_KV_BF16 && a->scale_kind != BPT_SCALE_NONE)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: a bf16 cache takes no scales", fn);
+  if (a->kv_dtype != BPT_KV_BF16 && a->scale_kind != BPT_SCALE_PER_HEAD && a->scale_kind != BPT_SCALE_PER_TOKEN_HEAD)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: a quantized cache needs per-head or per-token-head scales", fn);
+  if (a->src_dtype < BPT_F_BF16 || a->src_dtype > BPT_F_F32)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: new rows must be bf16, f16 or f32", fn);
+  if (a->slot_dtype != BPT_IDX_I32 && a->slot_dtype != BPT_IDX_I64)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: write_blocks/write_offsets must be int32 or int64", fn);
+  if (a->batch < 0 || a->num_queries < 0 || a->num_kv_heads < 1 || a->num_blocks < 1 || a->page_size < 1)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: bad sizes", fn);
+  if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: head_dim %d not supported (64, 128, 256)", fn, a->head_dim);
+  if ((int64_t)a->batch * a->num_queries * a->num_kv_heads == 0) return BPT_OK;
+  if (!a->k || !a->v || !a->write_blocks || !a->write_offsets || !a->k_cache || !a->v_cache)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: rows, slots and caches must be non-NULL", fn);
+  if (a->kv_dtype != BPT_KV_BF16 && (!a->k_scale || !a->v_scale))
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: k_scale and v_scale are required for a quantized cache", fn);
+  if ((int64_t)a->batch * a->num_queries * a->num_kv_heads * 2 / 8 >= (int64_t)0x7fffffff)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: too many rows", fn);
+
+  const int eb = a->kv_dtype == BPT_KV_BF16 ? 2 : 1;
+  bpt::AppendParams p;
+  p.k = a->k;
+  p.v = a->v;
+  p.n_sb = a->new_stride_b;
+  p.n_sq = a->new_stride_q;
+  p.n_sh = a->new_stride_h;
+  p.blocks = a->write_blocks;
+  p.offsets = a->write_offsets;
+  p.s_sb = a->slot_stride_b;
+  p.s_sq = a->slot_stride_q;
+  p.kc = (uint8_t*)a->k_cache;
+  p.vc = (uint8_t*)a->v_cache;
+  p.kv_sblk = a->kv_stride_block * eb;
+  p.kv_stok = a->kv_stride_token * eb;
+  p.kv_shead = a->kv_stride_head * eb;
+  p.ks = a->k_scale;
+  p.vs = a->v_scale;
+  p.sc_sblk = a->scale_stride_block;
+  p.sc_stok = a->scale_stride_token;
+  p.sc_shead = a->scale_stride_head;
+  p.B = a->batch;
+  p.Q = a->num_queries;
+  p.Hkv = a->num_kv_heads;
+  p.P = a->page_size;
+  p.num_blocks = a->num_blocks;
+  p.src_dtype = a->src_dtype;
+  p.slot_i64 = a->slot_dtype == BPT_IDX_I64;
+  hipError_t e = bpt::launch_append(p, a->kv_dtype, a->scale_kind, a->head_dim, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(fn, e);
+  return BPT_OK;
+}
+
+int bpt_fp8_decode_table(float* out256, void* stream) {
+  if (!out256) return fail(BPT_ERR_INVALID_ARGUMENT, "bpt_fp8_decode_table: out is NULL");
+  hipError_t e = bpt::launch_fp8_table(out256, (hipStream_t)stream);
+  return e == hipSuccess ? BPT_OK : hip_fail("bpt_fp8_decode_table", e);
+}
+
+int bpt_fp8_encode(const float* x, float scale, uint8_t* out, int64_t n, void* stream) {
+  if (n < 0 || (n > 0 && (!x || !out))) return fail(BPT_ERR_INVALID_ARGUMENT, "bpt_fp8_encode: bad buffers");
+  if (!(scale > 0.0f) || !std::isfinite(scale))
+    return fail(BPT_ERR_INVALID_ARGUMENT, "bpt_fp8_encode: scale must be positive and finite");
+  hipError_t e = bpt::launch_fp8_encode(x, scale, out, n, (hipStream_t)stream);
+  return e == hipSuccess ? BPT_OK : hip_fail("bpt_fp8_encode", e);
+}
+
+int bpt_read_probe(const void* buf, uint64_t bytes, float* partial_sums, int64_t* num_groups, void* stream) {
+  if (bytes % 16) return fail(BPT_ERR_INVALID_ARGUMENT, "bpt_read_probe: bytes must be a multiple of 16");
+  const int64_t g = bpt::read_probe_groups(bytes);
+  if (num_groups) *num_groups = g;
+  if (!partial_sums) return BPT_OK;
+  if (!buf || !aligned16(buf)) return fail(BPT_ERR_INVALID_ARGUMENT, "bpt_read_probe: buffer must be 16-byte aligned");
+  hipError_t e = bpt::launch_read_probe(buf, bytes, partial_sums, (hipStream_t)stream);
+  return e == hipSuccess ? BPT_OK : hip_fail("bpt_read_probe", e);
+}
+
+int bpt_copy_probe(void* dst, const void* src, uint64_t bytes, void* stream) {
+  if (bytes % 16 || !dst || !src || !aligned16(dst) || !aligned16(src))
+    return fail(BPT_ERR_INVALID_ARGUMENT, "bpt_copy_probe: 16-byte aligned buffers, bytes a multiple of 16");
+  if (bytes == 0) return BPT_OK;
+  hipError_t e = bpt::launch_copy_probe(dst, src, bytes, (hipStream_t)stream);
+  return e == hipSuccess ? BPT_OK : hip_fail("bpt_copy_probe", e);
+}
+
+}  // extern "C"

@@ -1,0 +1,176 @@
+/*
+ * bpt_amd.h — C ABI of the MI355X (gfx950) paged decode-attention path.
+ *
+ * Everything here takes plain device pointers, element strides and sizes; no framework types cross the
+ * boundary. Every entry point returns 0 on success, BPT_ERR_INVALID_ARGUMENT for a caller mistake found
+ * on the host (nothing launched), or BPT_ERR_HIP for a HIP runtime error; bpt_last_error() then holds a
+ * thread-local message. Launches go on the caller's stream; nothing synchronizes with the host, so every
+ * call can be captured in a HIP graph. The caller owns caches, block tables, lengths and outputs; the
+ * library writes only outputs and the caller-provided workspace.
+ *
+ * Reference interfaces replaced (paths relative to the fastserve source tree, src/fastserve/):
+ *   bpt_paged_decode     kernels/kv_attention.py:190-245 decode_attention (launcher) and :56-175 (the
+ *                        kernel), kernels/reference.py:205-211 merge_partials (the split-K combine), read
+ *                        through engine/kv_cache.py:165-169 PagedKVCache._gather's block-table layout,
+ *                        with engine/attention.py:12-20 causal_mask for several queries per sequence.
+ *   bpt_quant_append     engine/kv_cache.py:158-161 PagedKVCache.update (scatter write by write_blocks /
+ *                        write_offsets) fused with the quantizers kv/quant.py:44-45 (FP8 cast) and
+ *                        quant/w8a8.py:55-74 / kernels/reference.py:44-55 (per-token INT8, amax/127).
+ *   bpt_decode_plan      kernels/kv_attention.py:178-187 default_split (tokens per program) and the
+ *                        out/lse allocation of :218-220, as a host-only planning call.
+ */
+#ifndef BPT_AMD_H
+#define BPT_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BPT_ABI_VERSION 1
+
+/* return codes */
+#define BPT_OK 0
+#define BPT_ERR_INVALID_ARGUMENT 1
+#define BPT_ERR_HIP 2
+
+/* element type of the KV cache pools */
+typedef enum {
+  BPT_KV_BF16 = 0,        /* no quantization: bfloat16 keys and values                         */
+  BPT_KV_FP8_E4M3FN = 1,  /* OCP e4m3fn codes (0x7F/0xFF NaN, max 448), static per-head scale  */
+  BPT_KV_INT8 = 2         /* symmetric int8 codes, dynamic per-(token, head) scale amax/127     */
+} bpt_kv_dtype;
+
+/* how the fp32 scales are laid out */
+typedef enum {
+  BPT_SCALE_NONE = 0,            /* BF16 cache                                      */
+  BPT_SCALE_PER_HEAD = 1,        /* k_scale[Hkv], v_scale[Hkv]                       */
+  BPT_SCALE_PER_TOKEN_HEAD = 2   /* [num_blocks, page_size, Hkv], same paging as codes */
+} bpt_scale_kind;
+
+/* element type of q / new k, v rows and of the output */
+typedef enum { BPT_F_BF16 = 0, BPT_F_F16 = 1, BPT_F_F32 = 2 } bpt_float_dtype;
+
+/* element type of block tables and write-slot tensors */
+typedef enum { BPT_IDX_I32 = 0, BPT_IDX_I64 = 1 } bpt_index_dtype;
+
+/*
+ * Paged decode attention, Q >= 1 queries per sequence, causal within the query block.
+ *
+ *   q            [B, Q, Hq, D]   strides q_stride_{b,q,h} (elements; channel stride 1)
+ *   k/v_cache    [num_blocks, page_size, Hkv, D] by default; any layout expressible by
+ *                kv_stride_{block,token,head} (elements of the cache type; channel stride 1), so the
+ *                head-major pool [num_blocks, Hkv, page_size, D] and a contiguous [B, Hkv, T, D] cache
+ *                (block b*T/P + t/P, head stride T*D) use the same kernels.
+ *   k/v_scale    fp32; PER_HEAD: [Hkv]; PER_TOKEN_HEAD: strides scale_stride_{block,token,head}
+ *   block_table  [B, max_blocks_per_seq] (row stride table_stride_b) physical page of each logical page
+ *   context_lens [B] int32: tokens in the cache for each sequence, the Q new ones included. Query i of
+ *                sequence b sits at position context_lens[b] - Q + i and sees slots 0 .. that position.
+ *   out          [B, Q, Hq, D] (strides out_stride_{b,q,h}), BF16 or F32
+ *
+ * max_context bounds context_lens and sizes the launch (no device->host read); lengths above it, or
+ * above max_blocks_per_seq * page_size, are truncated to that bound. Page ids are clamped into
+ * [0, num_blocks). num_splits = 0 lets bpt_decode_plan choose the split-K partition count.
+ */
+typedef struct {
+  uint32_t struct_size; /* sizeof(bpt_decode_args): guards against a stale binding */
+  int32_t kv_dtype;     /* bpt_kv_dtype   */
+  int32_t scale_kind;   /* bpt_scale_kind */
+  int32_t q_dtype;      /* bpt_float_dtype */
+  int32_t out_dtype;    /* bpt_float_dtype: BF16 or F32 */
+  int32_t table_dtype;  /* bpt_index_dtype */
+
+  int32_t batch, num_queries, num_q_heads, num_kv_heads, head_dim, page_size;
+  int32_t num_blocks, max_blocks_per_seq, max_context;
+  int32_t num_splits;   /* in: 0 = auto. bpt_decode_plan writes the value used */
+  int32_t split_tokens; /* out of bpt_decode_plan: tokens per split */
+  float sm_scale;
+
+  const void* q;
+  int64_t q_stride_b, q_stride_q, q_stride_h;
+  const void* k_cache;
+  const void* v_cache;
+  int64_t kv_stride_block, kv_stride_token, kv_stride_head;
+  const float* k_scale;
+  const float* v_scale;
+  int64_t scale_stride_block, scale_stride_token, scale_stride_head;
+  const void* block_table;
+  int64_t table_stride_b;
+  const int32_t* context_lens;
+  void* out;
+  int64_t out_stride_b, out_stride_q, out_stride_h;
+  void* workspace;        /* split-K partials; bpt_decode_plan gives the size (0 when one split) */
+  size_t workspace_bytes;
+  void* mid_event;        /* optional hipEvent_t recorded between the split kernel and the combine */
+} bpt_decode_args;
+
+/*
+ * New K/V rows written into the paged pools, quantized on the way (store-before-attend).
+ *
+ *   k, v           [B, Q, Hkv, D] rows (strides new_stride_{b,q,h}), BF16 / F16 / F32
+ *   write_blocks   [B, Q] physical page of each row (negative = skip the row), strides slot_stride_{b,q}
+ *   write_offsets  [B, Q] slot inside that page
+ *   FP8:  code = e4m3fn(clamp(x / scale[h], -448, 448)), scale read from k/v_scale[Hkv]
+ *   INT8: s = max(amax|x| / 127, 1e-12); code = clamp(rint(x / s), -128, 127); s written to the
+ *         per-token-head scale pools at the row's slot
+ *   BF16: the row is stored as is.
+ * Rows whose block is outside [0, num_blocks) or whose offset is outside [0, page_size) are skipped.
+ */
+typedef struct {
+  uint32_t struct_size;
+  int32_t kv_dtype, scale_kind, src_dtype, slot_dtype;
+  int32_t batch, num_queries, num_kv_heads, head_dim, page_size, num_blocks;
+  const void* k;
+  const void* v;
+  int64_t new_stride_b, new_stride_q, new_stride_h;
+  const void* write_blocks;
+  const void* write_offsets;
+  int64_t slot_stride_b, slot_stride_q;
+  void* k_cache;
+  void* v_cache;
+  int64_t kv_stride_block, kv_stride_token, kv_stride_head;
+  float* k_scale; /* FP8: read [Hkv]; INT8: written per token-head */
+  float* v_scale;
+  int64_t scale_stride_block, scale_stride_token, scale_stride_head;
+} bpt_append_args;
+
+/* ---- entry points ------------------------------------------------------------------------------- */
+
+/* Host-only: validate args, choose num_splits/split_tokens, report workspace bytes. Touches no GPU. */
+int bpt_decode_plan(bpt_decode_args* args, size_t* workspace_bytes);
+
+/* Paged decode attention (split kernel, then the log-sum-exp combine when num_splits > 1). */
+int bpt_paged_decode(const bpt_decode_args* args, void* stream);
+
+/* Quantize-on-write of new K/V rows into their (page, slot). */
+int bpt_quant_append(const bpt_append_args* args, void* stream);
+
+/* Thread-local message of the last failing call ("" when none). */
+const char* bpt_last_error(void);
+
+/* BPT_ABI_VERSION of the built library. */
+int bpt_abi_version(void);
+
+/* ---- conversion and measurement primitives (used by the tests and the benchmark) ---------------- */
+
+/* out[i] = float(e4m3fn code i) for i in 0..255, decoded by the same device routine the kernels use. */
+int bpt_fp8_decode_table(float* out256, void* stream);
+
+/* out[i] = e4m3fn(clamp(x[i] / scale, -448, 448)), the FP8 write-path encoder, for n floats. */
+int bpt_fp8_encode(const float* x, float scale, uint8_t* out, int64_t n, void* stream);
+
+/* Streaming read of `bytes` (multiple of 16) from buf; one float per workgroup into partial_sums. The
+ * measured-peak probe, and the cache flush run before cold timings. Returns the workgroup count used
+ * in *num_groups so the caller can size partial_sums (call with partial_sums = NULL to query). */
+int bpt_read_probe(const void* buf, uint64_t bytes, float* partial_sums, int64_t* num_groups,
+                   void* stream);
+
+/* dst <- src, `bytes` a multiple of 16: the known-size kernel that calibrates HBM byte counters. */
+int bpt_copy_probe(void* dst, const void* src, uint64_t bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* BPT_AMD_H */

@@ -1,0 +1,228 @@
+"""GPU: paged decode attention against the oracle, at the tolerance max-abs 2e-3 / rel 1e-2
+(|got - want| <= 2e-3 + 1e-2 * |want| elementwise, want in float32).
+
+Covers what fastserve's kernel tests cover (tests/kernels/test_kernels_gpu.py:78-142): Qwen3 heads, GQA with
+1-8 query heads per KV head, per-row lengths including 0 and 1, lengths that end mid-page and mid-split,
+forced split counts from one split to one chunk per split, and the maximum context; plus what the paged,
+quantized path adds: FP8 / INT8 / BF16 pools, per-head and per-token scales, int32 and int64 block tables,
+head-major pools through strides, several causal queries per sequence, and all five measured shapes at full
+size.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+ATOL, RTOL = 2e-3, 1e-2
+
+
+def check(got: torch.Tensor, want: np.ndarray, what: str = ""):
+    got = got.float().cpu().numpy()
+    assert np.isfinite(got).all(), what
+    err = np.abs(got - want)
+    bound = ATOL + RTOL * np.abs(want)
+    bad = err > bound
+    assert not bad.any(), f"{what}: {bad.sum()} of {bad.size} outside tolerance, worst {err.max():.3e}"
+
+
+def oracle_out(w):
+    from bpt_amd.workloads import to_oracle
+
+    o = to_oracle(w)
+    out, _ = attention.paged_decode(
+        o["q"], o["k_pool"], o["v_pool"], o["block_table"], o["context_lens"], o["k_scale"], o["v_scale"],
+        o["kv_format"], o["scale"],
+    )
+    return out
+
+
+def make_case(fmt, lengths, hq=16, hkv=8, nq=1, page=16, scales="head", seed=0, pool_extra=5, head_major=False,
+              table_dtype=torch.int32, outliers=True):
+    """A small random paged cache in the given format, quantized with torch ops."""
+    from bpt_amd import workloads
+
+    gen = torch.Generator().manual_seed(seed)
+    d = 128
+    n_pages = [max((t + page - 1) // page, 0) for t in lengths]
+    nb = sum(n_pages) + pool_extra
+    perm = torch.randperm(nb, generator=gen)
+    max_blocks = max(max(n_pages), 1) + 2
+    table = torch.zeros((len(lengths), max_blocks), dtype=torch.int64)
+    c = 0
+    for i, n in enumerate(n_pages):
+        table[i, :n] = perm[c : c + n]
+        table[i, n:] = perm[(c + n) % nb]  # padding entries point at real pages
+        c += n
+    g = torch.Generator(device=DEV).manual_seed(seed + 1)
+    kf = torch.randn((nb, page, hkv, d), generator=g, device=DEV)
+    if outliers:
+        kf[..., torch.randperm(d, generator=gen)[:4].to(DEV)] *= 8.0
+    vf = torch.randn((nb, page, hkv, d), generator=g, device=DEV)
+    ks = vs = None
+    if fmt == "bf16":
+        kc, vc = kf.to(torch.bfloat16), vf.to(torch.bfloat16)
+    elif fmt == "fp8" and scales == "head":
+        ks = (kf.abs().amax(dim=(0, 1, 3)) / 448.0).float()
+        vs = (vf.abs().amax(dim=(0, 1, 3)) / 448.0).float()
+        kc, vc = workloads.quantize_per_head_fp8(kf, ks), workloads.quantize_per_head_fp8(vf, vs)
+    elif fmt == "int8" and scales == "token":
+        kc, ks = workloads.quantize_per_token_int8(kf)
+        vc, vs = workloads.quantize_per_token_int8(vf)
+    elif fmt == "int8" and scales == "head":
+        ks = (kf.abs().amax(dim=(0, 1, 3)) / 127.0).float()
+        vs = (vf.abs().amax(dim=(0, 1, 3)) / 127.0).float()
+        kc = torch.clamp(torch.round(kf / ks[:, None]), -128, 127).to(torch.int8)
+        vc = torch.clamp(torch.round(vf / vs[:, None]), -128, 127).to(torch.int8)
+    elif fmt == "fp8" and scales == "token":
+        ks = (kf.abs().amax(-1, keepdim=True) / 448.0).clamp(min=1e-12)
+        vs = (vf.abs().amax(-1, keepdim=True) / 448.0).clamp(min=1e-12)
+        kc = (kf / ks).clamp(-448, 448).to(torch.float8_e4m3fn)
+        vc = (vf / vs).clamp(-448, 448).to(torch.float8_e4m3fn)
+        ks, vs = ks[..., 0].contiguous(), vs[..., 0].contiguous()
+    else:
+        raise ValueError((fmt, scales))
+    if head_major:  # store as [NB, Hkv, P, D], pass the [NB, P, Hkv, D] view
+        kc = kc.transpose(1, 2).contiguous().transpose(1, 2)
+        vc = vc.transpose(1, 2).contiguous().transpose(1, 2)
+    q = torch.randn((len(lengths), nq, hq, d), generator=g, device=DEV).to(torch.bfloat16)
+    lens = torch.tensor(lengths, dtype=torch.int32, device=DEV)
+    return dict(q=q, k=kc, v=vc, table=table.to(DEV, table_dtype), lens=lens, ks=ks, vs=vs, fmt=fmt)
+
+
+def np_codes(t, fmt):
+    if fmt == "fp8":
+        return t.contiguous().view(torch.uint8).cpu().numpy()
+    if fmt == "int8":
+        return t.contiguous().cpu().numpy()
+    return t.float().contiguous().cpu().numpy()
+
+
+def run_case(c, scale=0.0883883, max_context=None, num_splits=None, out_dtype=torch.bfloat16, q=None):
+    from bpt_amd import paged_decode_attention
+
+    q = c["q"] if q is None else q
+    lengths = c["lens"].cpu().tolist()
+    mc = max(lengths + [0]) if max_context is None else max_context
+    got = paged_decode_attention(q, c["k"], c["v"], c["table"], c["lens"], c["ks"], c["vs"], scale=scale,
+                                 max_context=mc, num_splits=num_splits, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    want, _ = attention.paged_decode(
+        q.float().cpu().numpy(), np_codes(c["k"], c["fmt"]), np_codes(c["v"], c["fmt"]), c["table"].cpu().numpy(),
+        np.array(lengths), None if c["ks"] is None else c["ks"].cpu().numpy(),
+        None if c["vs"] is None else c["vs"].cpu().numpy(), c["fmt"], scale,
+    )
+    return got, want
+
+
+@pytest.mark.parametrize("fmt,scales", [("fp8", "head"), ("int8", "token"), ("bf16", None), ("int8", "head"),
+                                        ("fp8", "token")])
+@pytest.mark.parametrize("lengths", [[160, 1, 70, 0], [513, 16, 17, 31, 32, 33, 255, 4096]])
+def test_formats_and_ragged_lengths(fmt, scales, lengths):
+    c = make_case(fmt, lengths, scales=scales)
+    got, want = run_case(c)
+    check(got, want, f"{fmt}/{scales} auto splits")
+    for i, t in enumerate(lengths):
+        if t == 0:  # a sequence with no tokens gets zeros, not NaN
+            assert got[i].float().abs().sum().item() == 0
+
+
+@pytest.mark.parametrize("num_splits", [1, 2, 7, 64, 1000])
+def test_forced_split_counts(num_splits):
+    c = make_case("fp8", [4096, 1000, 33, 1])
+    got, want = run_case(c, num_splits=num_splits)
+    check(got, want, f"num_splits={num_splits}")
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 8), (32, 8), (64, 8), (12, 4), (40, 8)])
+def test_gqa_groups(hq, hkv):
+    c = make_case("fp8", [300, 77, 1024], hq=hq, hkv=hkv)
+    got, want = run_case(c)
+    check(got, want, f"Hq={hq} Hkv={hkv}")
+
+
+@pytest.mark.parametrize("nq", [2, 3, 5])
+@pytest.mark.parametrize("fmt", ["fp8", "bf16"])
+def test_multi_query_causal(nq, fmt):
+    c = make_case(fmt, [1030, 5, 64, 2000], nq=nq)
+    got, want = run_case(c)
+    check(got, want, f"Q={nq}")
+    got1, want1 = run_case(c, num_splits=3)
+    check(got1, want1, f"Q={nq}, 3 splits")
+
+
+@pytest.mark.parametrize("page", [1, 4, 8, 32, 64])
+def test_page_sizes(page):
+    c = make_case("fp8", [100, 257, 31], page=page)
+    got, want = run_case(c)
+    check(got, want, f"page {page}")
+
+
+def test_head_major_pool_int64_table_f32_out_and_q_dtypes():
+    c = make_case("int8", [700, 3, 128], scales="token", head_major=True, table_dtype=torch.int64)
+    got, want = run_case(c)
+    check(got, want, "head-major")
+    got, want = run_case(c, out_dtype=torch.float32)
+    assert got.dtype == torch.float32
+    check(got, want, "f32 out")
+    got, want = run_case(c, q=c["q"].float())
+    check(got, want, "f32 q")
+
+
+def test_lengths_beyond_max_context_are_truncated_to_it():
+    c = make_case("fp8", [600, 300])
+    from bpt_amd import paged_decode_attention
+
+    got = paged_decode_attention(c["q"], c["k"], c["v"], c["table"], c["lens"], c["ks"], c["vs"], scale=0.1,
+                                 max_context=256)
+    c2 = dict(c)
+    c2["lens"] = torch.tensor([256, 256], dtype=torch.int32, device=DEV)
+    want = paged_decode_attention(c["q"], c["k"], c["v"], c["table"], c2["lens"], c["ks"], c["vs"], scale=0.1,
+                                  max_context=256)
+    assert torch.equal(got, want)
+
+
+def test_output_buffer_is_used_and_3d_q_is_one_query():
+    from bpt_amd import paged_decode_attention
+
+    c = make_case("fp8", [64, 65])
+    out = torch.empty((2, 16, 128), dtype=torch.bfloat16, device=DEV)
+    r = paged_decode_attention(c["q"][:, 0], c["k"], c["v"], c["table"], c["lens"], c["ks"], c["vs"], scale=0.1,
+                               max_context=65, out=out)
+    assert r.data_ptr() == out.data_ptr() and r.shape == (2, 16, 128)
+    got, want = run_case(c, scale=0.1)
+    check(out, want[:, 0], "out buffer")
+
+
+def test_max_context_one_sequence():
+    c = make_case("fp8", [32768], pool_extra=0)
+    got, want = run_case(c)
+    check(got, want, "32768 tokens")
+    lens = torch.tensor([32001], dtype=torch.int32, device=DEV)
+    c["lens"] = lens
+    got, want = run_case(c, max_context=32768, num_splits=16)
+    check(got, want, "32001 tokens in 16 splits")
+
+
+@pytest.mark.parametrize("name", ["qwen3-0.6b-bf16", "qwen3-1.7b-fp8", "qwen3-1.7b-int8", "qwen3-8b-fp8-long",
+                                  "qwen3-1.7b-verify"])
+def test_measured_shapes_at_full_size(name):
+    from bpt_amd import paged_decode_attention, workloads
+
+    w = workloads.make(name, device=DEV, seed=0)
+    got = paged_decode_attention(*w.args(), **w.kwargs())
+    torch.cuda.synchronize()
+    check(got, oracle_out(w), name)
+
+
+def test_repeated_calls_are_deterministic():
+    from bpt_amd import paged_decode_attention, workloads
+
+    w = workloads.make("qwen3-1.7b-fp8", device=DEV, seed=1, batch=8)
+    a = paged_decode_attention(*w.args(), **w.kwargs())
+    b = paged_decode_attention(*w.args(), **w.kwargs())
+    assert torch.equal(a, b)
