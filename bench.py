@@ -1,7 +1,7 @@
 #!/usr/bin/env python
 """FP8-KV paged decode attention on one MI355X: KV-read HBM GB/s (% of peak) and µs/call.
 
-One step = one paged decode-attention call (split kernel + split-K combine) over the Qwen3-1.7B-shaped
+One step = one paged decode-attention call (one kernel launch, split-K combined inside) over the Qwen3-1.7B-shaped
 FP8 workload (32 sequences, ragged contexts U[256, 4096], pages scattered over a 2x pool), with inputs
 resident in HBM and the L2 / Infinity Cache evicted by a 1 GiB streaming read before every call (outside
 the timed events). `value` = algorithmic KV bytes read per call / mean event-timed call duration.
@@ -35,29 +35,27 @@ def log(msg: str) -> None:
 
 
 def timed_calls(call, flush, steps: int, warmup: int):
-    """Warmup, then `steps` cold calls: (total ms per call, split-kernel ms per call, wall seconds)."""
+    """Warmup, then `steps` cold calls: (ms per call from HIP events, wall seconds of the timed region).
+
+    Each call is one kernel launch, so the events bracket exactly the decode kernel.
+    """
     import torch
 
     for _ in range(warmup):
-        call(None)
+        call()
     torch.cuda.synchronize()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    mids = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    for e in mids:
-        e.record()  # create the HIP events whose handles the library records between its kernels
     torch.cuda.synchronize()  # barrier: one rank, so the synchronize is the barrier
     t0 = time.perf_counter()
     for i in range(steps):
         flush.run()
         starts[i].record()
-        call(mids[i])
+        call()
         ends[i].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    total = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    split = [s.elapsed_time(m) for s, m in zip(starts, mids)]
-    return total, split, wall
+    return [s.elapsed_time(e) for s, e in zip(starts, ends)], wall
 
 
 def measure_workload(name: str, flush, iters: int, warmup: int) -> dict:
@@ -69,16 +67,15 @@ def measure_workload(name: str, flush, iters: int, warmup: int) -> dict:
     out = torch.empty(tuple(w.q.shape), dtype=torch.bfloat16, device="cuda:0")
     args, kw = w.args(), w.kwargs()
 
-    def call(ev):
-        paged_decode_attention(*args, **kw, out=out, mid_event=ev)
+    def call():
+        paged_decode_attention(*args, **kw, out=out)
 
-    total, split, _ = timed_calls(call, flush, iters, warmup)
-    graph = measure.graph_time_ms(lambda: call(None), calls=10, warmup=2, iters=10)
+    total, _ = timed_calls(call, flush, iters, warmup)
+    graph = measure.graph_time_ms(call, calls=10, warmup=2, iters=10)
     nbytes = w.kv_bytes()
     med = statistics.median(total)
     row = {
         "us_per_call": round(med * 1e3, 2),
-        "split_kernel_us": round(statistics.median(split) * 1e3, 2),
         "graph_warm_us_per_call": round(statistics.median(graph) * 1e3, 2),
         "kv_bytes": nbytes,
         "gbps": round(nbytes / (med * 1e-3) / 1e9, 1),
@@ -104,10 +101,10 @@ def measure_workload(name: str, flush, iters: int, warmup: int) -> dict:
         last = torch.tensor([row_[-1] for row_ in w.extra["tables"]], dtype=torch.int32, device="cuda:0").view(b, 1)
         offs = torch.full((b, 1), 15, dtype=torch.int32, device="cuda:0")
 
-        def write(ev=None):
+        def write():
             quantize_append(k_new, v_new, w.k_cache, w.v_cache, w.k_scale, w.v_scale, last, offs)
 
-        wt, _, _ = timed_calls(write, flush, iters, warmup)
+        wt, _ = timed_calls(write, flush, iters, warmup)
         wg = measure.graph_time_ms(write, calls=20, warmup=2, iters=10)
         row["append_us_per_call"] = round(statistics.median(wt) * 1e3, 2)
         row["append_graph_us_per_call"] = round(statistics.median(wg) * 1e3, 2)
@@ -197,23 +194,21 @@ def main() -> int:
     out = torch.empty(tuple(w.q.shape), dtype=torch.bfloat16, device="cuda:0")
     pargs, kw = w.args(), w.kwargs()
 
-    def call(ev):
-        paged_decode_attention(*pargs, **kw, out=out, mid_event=ev)
+    def call():
+        paged_decode_attention(*pargs, **kw, out=out)
 
     log(f"timing {args.steps} cold steps after {args.warmup} warmup")
-    total, split, wall = timed_calls(call, flush, args.steps, args.warmup)
+    total, wall = timed_calls(call, flush, args.steps, args.warmup)
     nbytes = w.kv_bytes()
     ms_per_step = statistics.fmean(total)
-    split_ms = statistics.fmean(split)
     value = nbytes / (ms_per_step * 1e-3) / 1e9
-    achieved = nbytes / (split_ms * 1e-3) / 1e9
-    log(f"{ms_per_step * 1e3:.1f} us/call ({value:.0f} GB/s), split kernel {split_ms * 1e3:.1f} us")
+    log(f"{ms_per_step * 1e3:.1f} us/call ({value:.0f} GB/s)")
 
     read_gbps = measure.measured_read_gbps(4 << 30)
     log(f"read probe: {read_gbps:.0f} GB/s")
     from bpt_amd import decode_plan
 
-    splits, split_tokens, _ = decode_plan(*pargs, **kw)
+    groups, chunk_tokens, _, _ = decode_plan(*pargs, **kw)
     result = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -239,8 +234,8 @@ def main() -> int:
             "scales": w.shape.scales,
             "sum_context": sum(w.lengths),
             "kv_bytes_per_call": nbytes,
-            "num_splits": splits,
-            "split_tokens": split_tokens,
+            "workgroups": groups,
+            "chunk_tokens": chunk_tokens,
             "timing": f"HIP events around each call, {args.flush_bytes >> 20} MiB read flush before each (untimed)",
         },
         "us_per_call": round(ms_per_step * 1e3, 2),
@@ -251,12 +246,12 @@ def main() -> int:
         "wall_s_timed_region": round(wall, 4),
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode_split_kernel",
-            "achieved": round(achieved, 1),
+            "kernel": "decode_kernel",
+            "achieved": round(value, 1),
             "peak": PEAK_GBPS,
             "unit": "GB/s",
-            "frac": round(achieved / PEAK_GBPS, 4),
-            "kernel_us": round(split_ms * 1e3, 2),
+            "frac": round(value / PEAK_GBPS, 4),
+            "kernel_us": round(ms_per_step * 1e3, 2),
             "traffic": None,
         },
     }

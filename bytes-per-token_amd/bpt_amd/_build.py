@@ -42,8 +42,8 @@ def hipcc() -> str:
     return path
 
 
-def _compile(src: Path, obj: Path) -> None:
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
+def _compile(src: Path, obj: Path, defines: tuple[str, ...] = ()) -> None:
+    cmd = [hipcc(), *HIPCC_FLAGS, *(f"-D{d}" for d in defines), f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{proc.stderr}")
@@ -53,25 +53,31 @@ def _compile(src: Path, obj: Path) -> None:
             print(line)
 
 
-def build(verbose: bool = True) -> Path:
-    """Compile every csrc/*.hip for gfx950 and link libbpt_amd.so. Returns the library path."""
-    BUILD_DIR.mkdir(exist_ok=True)
+def build(verbose: bool = True, defines: tuple[str, ...] = (), out: Path | None = None) -> Path:
+    """Compile every csrc/*.hip for gfx950 and link libbpt_amd.so. Returns the library path.
+
+    `defines` (NAME=VALUE) override the kernels' compile-time tuning constants; `out` writes the library
+    elsewhere (tuning builds), leaving the in-tree one alone.
+    """
+    lib_path = LIB_PATH if out is None else Path(out)
+    build_dir = BUILD_DIR if out is None else lib_path.parent / (lib_path.stem + "_objs")
+    build_dir.mkdir(parents=True, exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
-    objects = [BUILD_DIR / (s.stem + ".o") for s in sources]
+    objects = [build_dir / (s.stem + ".o") for s in sources]
     workers = min(len(sources), int(os.environ.get("MAX_JOBS", "8")), 16)
     with ThreadPoolExecutor(max_workers=max(workers, 1)) as pool:
-        list(pool.map(_compile, sources, objects))
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+        list(pool.map(lambda so: _compile(so[0], so[1], tuple(defines)), zip(sources, objects)))
+    tmp = lib_path.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"linking libbpt_amd.so failed:\n{proc.stderr}")
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, lib_path)
     if verbose:
-        print(f"built {LIB_PATH} from {len(sources)} sources for {ARCH}")
-    return LIB_PATH
+        print(f"built {lib_path} from {len(sources)} sources for {ARCH}" + (f" with {list(defines)}" if defines else ""))
+    return lib_path
 
 
 if __name__ == "__main__":

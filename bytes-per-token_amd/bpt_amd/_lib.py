@@ -44,7 +44,8 @@ class DecodeArgs(ctypes.Structure):
         ("max_blocks_per_seq", _i32),
         ("max_context", _i32),
         ("num_splits", _i32),
-        ("split_tokens", _i32),
+        ("chunk_tokens", _i32),
+        ("grid_groups", _i32),
         ("sm_scale", ctypes.c_float),
         ("q", _vp),
         ("q_stride_b", _i64),
@@ -69,7 +70,8 @@ class DecodeArgs(ctypes.Structure):
         ("out_stride_h", _i64),
         ("workspace", _vp),
         ("workspace_bytes", ctypes.c_size_t),
-        ("mid_event", _vp),
+        ("counters", _vp),
+        ("counters_bytes", ctypes.c_size_t),
     ]
 
 
@@ -110,7 +112,10 @@ class AppendArgs(ctypes.Structure):
 
 # Every symbol include/bpt_amd.h declares, with its ctypes signature.
 SIGNATURES = {
-    "bpt_decode_plan": (_i32, [ctypes.POINTER(DecodeArgs), ctypes.POINTER(ctypes.c_size_t)]),
+    "bpt_decode_plan": (
+        _i32,
+        [ctypes.POINTER(DecodeArgs), ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)],
+    ),
     "bpt_paged_decode": (_i32, [ctypes.POINTER(DecodeArgs), _vp]),
     "bpt_quant_append": (_i32, [ctypes.POINTER(AppendArgs), _vp]),
     "bpt_last_error": (ctypes.c_char_p, []),

@@ -136,15 +136,32 @@ def _decode_args(
 def decode_plan(
     q, k_cache, v_cache, block_table, context_lens, k_scale=None, v_scale=None, *, scale, max_context, num_splits=None
 ) -> tuple[int, int, int]:
-    """(num_splits, split_tokens, workspace_bytes) the call would use. Host only: no GPU needed."""
+    """(workgroups, tokens per wave chunk, workspace bytes) the call would use. Host only: no GPU needed."""
     q4 = q if q.dim() == 4 else q[:, None]
     a, _ = _decode_args(
         q4, k_cache, v_cache, block_table, context_lens, k_scale, v_scale, scale, max_context, num_splits,
         torch.bfloat16,
     )
-    ws = ctypes.c_size_t(0)
-    _lib.check(_lib.lib().bpt_decode_plan(ctypes.byref(a), ctypes.byref(ws)))
-    return a.num_splits, a.split_tokens, ws.value
+    ws, cnt = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    _lib.check(_lib.lib().bpt_decode_plan(ctypes.byref(a), ctypes.byref(ws), ctypes.byref(cnt)))
+    return a.grid_groups, a.chunk_tokens, ws.value, cnt.value
+
+
+# Per (device, stream): one partials workspace and one zero-filled counter buffer. The kernel leaves the
+# counters at zero, so calls issued in order on one stream share them; other streams get their own.
+_BUFFERS: dict[tuple[str, int, int], torch.Tensor] = {}
+_GRAIN = 1 << 20
+
+
+def cached_buffer(kind: str, device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    """The cached zero-initialized uint8 buffer `kind` for (device, stream), grown to at least `nbytes`."""
+    key = (kind, device.index if device.index is not None else torch.cuda.current_device(), stream)
+    buf = _BUFFERS.get(key)
+    if buf is None or buf.numel() < nbytes:
+        size = max((nbytes + _GRAIN - 1) // _GRAIN * _GRAIN, _GRAIN)
+        buf = torch.zeros(size, dtype=torch.uint8, device=device)
+        _BUFFERS[key] = buf
+    return buf
 
 
 def paged_decode_attention(
@@ -161,7 +178,8 @@ def paged_decode_attention(
     num_splits: int | None = None,
     out: torch.Tensor | None = None,
     out_dtype: torch.dtype = torch.bfloat16,
-    mid_event: torch.cuda.Event | None = None,
+    workspace: torch.Tensor | None = None,
+    counters: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """softmax(q kᵀ · scale) v over each sequence's paged cache, dequantized in registers.
 
@@ -170,12 +188,14 @@ def paged_decode_attention(
     block_table   [B, max_blocks] int32 or int64
     context_lens  [B] int32, at most `max_context`
     k/v_scale     FP8 or INT8 only: [Hkv] per head, or [num_blocks, page_size, Hkv] per token and head (fp32)
-    max_context   upper bound on context_lens, known on the host (no device read); sizes the split-K grid
-    num_splits    split-K partitions (None: chosen from the shape)
+    max_context   upper bound on context_lens, known on the host (no device read); sizes the launch
+    num_splits    split-K partitions of a max_context-long sequence (None: balanced over the whole batch)
     out           optional [B, Q, Hq, D] output buffer; returned
-    mid_event     optional event recorded between the split kernel and the combine kernel (timing)
+    workspace     optional device buffer of at least decode_plan(...)[2] bytes for the split-K partials
+    counters      optional device buffer of at least decode_plan(...)[3] bytes, zero-filled before its first
+                  use (every call leaves it zeroed); default for both: cached per (device, stream)
 
-    Returns out [B, Q, Hq, D] (or [B, Hq, D]) in `out_dtype` (bf16 by default).
+    Returns out [B, Q, Hq, D] (or [B, Hq, D]) in `out_dtype` (bf16 by default). One kernel launch.
     """
     squeeze = q.dim() == 3
     q4 = q[:, None] if squeeze else q
@@ -197,16 +217,18 @@ def paged_decode_attention(
     a.out = out4.data_ptr()
     a.out_stride_b, a.out_stride_q, a.out_stride_h = out4.stride(0), out4.stride(1), out4.stride(2)
     lib = _lib.lib()
-    ws_bytes = ctypes.c_size_t(0)
-    _lib.check(lib.bpt_decode_plan(ctypes.byref(a), ctypes.byref(ws_bytes)))
-    workspace = None
-    if ws_bytes.value:
-        workspace = torch.empty((ws_bytes.value + 3) // 4, dtype=torch.float32, device=dev)
-        a.workspace = workspace.data_ptr()
-        a.workspace_bytes = workspace.numel() * 4
-    if mid_event is not None:
-        a.mid_event = mid_event.cuda_event
-    _lib.check(lib.bpt_paged_decode(ctypes.byref(a), ctypes.c_void_p(_stream(dev))))
+    ws_bytes, cnt_bytes = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    _lib.check(lib.bpt_decode_plan(ctypes.byref(a), ctypes.byref(ws_bytes), ctypes.byref(cnt_bytes)))
+    stream = _stream(dev)
+    if workspace is None:
+        workspace = cached_buffer("partials", dev, stream, ws_bytes.value)
+    if counters is None:
+        counters = cached_buffer("counters", dev, stream, cnt_bytes.value)
+    for name, t in (("workspace", workspace), ("counters", counters)):
+        _require(t.device == dev and t.is_contiguous(), f"{name} must be a contiguous tensor on q's device")
+    a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    a.counters, a.counters_bytes = counters.data_ptr(), counters.numel() * counters.element_size()
+    _lib.check(lib.bpt_paged_decode(ctypes.byref(a), ctypes.c_void_p(stream)))
     result = out if out is not None else out4
     return result[:, 0] if (squeeze and result.dim() == 4) else result
 

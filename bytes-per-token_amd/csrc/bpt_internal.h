@@ -4,15 +4,32 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#ifndef BPT_DECODE_LOADS
+#define BPT_DECODE_LOADS 4
+#endif
+#ifndef BPT_DECODE_LOADS_RG4
+#define BPT_DECODE_LOADS_RG4 4
+#endif
+#ifndef BPT_DECODE_GROUPS_PER_CU
+#define BPT_DECODE_GROUPS_PER_CU 2
+#endif
+
 namespace bpt {
 
-// Upper bound on the pages one split stages into LDS (split_tokens / page_size + 1).
-constexpr int kMaxSplitPages = 512;
-// Waves per workgroup of the split kernel, and 16-byte loads per lane per K (and per V) chunk.
+constexpr int kHeadDim = 128;
+// Largest batch the decode kernel takes: its chunk-count prefix sum lives in LDS.
+constexpr int kMaxBatch = 4096;
+// Waves per decode workgroup.
 constexpr int kDecodeWaves = 4;
-constexpr int kDecodeLoads = 4;
+// Compute units of an MI355X; the auto plan launches kDecodeGroupsPerCu workgroups per CU.
+constexpr int kComputeUnits = 256;
+constexpr int kDecodeGroupsPerCu = BPT_DECODE_GROUPS_PER_CU;
 
-// Derived, launch-ready form of bpt_decode_args (strides of the caches in bytes).
+// 16-byte K loads (and V loads) per lane per chunk: fewer for 4-row groups, whose q and accumulators take
+// twice the registers.
+constexpr int decode_loads(int rows_per_group) { return rows_per_group >= 4 ? BPT_DECODE_LOADS_RG4 : BPT_DECODE_LOADS; }
+
+// Launch-ready form of bpt_decode_args (cache strides in bytes).
 struct DecodeParams {
   const void* q;
   int64_t q_sb, q_sq, q_sh;
@@ -27,10 +44,14 @@ struct DecodeParams {
   const int32_t* lens;
   void* out;
   int64_t o_sb, o_sq, o_sh;
-  float* part_out;  // [B, Q, Hq, S, D]
-  float* part_lse;  // [B, Q, Hq, S], log2 units
-  int B, Q, Hq, Hkv, G, P, logP, num_blocks, max_blocks, S, split_tokens, n_rg, len_cap;
-  float qscale;  // sm_scale * log2(e)
+  float* ws_out;       // [slots, RG, D] normalized partial outputs
+  float* ws_lse;       // [slots, RG] log2-sum-exp of each partial
+  unsigned* counters;  // [B * HR] arrivals per segment; zero between calls
+  int B, Q, Hq, Hkv, G, P, logP, num_blocks, max_blocks, len_cap;
+  int n_rg, HR;      // row groups per KV head; segments per sequence (Hkv * n_rg)
+  int grid;          // workgroups launched
+  int64_t per_forced;  // chunks per workgroup when the caller fixed the split count, else 0
+  float qscale;      // sm_scale * log2(e)
   int q_dtype, out_dtype, table_i64;
 };
 
@@ -51,15 +72,9 @@ struct AppendParams {
   int src_dtype, slot_i64;
 };
 
-// Chunk of tokens one wave consumes per loop iteration for a KV element type (fp8/int8: 1 byte).
-inline int decode_chunk_tokens(int kv_dtype, int head_dim) {
-  int vec = kv_dtype == 0 ? 8 : 16;  // elements per 16-byte load
-  int lanes_per_token = head_dim / vec;
-  return kDecodeLoads * (64 / lanes_per_token);
-}
-
-hipError_t launch_decode(const DecodeParams& p, int kv_dtype, int scale_kind, int head_dim, int rows_per_group,
-                         hipStream_t stream, hipEvent_t mid_event);
+int decode_rows_per_load(int kv_dtype);
+int decode_chunk_tokens(int kv_dtype, int rows_per_group);
+hipError_t launch_decode(const DecodeParams& p, int kv_dtype, int scale_kind, int rows_per_group, hipStream_t stream);
 hipError_t launch_append(const AppendParams& p, int kv_dtype, int scale_kind, int head_dim, hipStream_t stream);
 hipError_t launch_fp8_table(float* out, hipStream_t stream);
 hipError_t launch_fp8_encode(const float* x, float scale, uint8_t* out, int64_t n, hipStream_t stream);

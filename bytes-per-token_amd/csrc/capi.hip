@@ -37,14 +37,18 @@ int log2i(int64_t x) {
 }
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 int float_bytes(int dt) { return dt == BPT_F_F32 ? 4 : 2; }
-
-// Workgroups the auto plan aims for: enough to keep every CU of a 256-CU MI355X streaming several splits.
-constexpr int64_t kTargetGroups = 2048;
+bool aligned_to(const void* p, int64_t stride_b, int64_t stride_q, int64_t stride_h, int elem) {
+  return ((uintptr_t)p % 16 == 0) && (stride_b * elem) % 16 == 0 && (stride_q * elem) % 16 == 0 &&
+         (stride_h * elem) % 16 == 0;
+}
 
 struct Plan {
-  int rows, rows_per_group, n_rg, chunk, split_tokens, num_splits, len_cap;
-  size_t workspace;
+  int rows, rows_per_group, n_rg, HR, chunk, grid, len_cap;
+  int64_t per_forced;
+  size_t ws_out_floats, ws_lse_floats, workspace, counters;
 };
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 int make_plan(const bpt_decode_args* a, Plan* pl) {
   const char* fn = "bpt_decode_plan";
@@ -64,54 +68,51 @@ int make_plan(const bpt_decode_args* a, Plan* pl) {
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: block table must be int32 or int64", fn);
   if (a->batch < 0 || a->num_queries < 1 || a->num_q_heads < 1 || a->num_kv_heads < 1)
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: batch >= 0, num_queries, num_q_heads, num_kv_heads >= 1", fn);
+  if (a->batch > bpt::kMaxBatch)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: batch %d exceeds %d", fn, a->batch, bpt::kMaxBatch);
   if (a->num_q_heads % a->num_kv_heads)
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: %d query heads are not a multiple of %d KV heads", fn,
                 a->num_q_heads, a->num_kv_heads);
-  if (a->head_dim != 128) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: head_dim %d not supported (128)", fn, a->head_dim);
+  if (a->head_dim != bpt::kHeadDim)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: head_dim %d not supported (128)", fn, a->head_dim);
   if (!is_pow2(a->page_size) || a->page_size > 1024)
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: page_size %d must be a power of two <= 1024", fn, a->page_size);
   if (a->num_blocks < 1 || a->max_blocks_per_seq < 1 || a->max_context < 0)
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: num_blocks, max_blocks_per_seq >= 1 and max_context >= 0", fn);
   if (a->num_splits < 0) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: num_splits must be >= 0", fn);
   if (!std::isfinite(a->sm_scale)) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: sm_scale must be finite", fn);
-  if (a->batch > 65535) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: batch %d exceeds 65535", fn, a->batch);
 
   const int G = a->num_q_heads / a->num_kv_heads;
   pl->rows = a->num_queries * G;
   pl->rows_per_group = pl->rows <= 1 ? 1 : (pl->rows <= 2 ? 2 : 4);
   pl->n_rg = (pl->rows + pl->rows_per_group - 1) / pl->rows_per_group;
-  if ((int64_t)a->num_kv_heads * pl->n_rg > 65535)
-    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: too many KV heads x row groups", fn);
-  pl->chunk = bpt::decode_chunk_tokens(a->kv_dtype, a->head_dim);
-
-  // Splits never straddle a chunk, and a split's pages must fit the LDS page table.
-  const int64_t max_split = ((int64_t)(bpt::kMaxSplitPages - 1) * a->page_size / pl->chunk) * pl->chunk;
-  const int64_t ctx = a->max_context > 0 ? a->max_context : 1;
-  int64_t split;
-  if (a->num_splits > 0) {
-    split = (ctx + a->num_splits - 1) / a->num_splits;
-    split = (split + pl->chunk - 1) / pl->chunk * pl->chunk;
-  } else {
-    const int64_t units = (int64_t)a->batch * a->num_kv_heads * pl->n_rg;
-    int64_t ideal = units * ctx / kTargetGroups;
-    const int64_t floor_tokens = (int64_t)pl->chunk * bpt::kDecodeWaves;
-    if (ideal < floor_tokens) ideal = floor_tokens;
-    split = 1;
-    while (split * 2 <= ideal) split *= 2;
-    if (split < pl->chunk) split = pl->chunk;
-  }
-  if (split > max_split) split = max_split;
-  if (split < pl->chunk) split = pl->chunk;
-  pl->split_tokens = (int)split;
-  pl->num_splits = (int)((ctx + split - 1) / split);
+  const int64_t hr = (int64_t)a->num_kv_heads * pl->n_rg;
+  if (hr > (1 << 20)) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: too many KV heads x row groups", fn);
+  pl->HR = (int)hr;
+  pl->chunk = bpt::decode_chunk_tokens(a->kv_dtype, pl->rows_per_group);
   const int64_t table_cap = (int64_t)a->max_blocks_per_seq * a->page_size;
   pl->len_cap = (int)(a->max_context < table_cap ? a->max_context : table_cap);
-  if (pl->num_splits > 1) {
-    const size_t rows_total = (size_t)a->batch * a->num_queries * a->num_q_heads * pl->num_splits;
-    pl->workspace = rows_total * (size_t)(a->head_dim + 1) * sizeof(float);
+  const int64_t max_nb = (pl->len_cap + pl->chunk - 1) / pl->chunk;
+  const int64_t seq_chunks = (int64_t)a->batch * max_nb;  // bound on the chunk prefix sum
+  if (seq_chunks > 0x7fffffffLL / (hr > 0 ? hr : 1))
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: batch x context x heads too large", fn);
+  const int64_t bound_c = seq_chunks * hr;
+  if (a->num_splits > 0) {
+    int64_t per = (max_nb + a->num_splits - 1) / a->num_splits;
+    pl->per_forced = per < 1 ? 1 : per;
+    int64_t grid = (bound_c + pl->per_forced - 1) / pl->per_forced;
+    pl->grid = (int)(grid < 1 ? 1 : grid);
   } else {
-    pl->workspace = 0;
+    pl->per_forced = 0;
+    int64_t grid = (int64_t)bpt::kComputeUnits * bpt::kDecodeGroupsPerCu;
+    if (bound_c < grid) grid = bound_c;
+    pl->grid = (int)(grid < 1 ? 1 : grid);
   }
+  const size_t slots = (size_t)a->batch * pl->HR + pl->grid;
+  pl->ws_out_floats = slots * pl->rows_per_group * a->head_dim;
+  pl->ws_lse_floats = slots * pl->rows_per_group;
+  pl->workspace = align256((pl->ws_out_floats + pl->ws_lse_floats) * sizeof(float));
+  pl->counters = align256((size_t)a->batch * pl->HR * sizeof(unsigned));
   return BPT_OK;
 }
 
@@ -123,13 +124,14 @@ const char* bpt_last_error(void) { return g_error.c_str(); }
 
 int bpt_abi_version(void) { return BPT_ABI_VERSION; }
 
-int bpt_decode_plan(bpt_decode_args* args, size_t* workspace_bytes) {
+int bpt_decode_plan(bpt_decode_args* args, size_t* workspace_bytes, size_t* counters_bytes) {
   Plan pl;
   int rc = make_plan(args, &pl);
   if (rc) return rc;
-  args->num_splits = pl.num_splits;
-  args->split_tokens = pl.split_tokens;
+  args->chunk_tokens = pl.chunk;
+  args->grid_groups = pl.grid;
   if (workspace_bytes) *workspace_bytes = pl.workspace;
+  if (counters_bytes) *counters_bytes = pl.counters;
   return BPT_OK;
 }
 
@@ -147,9 +149,14 @@ int bpt_paged_decode(const bpt_decode_args* a, void* stream) {
   if (!aligned16(a->k_cache) || !aligned16(a->v_cache) || (a->kv_stride_block * eb) % 16 ||
       (a->kv_stride_token * eb) % 16 || (a->kv_stride_head * eb) % 16)
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: cache pointers and strides must be 16-byte aligned", fn);
-  if (pl.num_splits > 1 && (!a->workspace || a->workspace_bytes < pl.workspace || ((uintptr_t)a->workspace & 3u)))
-    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: workspace of %zu bytes required for %d splits (got %zu)", fn,
-                pl.workspace, pl.num_splits, a->workspace_bytes);
+  if (!a->workspace || a->workspace_bytes < pl.workspace || ((uintptr_t)a->workspace & 255u))
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: a 256-byte aligned workspace of %zu bytes is required (got %zu)", fn,
+                pl.workspace, a->workspace_bytes);
+  if (!a->counters || a->counters_bytes < pl.counters || ((uintptr_t)a->counters & 3u))
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: a zeroed counter buffer of %zu bytes is required (got %zu)", fn,
+                pl.counters, a->counters_bytes);
+  if (!aligned_to(a->q, a->q_stride_b, a->q_stride_q, a->q_stride_h, float_bytes(a->q_dtype)))
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: q rows must be 16-byte aligned (pointer and strides)", fn);
 
   bpt::DecodeParams p;
   p.q = a->q;
@@ -173,9 +180,9 @@ int bpt_paged_decode(const bpt_decode_args* a, void* stream) {
   p.o_sb = a->out_stride_b;
   p.o_sq = a->out_stride_q;
   p.o_sh = a->out_stride_h;
-  p.part_out = (float*)a->workspace;
-  const size_t rows_total = (size_t)a->batch * a->num_queries * a->num_q_heads * pl.num_splits;
-  p.part_lse = pl.num_splits > 1 ? (float*)a->workspace + rows_total * a->head_dim : nullptr;
+  p.ws_out = (float*)a->workspace;
+  p.ws_lse = (float*)a->workspace + pl.ws_out_floats;
+  p.counters = (unsigned*)a->counters;
   p.B = a->batch;
   p.Q = a->num_queries;
   p.Hq = a->num_q_heads;
@@ -185,16 +192,16 @@ int bpt_paged_decode(const bpt_decode_args* a, void* stream) {
   p.logP = log2i(a->page_size);
   p.num_blocks = a->num_blocks;
   p.max_blocks = a->max_blocks_per_seq;
-  p.S = pl.num_splits;
-  p.split_tokens = pl.split_tokens;
   p.n_rg = pl.n_rg;
+  p.HR = pl.HR;
+  p.grid = pl.grid;
+  p.per_forced = pl.per_forced;
   p.len_cap = pl.len_cap;
   p.qscale = a->sm_scale * bpt::kLog2e;
   p.q_dtype = a->q_dtype;
   p.out_dtype = a->out_dtype;
   p.table_i64 = a->table_dtype == BPT_IDX_I64;
-  hipError_t e = bpt::launch_decode(p, a->kv_dtype, a->scale_kind, a->head_dim, pl.rows_per_group,
-                                    (hipStream_t)stream, (hipEvent_t)a->mid_event);
+  hipError_t e = bpt::launch_decode(p, a->kv_dtype, a->scale_kind, pl.rows_per_group, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(fn, e);
   return BPT_OK;
 }

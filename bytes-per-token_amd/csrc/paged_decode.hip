@@ -1,20 +1,28 @@
-// Paged decode attention over a BF16, FP8 (e4m3fn) or INT8 KV cache, dequantized in registers.
+// Paged decode attention over a BF16, FP8 (e4m3fn) or INT8 KV cache, dequantized in registers: one launch.
 //
-// Algorithm (follows fastserve kernels/kv_attention.py:56-175 and kernels/reference.py:186-211): one
-// workgroup per (sequence, KV head, row group, split). Its rows are the G query heads of the KV head times
-// the Q queries of the sequence, so each cached page is read from HBM once for all of them. Each split
-// writes its own normalized output and log-sum-exp; a second kernel combines the splits exactly.
+// Algorithm (follows fastserve kernels/kv_attention.py:56-175, kernels/reference.py:186-211): the rows of a
+// KV head are its G query heads times the sequence's Q queries, so each cached page is read from HBM once
+// for all of them. Keys and values stream through in chunks; every lane keeps an online softmax (running
+// max m, weight sum l, weighted value sum acc) over the tokens it saw, and states are merged exactly with
+// the log-sum-exp algebra of reference.merge_partials.
 //
-// Layout inside a wave (D = 128, one-byte codes): lane = slot * 8 + part. `part` owns channels
-// [16*part, 16*part + 16) and loads them with one 16-byte load per token; the 8 lanes of a slot cover one
-// token row (128 contiguous bytes), so one load instruction moves 8 whole token rows. Scores are summed
-// over the 8 lanes of a slot with DPP (quad_perm, row_half_mirror). Every slot keeps its own online-softmax
-// state (running max m, weight sum l, weighted value sum acc) over the tokens it saw; slots, then waves
-// (through LDS), are merged at the end with the same log-sum-exp algebra as the split combine.
+// Work decomposition (stream-K): a segment is one (sequence, KV head, row group) and owns ceil(len / CHUNK)
+// chunks; segments are laid end to end (sequence-major) and the launched workgroups split that line into
+// equal contiguous ranges, so ragged batches and long contexts balance to within one chunk. Each
+// workgroup computes the chunk counts' prefix sum itself (lengths stay on the device), walks its range
+// segment by segment ("pieces"), and its waves take the piece's chunks round-robin with the next chunk's
+// 16-byte loads in flight while the current one is computed. A segment covered by one workgroup is written
+// directly; otherwise every workgroup writes its piece's normalized output and log2-sum-exp to a
+// workspace slot, bumps the segment's arrival counter, and the last arriver combines all pieces and
+// resets the counter to zero (no waiting on other workgroups anywhere).
+//
+// Wave layout (D = 128, one-byte codes): lane = slot * 8 + part. `part` owns channels [16 part, 16 part + 16)
+// and loads them with one 16-byte load per token row; one load instruction covers 8 token rows. Scores are
+// summed over the 8 lanes of a slot with DPP. BF16 pools use 16 lanes per row (8 channels each).
 //
 // Scales fold out of the inner loop: a per-head K scale and sm_scale * log2(e) go into q once, a per-head V
-// scale multiplies the final output, and per-token scales multiply the reduced score (K) and the softmax
-// weight (V). Softmax runs in base 2 (exp2 of log2-scaled scores); lse is stored in log2 units.
+// scale multiplies the final output, per-token scales multiply the reduced score (K) and the softmax weight
+// (V). Softmax runs in base 2; the workspace lse is in log2 units.
 #include "bpt_device.h"
 #include "bpt_internal.h"
 
@@ -23,7 +31,9 @@ namespace bpt {
 template <int KV>
 struct KvTraits {
   static constexpr int kBytes = KV == kKvBf16 ? 2 : 1;
-  static constexpr int kVec = 16 / kBytes;  // elements in one 16-byte load
+  static constexpr int kVec = 16 / kBytes;          // elements in one 16-byte load
+  static constexpr int kLanesPerRow = kHeadDim / kVec;
+  static constexpr int kRowsPerLoad = 64 / kLanesPerRow;
 };
 
 // 16 bytes of cache -> kVec floats (codes, not yet scaled).
@@ -48,321 +58,572 @@ __device__ __forceinline__ void unpack16(const U4& r, float* f) {
   }
 }
 
-template <int KV, int SK, int D, int RG, int NW, int CL>
-__global__ __launch_bounds__(NW * 64) void decode_split_kernel(const DecodeParams p) {
-  constexpr int VEC = KvTraits<KV>::kVec;
-  constexpr int EB = KvTraits<KV>::kBytes;
-  constexpr int LPT = D / VEC;  // lanes per token row
-  constexpr int TPL = 64 / LPT; // token rows per load instruction
-  constexpr int CHUNK = CL * TPL;
-  static_assert(D % VEC == 0 && 64 % LPT == 0, "head_dim must split into 16-byte lanes");
+// One chunk of one lane's K and V rows (and per-token scales), and the physical page of each of its loads.
+template <int CL>
+struct ChunkRegs {
+  U4 k[CL];
+  U4 v[CL];
+  float ks[CL];
+  float vs[CL];
+};
 
-  __shared__ int s_pages[kMaxSplitPages];
+template <int CL>
+struct ChunkPages {
+  int e[CL];
+};
+
+__device__ __forceinline__ int sread(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// Cross-workgroup exchange of split-K partials. Workgroups run on different XCDs, whose L2 caches are
+// not coherent with each other. BPT_WS_COHERENT (default): partials are stored and loaded as
+// device-scope relaxed atomics, which gfx950 performs coherently (sc1) without whole-cache maintenance,
+// and publishing only waits for this wave's stores to complete. Otherwise: plain accesses bracketed by
+// device-scope fences (an L2 writeback on the writer, an L2 invalidate on the reader).
+#ifndef BPT_WS_COHERENT
+#define BPT_WS_COHERENT 1
+#endif
+
+__device__ __forceinline__ void ws_store(float* ptr, float v) {
+#if BPT_WS_COHERENT
+  __hip_atomic_store(ptr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#else
+  *ptr = v;
+#endif
+}
+
+__device__ __forceinline__ float ws_load(const float* ptr) {
+#if BPT_WS_COHERENT
+  return __hip_atomic_load(ptr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#else
+  return *ptr;
+#endif
+}
+
+__device__ __forceinline__ void ws_publish() {
+#if BPT_WS_COHERENT
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#else
+  __threadfence();
+#endif
+}
+
+__device__ __forceinline__ void ws_acquire() {
+#if BPT_WS_COHERENT
+  __asm__ volatile("" ::: "memory");
+#else
+  __threadfence();
+#endif
+}
+
+// A load the whole wave makes from one address, through the scalar cache (the data is read-only here).
+template <typename T>
+__device__ __forceinline__ T load_uniform(const T* ptr) {
+  return *(const __attribute__((address_space(4))) T*)ptr;
+}
+
+// Block-table entry `idx` of row `row`: int32 tables directly, int64 tables by their low word (page ids
+// are below 2^31; anything else is clamped into the pool by the caller).
+__device__ __forceinline__ int64_t table_word(const DecodeParams& p, int b, int idx) {
+  return ((int64_t)b * p.table_sb + idx) << p.table_i64;
+}
+
+// Physical pages of chunk kk's loads. PU: a page holds whole load rows (page_size >= rows per load), so each
+// load's page is wave-uniform and read with a scalar load; otherwise every lane reads its own row's page.
+template <int KV, int CL, bool PU>
+__device__ __forceinline__ void fetch_pages(const DecodeParams& p, int b, int kk, int len, int slot, ChunkPages<CL>& g) {
+  constexpr int RPL = KvTraits<KV>::kRowsPerLoad;
+  const int tb = kk * CL * RPL;
+  const int32_t* table = (const int32_t*)p.table;
+#pragma unroll
+  for (int i = 0; i < CL; ++i) {
+    int e;
+    if constexpr (PU) {
+      const int t0 = tb + i * RPL;  // wave-uniform
+      e = t0 < len ? load_uniform(table + table_word(p, b, t0 >> p.logP)) : 0;
+    } else {
+      const int t = tb + i * RPL + slot;
+      e = t < len ? table[table_word(p, b, t >> p.logP)] : 0;
+    }
+    g.e[i] = e < 0 ? 0 : (e >= p.num_blocks ? p.num_blocks - 1 : e);
+  }
+}
+
+// Issue chunk kk's 16-byte K and V loads (and per-token scales) into c.
+template <int KV, int SK, int CL>
+__device__ __forceinline__ void issue_chunk(const DecodeParams& p, const ChunkPages<CL>& g, int h, int kk, int len,
+                                            int slot, int64_t lane_off, ChunkRegs<CL>& c) {
+  constexpr int RPL = KvTraits<KV>::kRowsPerLoad;
+  const int tb = kk * CL * RPL;
+#pragma unroll
+  for (int i = 0; i < CL; ++i) {
+    const int t = tb + i * RPL + slot;
+    c.ks[i] = 1.0f;
+    c.vs[i] = 1.0f;
+    if (t < len) {
+      const int within = t & (p.P - 1);
+      const int64_t off = (int64_t)g.e[i] * p.kv_sblk + (int64_t)within * p.kv_stok + lane_off;
+      c.k[i] = load16(p.k + off);
+      c.v[i] = load16(p.v + off);
+      if constexpr (SK == kScaleTokenHead) {
+        const int64_t so = (int64_t)g.e[i] * p.sc_sblk + (int64_t)within * p.sc_stok + (int64_t)h * p.sc_shead;
+        c.ks[i] = p.ks[so];
+        c.vs[i] = p.vs[so];
+      }
+    } else {
+      c.k[i] = U4{0, 0, 0, 0};
+      c.v[i] = U4{0, 0, 0, 0};
+    }
+  }
+}
+
+// This lane's VEC query channels of row (b, qi, hq), loaded as 16-byte vectors, times cs.
+template <int VEC>
+__device__ __forceinline__ void load_q(const DecodeParams& p, int64_t base, float cs, float* q) {
+  const uint8_t* src = (const uint8_t*)p.q;
+  if (p.q_dtype == kFF32) {
+    const U4* v = (const U4*)(src + base * 4);
+    U4 raw[VEC / 4];
+#pragma unroll
+    for (int j = 0; j < VEC / 4; ++j) raw[j] = v[j];
+#pragma unroll
+    for (int j = 0; j < VEC / 4; ++j) {
+      q[4 * j] = __uint_as_float(raw[j].x) * cs;
+      q[4 * j + 1] = __uint_as_float(raw[j].y) * cs;
+      q[4 * j + 2] = __uint_as_float(raw[j].z) * cs;
+      q[4 * j + 3] = __uint_as_float(raw[j].w) * cs;
+    }
+  } else {
+    const U4* v = (const U4*)(src + base * 2);
+    U4 raw[VEC / 8];
+#pragma unroll
+    for (int j = 0; j < VEC / 8; ++j) raw[j] = v[j];
+#pragma unroll
+    for (int j = 0; j < VEC / 8; ++j) {
+      const uint32_t w[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float lo, hi;
+        if (p.q_dtype == kFBf16) {
+          lo = __uint_as_float(w[e] << 16);
+          hi = __uint_as_float(w[e] & 0xffff0000u);
+        } else {
+          lo = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[e] & 0xffffu));
+          hi = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[e] >> 16));
+        }
+        q[8 * j + 2 * e] = lo * cs;
+        q[8 * j + 2 * e + 1] = hi * cs;
+      }
+    }
+  }
+}
+
+// Fold chunk kk into this lane's online-softmax state.
+template <int KV, int SK, int RG, int CL>
+__device__ __forceinline__ void compute_chunk(const ChunkRegs<CL>& c, int kk, int slot,
+                                              const float (&q)[RG][KvTraits<KV>::kVec], const int (&rlen)[RG],
+                                              float (&m)[RG], float (&l)[RG], float (&acc)[RG][KvTraits<KV>::kVec]) {
+  constexpr int VEC = KvTraits<KV>::kVec;
+  constexpr int LPR = KvTraits<KV>::kLanesPerRow;
+  constexpr int RPL = KvTraits<KV>::kRowsPerLoad;
+  constexpr int CH = CL * RPL;
+  const int tb = kk * CH + slot;
+
+  float s[CL][RG];
+#pragma unroll
+  for (int i = 0; i < CL; ++i) {
+    float kf[VEC];
+    unpack16<KV>(c.k[i], kf);
+#pragma unroll
+    for (int r = 0; r < RG; ++r) {
+      float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+      for (int v = 0; v < VEC; v += 2) {
+        a0 = fmaf(q[r][v], kf[v], a0);
+        a1 = fmaf(q[r][v + 1], kf[v + 1], a1);
+      }
+      s[i][r] = a0 + a1;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < CL; ++i) {
+    const int t = tb + i * RPL;
+#pragma unroll
+    for (int r = 0; r < RG; ++r) {
+      float x = group_sum<LPR>(s[i][r]);
+      if constexpr (SK == kScaleTokenHead) x *= c.ks[i];
+      s[i][r] = t < rlen[r] ? x : kNegInf;
+    }
+  }
+  float pw[CL][RG];
+#pragma unroll
+  for (int r = 0; r < RG; ++r) {
+    float mc = s[0][r];
+#pragma unroll
+    for (int i = 1; i < CL; ++i) mc = fmaxf(mc, s[i][r]);
+    const float mn = fmaxf(m[r], mc);
+    const float mu = mn == kNegInf ? 0.0f : mn;
+    const float alpha = fast_exp2(m[r] - mu);
+    m[r] = mn;
+    float lsum = l[r] * alpha;
+#pragma unroll
+    for (int i = 0; i < CL; ++i) {
+      const float e = fast_exp2(s[i][r] - mu);
+      lsum += e;
+      pw[i][r] = e * c.vs[i];
+    }
+    l[r] = lsum;
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) acc[r][v] *= alpha;
+  }
+#pragma unroll
+  for (int i = 0; i < CL; ++i) {
+    float vf[VEC];
+    unpack16<KV>(c.v[i], vf);
+#pragma unroll
+    for (int r = 0; r < RG; ++r) {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) acc[r][v] = fmaf(pw[i][r], vf[v], acc[r][v]);
+    }
+  }
+}
+
+template <int KV, int SK, int RG, bool PU>
+__global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeParams p) {
+  constexpr int NW = kDecodeWaves;
+  constexpr int NT = NW * 64;
+  constexpr int D = kHeadDim;
+  constexpr int VEC = KvTraits<KV>::kVec;
+  constexpr int LPR = KvTraits<KV>::kLanesPerRow;
+  constexpr int CL = decode_loads(RG);
+  constexpr int CH = CL * KvTraits<KV>::kRowsPerLoad;
+
+  __shared__ int s_prefix[kMaxBatch + 1];
+  __shared__ int s_wsum[NW];
+  __shared__ int s_last;
   __shared__ float s_m[NW][RG];
   __shared__ float s_l[NW][RG];
   __shared__ float s_acc[NW][RG][D];
 
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int split = blockIdx.x;
-  const int h = blockIdx.y / p.n_rg;
-  const int rg = blockIdx.y - h * p.n_rg;
-  const int b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = sread(tid >> 6);
+  const int B = p.B;
 
-  int len = p.lens[b];
-  len = len < 0 ? 0 : (len > p.len_cap ? p.len_cap : len);
-  const int t0 = split * p.split_tokens;
-  if (p.S > 1 && t0 >= len) return;  // nothing to write: the combine reads splits below len only
-  const int t_end = min(t0 + p.split_tokens, len);
-
-  // Stage the split's page ids in LDS, clamped into the pool.
-  const int p0 = t0 >> p.logP;
-  const int np = t_end > t0 ? ((t_end - 1) >> p.logP) - p0 + 1 : 0;
-  for (int i = threadIdx.x; i < np; i += NW * 64) {
-    int64_t e = load_index(p.table, (int64_t)b * p.table_sb + p0 + i, p.table_i64 != 0);
-    e = e < 0 ? 0 : (e >= p.num_blocks ? p.num_blocks - 1 : e);
-    s_pages[i] = (int)e;
+  // ---- chunks per sequence and their exclusive prefix sum (the segment line), in LDS ----------------
+  {
+    const int per_thread = (B + NT - 1) / NT;
+    const int lo = min(tid * per_thread, B);
+    const int hi = min(lo + per_thread, B);
+    int sum = 0;
+    for (int b = lo; b < hi; ++b) {
+      int len = p.lens[b];
+      len = len < 0 ? 0 : (len > p.len_cap ? p.len_cap : len);
+      sum += (len + CH - 1) / CH;
+    }
+    int x = sum;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(x, off, 64);
+      if (lane >= off) x += y;
+    }
+    if (lane == 63) s_wsum[tid >> 6] = x;
+    __syncthreads();
+    int run = 0;
+    for (int w = 0; w < (tid >> 6); ++w) run += s_wsum[w];
+    run += x - sum;
+    for (int b = lo; b < hi; ++b) {
+      s_prefix[b] = run;
+      int len = p.lens[b];
+      len = len < 0 ? 0 : (len > p.len_cap ? p.len_cap : len);
+      run += (len + CH - 1) / CH;
+    }
+    if (tid == 0) {
+      int total = 0;
+      for (int w = 0; w < NW; ++w) total += s_wsum[w];
+      s_prefix[B] = total;
+    }
+    __syncthreads();
   }
 
-  const int slot = lane / LPT;
-  const int part = lane - slot * LPT;
+  // ---- sequences with no tokens get zero output ---------------------------------------------------
+  {
+    const int row_elems = p.Q * p.Hq * D;
+    for (int b = blockIdx.x; b < B; b += gridDim.x) {
+      if (s_prefix[b + 1] != s_prefix[b]) continue;
+      for (int i = tid; i < row_elems; i += NT) {
+        const int ch = i % D;
+        const int hq = (i / D) % p.Hq;
+        const int qi = i / (D * p.Hq);
+        store_float(p.out, (int64_t)b * p.o_sb + (int64_t)qi * p.o_sq + (int64_t)hq * p.o_sh + ch, p.out_dtype,
+                    0.0f);
+      }
+    }
+  }
+
+  // ---- this workgroup's range of chunks -----------------------------------------------------------
+  const int HR = p.HR;
+  const int64_t C = (int64_t)HR * s_prefix[B];
+  if (C == 0) return;
+  const int64_t per = p.per_forced > 0 ? p.per_forced : (C + gridDim.x - 1) / gridDim.x;
+  const int64_t g = blockIdx.x;
+  int64_t c = g * per;
+  if (c >= C) return;
+  const int64_t c_end = min(c + per, C);
+
+  int b;
+  {
+    int lo = 0, hi = B - 1;  // largest b with HR * prefix[b] <= c
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if ((int64_t)HR * s_prefix[mid] <= c) lo = mid; else hi = mid - 1;
+    }
+    b = sread(lo);
+  }
+  int nb = sread(s_prefix[b + 1] - s_prefix[b]);
+  int hr, k;
+  {
+    const int64_t r = c - (int64_t)HR * s_prefix[b];
+    hr = sread((int)(r / nb));
+    k = sread((int)(r - (int64_t)hr * nb));
+  }
+
+  const int slot = lane / LPR;
+  const int part = lane - slot * LPR;
   const int rows = p.Q * p.G;
 
-  // This lane's slice of each row's query, pre-scaled.
-  float q[RG][VEC];
-  int rlen[RG];
-  float kscale_head = 1.0f;
-  if constexpr (SK == kScaleHead) kscale_head = p.ks[h];
-#pragma unroll
-  for (int r = 0; r < RG; ++r) {
-    const int gr = rg * RG + r;
-    if (gr < rows) {
-      const int qi = gr / p.G;
-      const int hq = h * p.G + (gr - qi * p.G);
-      const int64_t base = (int64_t)b * p.q_sb + (int64_t)qi * p.q_sq + (int64_t)hq * p.q_sh + part * VEC;
-      const float c = p.qscale * kscale_head;
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) q[r][v] = load_float(p.q, base + v, p.q_dtype) * c;
-      rlen[r] = len - (p.Q - 1 - qi);
-    } else {
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) q[r][v] = 0.0f;
-      rlen[r] = 0;
-    }
-  }
+  for (;;) {
+    const int64_t seg_c0 = (int64_t)HR * s_prefix[b] + (int64_t)hr * nb;
+    const int64_t pe = min(c_end, seg_c0 + nb);
+    const int k_end = k + (int)(pe - c);
+    const int h = hr / p.n_rg;
+    const int rg = hr - h * p.n_rg;
+    int len = load_uniform(p.lens + b);
+    len = len < 0 ? 0 : (len > p.len_cap ? p.len_cap : len);
 
-  float m[RG], l[RG], acc[RG][VEC];
+    // This lane's slice of each row's query, pre-scaled.
+    float q[RG][VEC];
+    int rlen[RG];
+    float kscale_head = 1.0f;
+    if constexpr (SK == kScaleHead) kscale_head = load_uniform(p.ks + h);
 #pragma unroll
-  for (int r = 0; r < RG; ++r) {
-    m[r] = kNegInf;
-    l[r] = 0.0f;
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) acc[r][v] = 0.0f;
-  }
-
-  __syncthreads();
-
-  const int64_t lane_off = (int64_t)h * p.kv_shead + part * 16;
-  const int pmask = p.P - 1;
-
-  for (int c0 = t0 + wave * CHUNK; c0 < t_end; c0 += NW * CHUNK) {
-    U4 kr[CL], vr[CL];
-    float ksc[CL], vsc[CL];
-    int tok[CL];
-#pragma unroll
-    for (int i = 0; i < CL; ++i) {
-      const int t = c0 + i * TPL + slot;
-      tok[i] = t;
-      ksc[i] = 1.0f;
-      vsc[i] = 1.0f;
-      if (t < t_end) {
-        const int page = s_pages[(t >> p.logP) - p0];
-        const int within = t & pmask;
-        const int64_t off = (int64_t)page * p.kv_sblk + (int64_t)within * p.kv_stok + lane_off;
-        kr[i] = load16(p.k + off);
-        vr[i] = load16(p.v + off);
-        if constexpr (SK == kScaleTokenHead) {
-          const int64_t so = (int64_t)page * p.sc_sblk + (int64_t)within * p.sc_stok + (int64_t)h * p.sc_shead;
-          ksc[i] = p.ks[so];
-          vsc[i] = p.vs[so];
-        }
+    for (int r = 0; r < RG; ++r) {
+      const int gr = rg * RG + r;
+      if (gr < rows) {
+        const int qi = gr / p.G;
+        const int hq = h * p.G + (gr - qi * p.G);
+        const int64_t base = (int64_t)b * p.q_sb + (int64_t)qi * p.q_sq + (int64_t)hq * p.q_sh + part * VEC;
+        load_q<VEC>(p, base, p.qscale * kscale_head, q[r]);
+        rlen[r] = len - (p.Q - 1 - qi);
       } else {
-        kr[i] = U4{0, 0, 0, 0};
-        vr[i] = U4{0, 0, 0, 0};
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) q[r][v] = 0.0f;
+        rlen[r] = 0;
       }
     }
 
-    // Scores of every row against the chunk's tokens.
-    float s[CL][RG];
+    float m[RG], l[RG], acc[RG][VEC];
 #pragma unroll
-    for (int i = 0; i < CL; ++i) {
-      float kf[VEC];
-      unpack16<KV>(kr[i], kf);
+    for (int r = 0; r < RG; ++r) {
+      m[r] = kNegInf;
+      l[r] = 0.0f;
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) acc[r][v] = 0.0f;
+    }
+
+    // Chunks k + wave, k + wave + NW, ... of this piece, the next one's loads in flight.
+    const int64_t lane_off = (int64_t)h * p.kv_shead + part * 16;
+    // Pages are fetched one chunk ahead of the loads that use them, which run one chunk ahead of compute.
+    {
+      ChunkRegs<CL> ca, cb;
+      ChunkPages<CL> ga, gb;
+      int kk = k + wave;
+      if (kk < k_end) {
+        fetch_pages<KV, CL, PU>(p, b, kk, len, slot, ga);
+        issue_chunk<KV, SK, CL>(p, ga, h, kk, len, slot, lane_off, ca);
+      }
+      if (kk + NW < k_end) fetch_pages<KV, CL, PU>(p, b, kk + NW, len, slot, gb);
+      while (kk < k_end) {
+        const int kn = kk + NW;
+        const int kn2 = kn + NW;
+        if (kn < k_end) issue_chunk<KV, SK, CL>(p, gb, h, kn, len, slot, lane_off, cb);
+        if (kn2 < k_end) fetch_pages<KV, CL, PU>(p, b, kn2, len, slot, ga);
+        compute_chunk<KV, SK, RG, CL>(ca, kk, slot, q, rlen, m, l, acc);
+        if (kn >= k_end) break;
+        const int kn3 = kn2 + NW;
+        if (kn2 < k_end) issue_chunk<KV, SK, CL>(p, ga, h, kn2, len, slot, lane_off, ca);
+        if (kn3 < k_end) fetch_pages<KV, CL, PU>(p, b, kn3, len, slot, gb);
+        compute_chunk<KV, SK, RG, CL>(cb, kn, slot, q, rlen, m, l, acc);
+        kk = kn2;
+      }
+    }
+
+    // Merge the slots of the wave (disjoint tokens, same channels).
+#pragma unroll
+    for (int off = LPR; off < 64; off <<= 1) {
 #pragma unroll
       for (int r = 0; r < RG; ++r) {
-        float a0 = 0.0f, a1 = 0.0f;
+        const float mo = shfl_xor_f(m[r], off);
+        const float lo = shfl_xor_f(l[r], off);
+        const float mn = fmaxf(m[r], mo);
+        const float mu = mn == kNegInf ? 0.0f : mn;
+        const float a = fast_exp2(m[r] - mu);
+        const float e = fast_exp2(mo - mu);
+        l[r] = l[r] * a + lo * e;
 #pragma unroll
-        for (int v = 0; v < VEC; v += 2) {
-          a0 = fmaf(q[r][v], kf[v], a0);
-          a1 = fmaf(q[r][v + 1], kf[v + 1], a1);
+        for (int v = 0; v < VEC; ++v) acc[r][v] = acc[r][v] * a + shfl_xor_f(acc[r][v], off) * e;
+        m[r] = mn;
+      }
+    }
+    if (slot == 0) {
+#pragma unroll
+      for (int r = 0; r < RG; ++r) {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) s_acc[wave][r][part * VEC + v] = acc[r][v];
+        if (part == 0) {
+          s_m[wave][r] = m[r];
+          s_l[wave][r] = l[r];
         }
-        s[i][r] = a0 + a1;
       }
     }
+    __syncthreads();
+
+    // Merge the waves; write the segment's output, or this piece's partial.
+    const int seg = b * HR + hr;
+    const int64_t g_first = seg_c0 / per;
+    const int64_t g_last = (seg_c0 + nb - 1) / per;
+    const bool whole = g_first == g_last;
+    const int64_t wslot = (int64_t)seg + g;
+    const float vscale_head = SK == kScaleHead ? load_uniform(p.vs + h) : 1.0f;
+    for (int idx = tid; idx < RG * D; idx += NT) {
+      const int r = idx / D;
+      const int ch = idx - r * D;
+      const int gr = rg * RG + r;
+      if (gr >= rows) continue;
+      float M = s_m[0][r];
 #pragma unroll
-    for (int i = 0; i < CL; ++i) {
+      for (int w = 1; w < NW; ++w) M = fmaxf(M, s_m[w][r]);
+      const float mu = M == kNegInf ? 0.0f : M;
+      float L = 0.0f, A = 0.0f;
 #pragma unroll
-      for (int r = 0; r < RG; ++r) {
-        float x = group_sum<LPT>(s[i][r]);
-        if constexpr (SK == kScaleTokenHead) x *= ksc[i];
-        s[i][r] = tok[i] < rlen[r] ? x : kNegInf;
+      for (int w = 0; w < NW; ++w) {
+        const float e = fast_exp2(s_m[w][r] - mu);
+        L += s_l[w][r] * e;
+        A += s_acc[w][r][ch] * e;
+      }
+      const float o = L > 0.0f ? A / L * vscale_head : 0.0f;
+      if (whole) {
+        const int qi = gr / p.G;
+        const int hq = h * p.G + (gr - qi * p.G);
+        store_float(p.out, (int64_t)b * p.o_sb + (int64_t)qi * p.o_sq + (int64_t)hq * p.o_sh + ch, p.out_dtype, o);
+      } else {
+        ws_store(p.ws_out + (wslot * RG + r) * D + ch, o);
+        if (ch == 0) ws_store(p.ws_lse + wslot * RG + r, L > 0.0f ? M + __log2f(L) : kNegInf);
       }
     }
 
-    // Online softmax over the chunk, per slot.
-    float pw[CL][RG];
-#pragma unroll
-    for (int r = 0; r < RG; ++r) {
-      float mc = s[0][r];
-#pragma unroll
-      for (int i = 1; i < CL; ++i) mc = fmaxf(mc, s[i][r]);
-      const float mn = fmaxf(m[r], mc);
-      const float mu = mn == kNegInf ? 0.0f : mn;
-      const float alpha = fast_exp2(m[r] - mu);
-      m[r] = mn;
-      float lsum = l[r] * alpha;
-#pragma unroll
-      for (int i = 0; i < CL; ++i) {
-        const float e = fast_exp2(s[i][r] - mu);
-        lsum += e;
-        pw[i][r] = e * vsc[i];
+    if (!whole) {
+      // Publish this piece, then count it. Partials travel as device-coherent accesses, so the only
+      // ordering needed is that this workgroup's stores have completed before its arrival is counted.
+      ws_publish();
+      __syncthreads();
+      if (tid == 0) {
+        const unsigned npieces = (unsigned)(g_last - g_first + 1);
+        const unsigned prev = __hip_atomic_fetch_add(p.counters + seg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = prev == npieces - 1;
       }
-      l[r] = lsum;
+      __syncthreads();
+      if (s_last) {  // every piece has arrived: combine them (reference.merge_partials) and reset the counter
+        ws_acquire();
+        const int npieces = (int)(g_last - g_first + 1);
+        for (int idx = tid; idx < RG * D; idx += NT) {
+          const int r = idx / D;
+          const int ch = idx - r * D;
+          const int gr = rg * RG + r;
+          if (gr >= rows) continue;
+          const float* lse = p.ws_lse + ((int64_t)seg + g_first) * RG + r;
+          const float* part = p.ws_out + (((int64_t)seg + g_first) * RG + r) * D + ch;
+          float M = kNegInf;
+          for (int j = 0; j < npieces; ++j) M = fmaxf(M, ws_load(lse + (int64_t)j * RG));
+          const float mu = M == kNegInf ? 0.0f : M;
+          float W = 0.0f, O = 0.0f;
+          for (int j0 = 0; j0 < npieces; j0 += 8) {
+            float lv[8], ov[8];
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) acc[r][v] *= alpha;
-    }
+            for (int j = 0; j < 8; ++j) {
+              const bool in = j0 + j < npieces;
+              lv[j] = in ? ws_load(lse + (int64_t)(j0 + j) * RG) : kNegInf;
+              ov[j] = in ? ws_load(part + (int64_t)(j0 + j) * RG * D) : 0.0f;
+            }
 #pragma unroll
-    for (int i = 0; i < CL; ++i) {
-      float vf[VEC];
-      unpack16<KV>(vr[i], vf);
-#pragma unroll
-      for (int r = 0; r < RG; ++r) {
-#pragma unroll
-        for (int v = 0; v < VEC; ++v) acc[r][v] = fmaf(pw[i][r], vf[v], acc[r][v]);
+            for (int j = 0; j < 8; ++j) {
+              const float e = fast_exp2(lv[j] - mu);
+              W += e;
+              O = fmaf(e, ov[j], O);
+            }
+          }
+          const int qi = gr / p.G;
+          const int hq = h * p.G + (gr - qi * p.G);
+          store_float(p.out, (int64_t)b * p.o_sb + (int64_t)qi * p.o_sq + (int64_t)hq * p.o_sh + ch, p.out_dtype,
+                      W > 0.0f ? O / W : 0.0f);
+        }
+        if (tid == 0) __hip_atomic_store(p.counters + seg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
-  }
+    __syncthreads();  // the LDS merge buffers are rewritten by the next piece
 
-  // Merge the slots of the wave: lanes with the same part hold states over disjoint tokens.
-#pragma unroll
-  for (int off = LPT; off < 64; off <<= 1) {
-#pragma unroll
-    for (int r = 0; r < RG; ++r) {
-      const float mo = shfl_xor_f(m[r], off);
-      const float lo = shfl_xor_f(l[r], off);
-      const float mn = fmaxf(m[r], mo);
-      const float mu = mn == kNegInf ? 0.0f : mn;
-      const float a = fast_exp2(m[r] - mu);
-      const float c = fast_exp2(mo - mu);
-      l[r] = l[r] * a + lo * c;
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) acc[r][v] = acc[r][v] * a + shfl_xor_f(acc[r][v], off) * c;
-      m[r] = mn;
+    c = pe;
+    if (c >= c_end) break;
+    ++hr;
+    k = 0;
+    if (hr == HR) {
+      hr = 0;
+      do {
+        ++b;
+      } while (s_prefix[b + 1] == s_prefix[b]);
+      b = sread(b);
+      nb = sread(s_prefix[b + 1] - s_prefix[b]);
     }
   }
-  if (slot == 0) {
-#pragma unroll
-    for (int r = 0; r < RG; ++r) {
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) s_acc[wave][r][part * VEC + v] = acc[r][v];
-      if (part == 0) {
-        s_m[wave][r] = m[r];
-        s_l[wave][r] = l[r];
-      }
-    }
-  }
-  __syncthreads();
-
-  // Merge the waves and write this split's result.
-  const float vscale_head = SK == kScaleHead ? p.vs[h] : 1.0f;
-  for (int idx = threadIdx.x; idx < RG * D; idx += NW * 64) {
-    const int r = idx / D;
-    const int ch = idx - r * D;
-    const int gr = rg * RG + r;
-    if (gr >= rows) continue;
-    float M = s_m[0][r];
-#pragma unroll
-    for (int w = 1; w < NW; ++w) M = fmaxf(M, s_m[w][r]);
-    const float mu = M == kNegInf ? 0.0f : M;
-    float L = 0.0f, A = 0.0f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      const float e = fast_exp2(s_m[w][r] - mu);
-      L += s_l[w][r] * e;
-      A += s_acc[w][r][ch] * e;
-    }
-    const float o = L > 0.0f ? A / L * vscale_head : 0.0f;
-    const int qi = gr / p.G;
-    const int hq = h * p.G + (gr - qi * p.G);
-    if (p.S == 1) {
-      const int64_t oi = (int64_t)b * p.o_sb + (int64_t)qi * p.o_sq + (int64_t)hq * p.o_sh + ch;
-      store_float(p.out, oi, p.out_dtype, o);
-    } else {
-      const int64_t row = ((int64_t)b * p.Q + qi) * p.Hq + hq;
-      p.part_out[(row * p.S + split) * D + ch] = o;
-      if (ch == 0) p.part_lse[row * p.S + split] = L > 0.0f ? M + __log2f(L) : kNegInf;
-    }
-  }
-  (void)EB;
 }
 
-// Exact combine of the splits (reference.merge_partials): out = sum_s 2^(lse_s - M) out_s / sum_s 2^(lse_s - M).
-// One wave per (sequence, query, head) row; only splits that start below the sequence's length exist.
-template <int D>
-__global__ __launch_bounds__(256) void decode_combine_kernel(const DecodeParams p) {
-  constexpr int PER = D / 64;
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int64_t nrows = (int64_t)p.B * p.Q * p.Hq;
-  if (row >= nrows) return;
-  const int b = (int)(row / ((int64_t)p.Q * p.Hq));
-  const int rem = (int)(row - (int64_t)b * p.Q * p.Hq);
-  const int qi = rem / p.Hq;
-  const int hq = rem - qi * p.Hq;
-  int len = p.lens[b];
-  len = len < 0 ? 0 : (len > p.len_cap ? p.len_cap : len);
-  const int ns = min((len + p.split_tokens - 1) / p.split_tokens, p.S);
-
-  const float* lse = p.part_lse + row * p.S;
-  float M = kNegInf;
-  for (int s = lane; s < ns; s += 64) M = fmaxf(M, lse[s]);
-  M = wave_max(M);
-  const float mu = M == kNegInf ? 0.0f : M;
-
-  float o[PER];
-#pragma unroll
-  for (int j = 0; j < PER; ++j) o[j] = 0.0f;
-  float W = 0.0f;
-  const float* part = p.part_out + row * p.S * D + lane * PER;
-  for (int s = 0; s < ns; ++s) {
-    const float w = fast_exp2(lse[s] - mu);
-    W += w;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) o[j] = fmaf(w, part[(int64_t)s * D + j], o[j]);
-  }
-  const float inv = W > 0.0f ? 1.0f / W : 0.0f;
-  const int64_t oi = (int64_t)b * p.o_sb + (int64_t)qi * p.o_sq + (int64_t)hq * p.o_sh + lane * PER;
-#pragma unroll
-  for (int j = 0; j < PER; ++j) store_float(p.out, oi + j, p.out_dtype, o[j] * inv);
-}
-
-template <int KV, int SK, int D, int RG>
-static hipError_t launch_split_t(const DecodeParams& p, hipStream_t stream) {
-  dim3 grid(p.S, p.Hkv * p.n_rg, p.B);
-  dim3 block(kDecodeWaves * 64);
-  hipLaunchKernelGGL((decode_split_kernel<KV, SK, D, RG, kDecodeWaves, kDecodeLoads>), grid, block, 0, stream, p);
+template <int KV, int SK, int RG>
+static hipError_t launch_t(const DecodeParams& p, bool page_uniform, hipStream_t stream) {
+  dim3 grid(p.grid), block(kDecodeWaves * 64);
+  if (page_uniform)
+    hipLaunchKernelGGL((decode_kernel<KV, SK, RG, true>), grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL((decode_kernel<KV, SK, RG, false>), grid, block, 0, stream, p);
   return hipGetLastError();
 }
 
-template <int KV, int SK, int D>
-static hipError_t launch_split_rg(const DecodeParams& p, int rg, hipStream_t stream) {
+template <int KV, int SK>
+static hipError_t launch_rg(const DecodeParams& p, int rg, bool pu, hipStream_t stream) {
   switch (rg) {
-    case 1: return launch_split_t<KV, SK, D, 1>(p, stream);
-    case 2: return launch_split_t<KV, SK, D, 2>(p, stream);
-    case 4: return launch_split_t<KV, SK, D, 4>(p, stream);
+    case 1: return launch_t<KV, SK, 1>(p, pu, stream);
+    case 2: return launch_t<KV, SK, 2>(p, pu, stream);
+    case 4: return launch_t<KV, SK, 4>(p, pu, stream);
     default: return hipErrorInvalidValue;
   }
 }
 
-template <int D>
-static hipError_t launch_split_d(const DecodeParams& p, int kv, int sk, int rg, hipStream_t stream) {
-  if (kv == kKvBf16) return launch_split_rg<kKvBf16, kScaleNone, D>(p, rg, stream);
-  if (kv == kKvFp8 && sk == kScaleHead) return launch_split_rg<kKvFp8, kScaleHead, D>(p, rg, stream);
-  if (kv == kKvFp8 && sk == kScaleTokenHead) return launch_split_rg<kKvFp8, kScaleTokenHead, D>(p, rg, stream);
-  if (kv == kKvInt8 && sk == kScaleHead) return launch_split_rg<kKvInt8, kScaleHead, D>(p, rg, stream);
-  if (kv == kKvInt8 && sk == kScaleTokenHead) return launch_split_rg<kKvInt8, kScaleTokenHead, D>(p, rg, stream);
+int decode_chunk_tokens(int kv_dtype, int rows_per_group) {
+  return decode_loads(rows_per_group) * decode_rows_per_load(kv_dtype);
+}
+
+int decode_rows_per_load(int kv_dtype) {
+  return kv_dtype == kKvBf16 ? KvTraits<kKvBf16>::kRowsPerLoad : KvTraits<kKvFp8>::kRowsPerLoad;
+}
+
+hipError_t launch_decode(const DecodeParams& p, int kv_dtype, int scale_kind, int rows_per_group, hipStream_t stream) {
+  const bool pu = p.P >= decode_rows_per_load(kv_dtype);
+  if (kv_dtype == kKvBf16) return launch_rg<kKvBf16, kScaleNone>(p, rows_per_group, pu, stream);
+  if (kv_dtype == kKvFp8 && scale_kind == kScaleHead) return launch_rg<kKvFp8, kScaleHead>(p, rows_per_group, pu, stream);
+  if (kv_dtype == kKvFp8 && scale_kind == kScaleTokenHead)
+    return launch_rg<kKvFp8, kScaleTokenHead>(p, rows_per_group, pu, stream);
+  if (kv_dtype == kKvInt8 && scale_kind == kScaleHead) return launch_rg<kKvInt8, kScaleHead>(p, rows_per_group, pu, stream);
+  if (kv_dtype == kKvInt8 && scale_kind == kScaleTokenHead)
+    return launch_rg<kKvInt8, kScaleTokenHead>(p, rows_per_group, pu, stream);
   return hipErrorInvalidValue;
-}
-
-hipError_t launch_decode(const DecodeParams& p, int kv_dtype, int scale_kind, int head_dim, int rows_per_group,
-                         hipStream_t stream, hipEvent_t mid_event) {
-  hipError_t e;
-  switch (head_dim) {
-    case 128: e = launch_split_d<128>(p, kv_dtype, scale_kind, rows_per_group, stream); break;
-    default: return hipErrorInvalidValue;
-  }
-  if (e != hipSuccess) return e;
-  if (mid_event) {
-    e = hipEventRecord(mid_event, stream);
-    if (e != hipSuccess) return e;
-  }
-  if (p.S > 1) {
-    const int64_t nrows = (int64_t)p.B * p.Q * p.Hq;
-    dim3 grid((unsigned)((nrows + 3) / 4));
-    hipLaunchKernelGGL(decode_combine_kernel<128>, grid, dim3(256), 0, stream, p);
-    e = hipGetLastError();
-  }
-  return e;
 }
 
 }  // namespace bpt

@@ -72,7 +72,18 @@ typedef enum { BPT_IDX_I32 = 0, BPT_IDX_I64 = 1 } bpt_index_dtype;
  *
  * max_context bounds context_lens and sizes the launch (no device->host read); lengths above it, or
  * above max_blocks_per_seq * page_size, are truncated to that bound. Page ids are clamped into
- * [0, num_blocks). num_splits = 0 lets bpt_decode_plan choose the split-K partition count.
+ * [0, num_blocks). batch is at most 4096.
+ *
+ * Split-K: each (sequence, KV head) is cut into partitions whose log-sum-exp partials are combined exactly
+ * inside the same launch. num_splits = 0 balances the whole batch over the launched workgroups (ragged
+ * lengths included); num_splits = S > 0 cuts a max_context-long sequence into S partitions (shorter ones
+ * into proportionally fewer).
+ *
+ * Buffers: bpt_decode_plan reports the size of `workspace` (the split-K partials; any content) and of
+ * `counters` (one uint32 arrival counter per (sequence, KV head, row group)). The counters must be zero
+ * before the first call (allocate them zeroed) and every completed call leaves them zero again, so one
+ * pair serves any number of calls issued in order on one stream, whatever their shapes. Calls that may
+ * overlap (different streams) need separate buffers. q rows and the caches must be 16-byte aligned.
  */
 typedef struct {
   uint32_t struct_size; /* sizeof(bpt_decode_args): guards against a stale binding */
@@ -84,8 +95,9 @@ typedef struct {
 
   int32_t batch, num_queries, num_q_heads, num_kv_heads, head_dim, page_size;
   int32_t num_blocks, max_blocks_per_seq, max_context;
-  int32_t num_splits;   /* in: 0 = auto. bpt_decode_plan writes the value used */
-  int32_t split_tokens; /* out of bpt_decode_plan: tokens per split */
+  int32_t num_splits;   /* in: 0 = balance automatically, S > 0 = S partitions of a max_context sequence */
+  int32_t chunk_tokens; /* out of bpt_decode_plan: tokens one wave streams per step */
+  int32_t grid_groups;  /* out of bpt_decode_plan: workgroups launched */
   float sm_scale;
 
   const void* q;
@@ -101,9 +113,10 @@ typedef struct {
   const int32_t* context_lens;
   void* out;
   int64_t out_stride_b, out_stride_q, out_stride_h;
-  void* workspace;        /* split-K partials; bpt_decode_plan gives the size (0 when one split) */
+  void* workspace;        /* split-K partials, 256-byte aligned */
   size_t workspace_bytes;
-  void* mid_event;        /* optional hipEvent_t recorded between the split kernel and the combine */
+  void* counters;         /* uint32 arrival counters, zero before first use and after every call */
+  size_t counters_bytes;
 } bpt_decode_args;
 
 /*
@@ -138,10 +151,11 @@ typedef struct {
 
 /* ---- entry points ------------------------------------------------------------------------------- */
 
-/* Host-only: validate args, choose num_splits/split_tokens, report workspace bytes. Touches no GPU. */
-int bpt_decode_plan(bpt_decode_args* args, size_t* workspace_bytes);
+/* Host-only: validate args, fill chunk_tokens / grid_groups, report the workspace and counter sizes in
+ * bytes. Touches no GPU. */
+int bpt_decode_plan(bpt_decode_args* args, size_t* workspace_bytes, size_t* counters_bytes);
 
-/* Paged decode attention (split kernel, then the log-sum-exp combine when num_splits > 1). */
+/* Paged decode attention: one kernel launch, split-K partials combined in the same launch. */
 int bpt_paged_decode(const bpt_decode_args* args, void* stream);
 
 /* Quantize-on-write of new K/V rows into their (page, slot). */

@@ -43,33 +43,57 @@ def cpu_case(fmt="fp8", b=2, nq=1, hq=16, hkv=8, d=128, nb=64, page=16, max_bloc
     return q, k, v, table, lens, ks, vs
 
 
+def align256(x):
+    return (x + 255) // 256 * 256
+
+
+def expected_workspace(batch, segments_per_seq, rows_per_group, grid):
+    slots = batch * segments_per_seq + grid
+    return align256(slots * rows_per_group * (128 + 1) * 4)  # normalized outputs + log-sum-exp, float32
+
+
+def expected_counters(batch, segments_per_seq):
+    return align256(batch * segments_per_seq * 4)  # one uint32 per segment
+
+
 def test_plan_honours_requested_splits(built_lib):
+    # 32/8 heads: 4 rows per KV head, 32-token chunks; 32768 tokens in 32 partitions of 32 chunks each.
     q, k, v, table, lens, ks, vs = cpu_case(b=4, hq=32, max_blocks=2048, nb=8192)
-    splits, split_tokens, ws = decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=32768, num_splits=32)
-    assert (splits, split_tokens) == (32, 1024)
-    assert ws == 4 * 1 * 32 * 32 * (128 + 1) * 4  # out partials + lse, float32
+    grid, chunk, ws, cnt = decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=32768, num_splits=32)
+    assert chunk == 32 and grid == 4 * 8 * 32
+    assert ws == expected_workspace(4, 8, 4, grid) and cnt == expected_counters(4, 8)
 
 
-def test_plan_auto_single_split_needs_no_workspace(built_lib):
-    q, k, v, table, lens, ks, vs = cpu_case("bf16", b=1)
-    splits, split_tokens, ws = decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=64, num_splits=1)
-    assert splits == 1 and ws == 0 and split_tokens % 16 == 0 and split_tokens >= 64
+def test_plan_auto_launches_two_groups_per_cu_at_most(built_lib):
+    q, k, v, table, lens, ks, vs = cpu_case("fp8", b=32, max_blocks=256, nb=8192)
+    grid, chunk, ws, cnt = decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=4096)
+    assert chunk % 8 == 0 and grid == 512 and ws == expected_workspace(32, 8, 2, 512) and cnt == expected_counters(32, 8)
+    qb, kb, vb, tb, lb, _, _ = cpu_case("bf16", b=1)
+    grid, chunk_bf16, _, _ = decode_plan(qb, kb, vb, tb, lb, None, None, scale=0.1, max_context=64)
+    assert chunk_bf16 == chunk // 2  # 16 lanes per bf16 row, 8 per one-byte row: half the rows per load
+    assert grid == 8 * -(-64 // chunk_bf16)  # never more groups than chunks that could exist
 
 
-@pytest.mark.parametrize("max_context", [1, 100, 4096, 32768])
-def test_auto_plan_covers_the_context_in_whole_chunks(built_lib, max_context):
+@pytest.mark.parametrize("max_context", [0, 1, 100, 4096, 32768])
+def test_plan_workspace_grows_with_the_launch(built_lib, max_context):
     q, k, v, table, lens, ks, vs = cpu_case(b=32, max_blocks=4096, nb=8192)
-    splits, split_tokens, _ = decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=max_context)
-    assert split_tokens % 32 == 0 and splits * split_tokens >= max_context
-    assert (splits - 1) * split_tokens < max(max_context, 1)
-    assert split_tokens // 16 + 1 <= 512  # the split's pages fit the LDS page table
+    grid, chunk, ws, cnt = decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=max_context)
+    bound = 32 * 8 * -(-min(max_context, 4096 * 16) // chunk)
+    assert 1 <= grid <= max(min(512, bound), 1)
+    assert ws == expected_workspace(32, 8, 2, grid) and cnt == expected_counters(32, 8)
+
+
+def test_plan_rejects_oversized_batches(built_lib):
+    q, k, v, table, lens, ks, vs = cpu_case(b=4097)
+    with pytest.raises(ValueError, match="exceeds 4096"):
+        decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=16)
 
 
 def test_stale_binding_is_refused(built_lib):
     a = _lib.DecodeArgs()
     a.struct_size = 12
     with pytest.raises(ValueError, match="stale binding"):
-        _lib.check(built_lib.bpt_decode_plan(ctypes.byref(a), None))
+        _lib.check(built_lib.bpt_decode_plan(ctypes.byref(a), None, None))
 
 
 @pytest.mark.parametrize(

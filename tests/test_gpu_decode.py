@@ -219,6 +219,40 @@ def test_measured_shapes_at_full_size(name):
     check(got, oracle_out(w), name)
 
 
+def test_many_short_sequences_share_workgroups():
+    """More segments than workgroups: a workgroup's range walks many (sequence, head) segments, with
+    empty sequences at the start, middle and end of the batch."""
+    lengths = [0] + [int(x) for x in np.random.default_rng(3).integers(1, 200, 300)] + [0, 5, 0]
+    c = make_case("fp8", lengths, pool_extra=3)
+    got, want = run_case(c)
+    check(got, want, "300 short sequences")
+    for i, t in enumerate(lengths):
+        if t == 0:
+            assert got[i].float().abs().sum().item() == 0
+
+
+def test_workspace_counters_reset_between_calls_of_different_shapes():
+    """One cached workspace serves calls of different shapes in a row; an explicit zeroed one works too."""
+    from bpt_amd import decode_plan, paged_decode_attention
+
+    cases = [make_case("fp8", [3000, 17, 900], seed=s) for s in range(2)] + [make_case("int8", [4096] * 4, scales="token")]
+    for rep in range(2):
+        for c in cases:
+            got, want = run_case(c, num_splits=None if rep else 8)
+            check(got, want, f"rep {rep}")
+    c = cases[0]
+    _, _, ws_bytes, cnt_bytes = decode_plan(c["q"], c["k"], c["v"], c["table"], c["lens"], c["ks"], c["vs"],
+                                            scale=0.1, max_context=3000, num_splits=16)
+    ws = torch.full((ws_bytes,), 0x7F, dtype=torch.uint8, device=DEV)  # partials need no initialization
+    cnt = torch.zeros(cnt_bytes, dtype=torch.uint8, device=DEV)
+    a = paged_decode_attention(c["q"], c["k"], c["v"], c["table"], c["lens"], c["ks"], c["vs"], scale=0.1,
+                               max_context=3000, num_splits=16, workspace=ws, counters=cnt)
+    b = paged_decode_attention(c["q"], c["k"], c["v"], c["table"], c["lens"], c["ks"], c["vs"], scale=0.1,
+                               max_context=3000, num_splits=16, workspace=ws, counters=cnt)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and cnt.abs().sum().item() == 0
+
+
 def test_repeated_calls_are_deterministic():
     from bpt_amd import paged_decode_attention, workloads
 
