@@ -13,6 +13,9 @@
 #ifndef BPT_DECODE_GROUPS_PER_CU
 #define BPT_DECODE_GROUPS_PER_CU 2
 #endif
+#ifndef BPT_DECODE_WAVES
+#define BPT_DECODE_WAVES 4
+#endif
 
 namespace bpt {
 
@@ -20,7 +23,7 @@ constexpr int kHeadDim = 128;
 // Largest batch the decode kernel takes: its chunk-count prefix sum lives in LDS.
 constexpr int kMaxBatch = 4096;
 // Waves per decode workgroup.
-constexpr int kDecodeWaves = 4;
+constexpr int kDecodeWaves = BPT_DECODE_WAVES;
 // Compute units of an MI355X; the auto plan launches kDecodeGroupsPerCu workgroups per CU.
 constexpr int kComputeUnits = 256;
 constexpr int kDecodeGroupsPerCu = BPT_DECODE_GROUPS_PER_CU;

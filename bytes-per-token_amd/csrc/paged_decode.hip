@@ -148,26 +148,43 @@ __device__ __forceinline__ void fetch_pages(const DecodeParams& p, int b, int kk
   }
 }
 
-// Issue chunk kk's 16-byte K and V loads (and per-token scales) into c.
-template <int KV, int SK, int CL>
+// Issue chunk kk's 16-byte K and V loads (and per-token scales) into c. PU: each load's page and the row
+// offset of its first token are wave-uniform, so the address is a scalar base plus this lane's constant
+// 32-bit offset (slot rows down, part * 16 bytes across).
+template <int KV, int SK, int CL, bool PU>
 __device__ __forceinline__ void issue_chunk(const DecodeParams& p, const ChunkPages<CL>& g, int h, int kk, int len,
-                                            int slot, int64_t lane_off, ChunkRegs<CL>& c) {
+                                            int slot, int part, ChunkRegs<CL>& c) {
   constexpr int RPL = KvTraits<KV>::kRowsPerLoad;
   const int tb = kk * CL * RPL;
+  const int64_t head_off = (int64_t)h * p.kv_shead;
 #pragma unroll
   for (int i = 0; i < CL; ++i) {
     const int t = tb + i * RPL + slot;
     c.ks[i] = 1.0f;
     c.vs[i] = 1.0f;
     if (t < len) {
-      const int within = t & (p.P - 1);
-      const int64_t off = (int64_t)g.e[i] * p.kv_sblk + (int64_t)within * p.kv_stok + lane_off;
-      c.k[i] = load16(p.k + off);
-      c.v[i] = load16(p.v + off);
-      if constexpr (SK == kScaleTokenHead) {
-        const int64_t so = (int64_t)g.e[i] * p.sc_sblk + (int64_t)within * p.sc_stok + (int64_t)h * p.sc_shead;
-        c.ks[i] = p.ks[so];
-        c.vs[i] = p.vs[so];
+      if constexpr (PU) {
+        const int w0 = (tb + i * RPL) & (p.P - 1);  // wave-uniform: this lane's row is w0 + slot
+        const int64_t base = (int64_t)g.e[i] * p.kv_sblk + (int64_t)w0 * p.kv_stok + head_off;
+        const uint32_t lane_off = (uint32_t)(slot * p.kv_stok) + (uint32_t)part * 16u;
+        c.k[i] = load16(p.k + base + lane_off);
+        c.v[i] = load16(p.v + base + lane_off);
+        if constexpr (SK == kScaleTokenHead) {
+          const int64_t sb = (int64_t)g.e[i] * p.sc_sblk + (int64_t)w0 * p.sc_stok + (int64_t)h * p.sc_shead;
+          const uint32_t so = (uint32_t)(slot * p.sc_stok);
+          c.ks[i] = p.ks[sb + so];
+          c.vs[i] = p.vs[sb + so];
+        }
+      } else {
+        const int within = t & (p.P - 1);
+        const int64_t off = (int64_t)g.e[i] * p.kv_sblk + (int64_t)within * p.kv_stok + head_off + part * 16;
+        c.k[i] = load16(p.k + off);
+        c.v[i] = load16(p.v + off);
+        if constexpr (SK == kScaleTokenHead) {
+          const int64_t so = (int64_t)g.e[i] * p.sc_sblk + (int64_t)within * p.sc_stok + (int64_t)h * p.sc_shead;
+          c.ks[i] = p.ks[so];
+          c.vs[i] = p.vs[so];
+        }
       }
     } else {
       c.k[i] = U4{0, 0, 0, 0};
@@ -176,7 +193,33 @@ __device__ __forceinline__ void issue_chunk(const DecodeParams& p, const ChunkPa
   }
 }
 
-// This lane's VEC query channels of row (b, qi, hq), loaded as 16-byte vectors, times cs.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Softmax weights are 2^(score - m + kBias) with the reference point m kept within kSlack of the largest
+// score seen (log2 units): weights stay below 2^12, well inside f16, and small ones keep f16 precision.
+constexpr float kBias = 4.0f;
+constexpr float kSlack = 8.0f;
+
+// Round-to-nearest-even float -> bf16 pair.
+__device__ __forceinline__ bf16x2 pack_bf16(float a, float b) {
+  return bf16x2{(__bf16)a, (__bf16)b};
+}
+
+// The query rows of a piece in the form the score path consumes. Dot-product paths (FP8, BF16 caches)
+// keep q unscaled as bf16 pairs: exact for a bf16 q; for an f16 / f32 q (QS) a second pair holds the
+// rounding remainder, so hi + lo carries 16 significant bits. The INT8 path keeps floats pre-scaled.
+template <int KV, int RG, bool QS>
+struct QRows {
+  static constexpr int VEC = KvTraits<KV>::kVec;
+  static constexpr bool kDot = KV != kKvInt8;
+  bf16x2 hi[RG][kDot ? VEC / 2 : 1];
+  bf16x2 lo[RG][(kDot && QS) ? VEC / 2 : 1];
+  float f[RG][kDot ? 1 : VEC];
+  float scale;  // applied to each reduced score
+};
+
+// This lane's VEC query channels of row (b, qi, hq), loaded as 16-byte vectors (unscaled floats).
 template <int VEC>
 __device__ __forceinline__ void load_q(const DecodeParams& p, int64_t base, float cs, float* q) {
   const uint8_t* src = (const uint8_t*)p.q;
@@ -218,30 +261,63 @@ __device__ __forceinline__ void load_q(const DecodeParams& p, int64_t base, floa
 }
 
 // Fold chunk kk into this lane's online-softmax state.
-template <int KV, int SK, int RG, int CL>
-__device__ __forceinline__ void compute_chunk(const ChunkRegs<CL>& c, int kk, int slot,
-                                              const float (&q)[RG][KvTraits<KV>::kVec], const int (&rlen)[RG],
-                                              float (&m)[RG], float (&l)[RG], float (&acc)[RG][KvTraits<KV>::kVec]) {
+template <int KV, int SK, int RG, int CL, bool QS>
+__device__ __forceinline__ void compute_chunk(const ChunkRegs<CL>& c, int kk, int slot, const QRows<KV, RG, QS>& q,
+                                              const int (&rlen)[RG], float (&m)[RG], float (&l)[RG],
+                                              float (&acc)[RG][KvTraits<KV>::kVec]) {
   constexpr int VEC = KvTraits<KV>::kVec;
   constexpr int LPR = KvTraits<KV>::kLanesPerRow;
   constexpr int RPL = KvTraits<KV>::kRowsPerLoad;
   constexpr int CH = CL * RPL;
+  constexpr bool kDotK = KV != kKvInt8;  // scores from packed bf16 dot products
+  constexpr bool kDotV = KV == kKvFp8;   // values through packed f16 dot products over token pairs
+  static_assert(!kDotV || CL % 2 == 0, "token pairs need an even number of loads per chunk");
   const int tb = kk * CH + slot;
 
+  // ---- scores: this lane's partial dot products, summed over the lanes of each token row ------------
   float s[CL][RG];
 #pragma unroll
   for (int i = 0; i < CL; ++i) {
-    float kf[VEC];
-    unpack16<KV>(c.k[i], kf);
+    const uint32_t w[4] = {c.k[i].x, c.k[i].y, c.k[i].z, c.k[i].w};
+    if constexpr (kDotK) {
+      bf16x2 kp[VEC / 2];
+      if constexpr (KV == kKvFp8) {
 #pragma unroll
-    for (int r = 0; r < RG; ++r) {
-      float a0 = 0.0f, a1 = 0.0f;
+        for (int j = 0; j < 4; ++j) {
+          kp[2 * j] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[j], 1.0f, false);
+          kp[2 * j + 1] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[j], 1.0f, true);
+        }
+      } else {
 #pragma unroll
-      for (int v = 0; v < VEC; v += 2) {
-        a0 = fmaf(q[r][v], kf[v], a0);
-        a1 = fmaf(q[r][v + 1], kf[v + 1], a1);
+        for (int j = 0; j < 4; ++j) kp[j] = __builtin_bit_cast(bf16x2, w[j]);
       }
-      s[i][r] = a0 + a1;
+#pragma unroll
+      for (int r = 0; r < RG; ++r) {
+        float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < VEC / 2; j += 2) {
+          a0 = __builtin_amdgcn_fdot2_f32_bf16(q.hi[r][j], kp[j], a0, false);
+          a1 = __builtin_amdgcn_fdot2_f32_bf16(q.hi[r][j + 1], kp[j + 1], a1, false);
+          if constexpr (QS) {
+            a0 = __builtin_amdgcn_fdot2_f32_bf16(q.lo[r][j], kp[j], a0, false);
+            a1 = __builtin_amdgcn_fdot2_f32_bf16(q.lo[r][j + 1], kp[j + 1], a1, false);
+          }
+        }
+        s[i][r] = a0 + a1;
+      }
+    } else {
+      float kf[VEC];
+      unpack16<KV>(c.k[i], kf);
+#pragma unroll
+      for (int r = 0; r < RG; ++r) {
+        float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+        for (int v = 0; v < VEC; v += 2) {
+          a0 = fmaf(q.f[r][v], kf[v], a0);
+          a1 = fmaf(q.f[r][v + 1], kf[v + 1], a1);
+        }
+        s[i][r] = a0 + a1;
+      }
     }
   }
 #pragma unroll
@@ -249,22 +325,32 @@ __device__ __forceinline__ void compute_chunk(const ChunkRegs<CL>& c, int kk, in
     const int t = tb + i * RPL;
 #pragma unroll
     for (int r = 0; r < RG; ++r) {
-      float x = group_sum<LPR>(s[i][r]);
+      float x = group_sum<LPR>(s[i][r]) * q.scale;
       if constexpr (SK == kScaleTokenHead) x *= c.ks[i];
       s[i][r] = t < rlen[r] ? x : kNegInf;
     }
   }
+
+  // ---- online softmax. m is a reference point, moved only when a score passes it by kSlack: weights
+  // are 2^(score - m + kBias) <= 2^(kSlack + kBias), so the accumulators are rarely rescaled and the
+  // packed f16 weights never overflow. ------------------------------------------------------------------
   float pw[CL][RG];
 #pragma unroll
   for (int r = 0; r < RG; ++r) {
     float mc = s[0][r];
 #pragma unroll
     for (int i = 1; i < CL; ++i) mc = fmaxf(mc, s[i][r]);
-    const float mn = fmaxf(m[r], mc);
-    const float mu = mn == kNegInf ? 0.0f : mn;
-    const float alpha = fast_exp2(m[r] - mu);
-    m[r] = mn;
-    float lsum = l[r] * alpha;
+    const bool move = mc > m[r] + kSlack;
+    if (__any(move)) {
+      const float mn = move ? mc : m[r];
+      const float alpha = move ? fast_exp2(m[r] - mn) : 1.0f;  // 0 when m was -inf
+      l[r] *= alpha;
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) acc[r][v] *= alpha;
+      m[r] = mn;
+    }
+    const float mu = (m[r] == kNegInf ? 0.0f : m[r]) - kBias;
+    float lsum = l[r];
 #pragma unroll
     for (int i = 0; i < CL; ++i) {
       const float e = fast_exp2(s[i][r] - mu);
@@ -272,22 +358,126 @@ __device__ __forceinline__ void compute_chunk(const ChunkRegs<CL>& c, int kk, in
       pw[i][r] = e * c.vs[i];
     }
     l[r] = lsum;
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) acc[r][v] *= alpha;
   }
+
+  // ---- values ------------------------------------------------------------------------------------------
+  if constexpr (kDotV) {
+    // Two token rows of this lane at a time: bytes of rows a and b are interleaved so one f16 pair holds
+    // channel c of both rows, and one dot product adds both rows' weighted contributions to channel c.
 #pragma unroll
-  for (int i = 0; i < CL; ++i) {
-    float vf[VEC];
-    unpack16<KV>(c.v[i], vf);
+    for (int i = 0; i < CL; i += 2) {
+      f16x2 pp[RG];
 #pragma unroll
-    for (int r = 0; r < RG; ++r) {
+      for (int r = 0; r < RG; ++r) pp[r] = f16x2{(_Float16)pw[i][r], (_Float16)pw[i + 1][r]};
+      const uint32_t a[4] = {c.v[i].x, c.v[i].y, c.v[i].z, c.v[i].w};
+      const uint32_t b[4] = {c.v[i + 1].x, c.v[i + 1].y, c.v[i + 1].z, c.v[i + 1].w};
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) acc[r][v] = fmaf(pw[i][r], vf[v], acc[r][v]);
+      for (int d = 0; d < 4; ++d) {
+        const uint32_t lo = __builtin_amdgcn_perm(b[d], a[d], 0x05010400u);  // a.c0 b.c0 a.c1 b.c1
+        const uint32_t hi = __builtin_amdgcn_perm(b[d], a[d], 0x07030602u);  // a.c2 b.c2 a.c3 b.c3
+        const f16x2 v0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 1.0f, false);
+        const f16x2 v1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 1.0f, true);
+        const f16x2 v2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 1.0f, false);
+        const f16x2 v3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 1.0f, true);
+#pragma unroll
+        for (int r = 0; r < RG; ++r) {
+          acc[r][4 * d + 0] = __builtin_amdgcn_fdot2(v0, pp[r], acc[r][4 * d + 0], false);
+          acc[r][4 * d + 1] = __builtin_amdgcn_fdot2(v1, pp[r], acc[r][4 * d + 1], false);
+          acc[r][4 * d + 2] = __builtin_amdgcn_fdot2(v2, pp[r], acc[r][4 * d + 2], false);
+          acc[r][4 * d + 3] = __builtin_amdgcn_fdot2(v3, pp[r], acc[r][4 * d + 3], false);
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < CL; ++i) {
+      float vf[VEC];
+      unpack16<KV>(c.v[i], vf);
+#pragma unroll
+      for (int r = 0; r < RG; ++r) {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) acc[r][v] = fmaf(pw[i][r], vf[v], acc[r][v]);
+      }
     }
   }
 }
 
-template <int KV, int SK, int RG, bool PU>
+// Merge the online-softmax states of the wave's slots (same channels, disjoint tokens) and store the
+// wave's state for one segment: m and l per row, acc per row and channel.
+template <int KV, int RG>
+__device__ __forceinline__ void close_state(float (&m)[RG], float (&l)[RG], float (&acc)[RG][KvTraits<KV>::kVec],
+                                            int slot, int part, float* sm, float* sl, float* sacc) {
+  constexpr int VEC = KvTraits<KV>::kVec;
+  constexpr int LPR = KvTraits<KV>::kLanesPerRow;
+#pragma unroll
+  for (int off = LPR; off < 64; off <<= 1) {
+#pragma unroll
+    for (int r = 0; r < RG; ++r) {
+      const float mo = shfl_xor_f(m[r], off);
+      const float lo = shfl_xor_f(l[r], off);
+      const float mn = fmaxf(m[r], mo);
+      const float mu = mn == kNegInf ? 0.0f : mn;
+      const float a = l[r] > 0.0f ? fast_exp2(m[r] - mu) : 0.0f;
+      const float e = lo > 0.0f ? fast_exp2(mo - mu) : 0.0f;
+      l[r] = l[r] * a + lo * e;
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        const float other = shfl_xor_f(acc[r][v], off);
+        acc[r][v] = (a > 0.0f ? acc[r][v] * a : 0.0f) + (e > 0.0f ? other * e : 0.0f);
+      }
+      m[r] = mn;
+    }
+  }
+  if (slot == 0) {
+#pragma unroll
+    for (int r = 0; r < RG; ++r) {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) sacc[r * kHeadDim + part * VEC + v] = acc[r][v];
+      if (part == 0) {
+        sm[r] = m[r];
+        sl[r] = l[r];
+      }
+    }
+  }
+}
+
+// The q rows of segment (b, KV head h, row group rg): bf16 pairs for the dot-product paths, pre-scaled
+// floats for INT8; and the tokens each row sees (query i of Q sits at position len - Q + i).
+template <int KV, int RG, bool QS>
+__device__ __forceinline__ void load_q_rows(const DecodeParams& p, QRows<KV, RG, QS>& q, int (&rlen)[RG], int b, int h,
+                                            int rg, int rows, int part, int len, float kscale_head) {
+  constexpr int VEC = KvTraits<KV>::kVec;
+  q.scale = QRows<KV, RG, QS>::kDot ? p.qscale * kscale_head : 1.0f;
+#pragma unroll
+  for (int r = 0; r < RG; ++r) {
+    const int gr = rg * RG + r;
+    float qf[VEC];
+    if (gr < rows) {
+      const int qi = gr / p.G;
+      const int hq = h * p.G + (gr - qi * p.G);
+      const int64_t base = (int64_t)b * p.q_sb + (int64_t)qi * p.q_sq + (int64_t)hq * p.q_sh + part * VEC;
+      load_q<VEC>(p, base, QRows<KV, RG, QS>::kDot ? 1.0f : p.qscale * kscale_head, qf);
+      rlen[r] = len - (p.Q - 1 - qi);
+    } else {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) qf[v] = 0.0f;
+      rlen[r] = 0;
+    }
+    if constexpr (QRows<KV, RG, QS>::kDot) {
+#pragma unroll
+      for (int j = 0; j < VEC / 2; ++j) {
+        q.hi[r][j] = pack_bf16(qf[2 * j], qf[2 * j + 1]);
+        if constexpr (QS)
+          q.lo[r][j] = pack_bf16(qf[2 * j] - (float)q.hi[r][j].x, qf[2 * j + 1] - (float)q.hi[r][j].y);
+      }
+    } else {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) q.f[r][v] = qf[v];
+    }
+  }
+}
+
+template <int KV, int SK, int RG, bool PU, bool QS>
 __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeParams p) {
   constexpr int NW = kDecodeWaves;
   constexpr int NT = NW * 64;
@@ -297,7 +487,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
   constexpr int CL = decode_loads(RG);
   constexpr int CH = CL * KvTraits<KV>::kRowsPerLoad;
 
-  __shared__ int s_prefix[kMaxBatch + 1];
+  extern __shared__ int s_prefix[];  // [B + 1] chunks per sequence, exclusive prefix sum
   __shared__ int s_wsum[NW];
   __shared__ int s_last;
   __shared__ float s_m[NW][RG];
@@ -391,6 +581,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
   const int part = lane - slot * LPR;
   const int rows = p.Q * p.G;
 
+  // ---- pieces: the parts of segments inside [c, c_end) ------------------------------------------------
   for (;;) {
     const int64_t seg_c0 = (int64_t)HR * s_prefix[b] + (int64_t)hr * nb;
     const int64_t pe = min(c_end, seg_c0 + nb);
@@ -400,27 +591,10 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
     int len = load_uniform(p.lens + b);
     len = len < 0 ? 0 : (len > p.len_cap ? p.len_cap : len);
 
-    // This lane's slice of each row's query, pre-scaled.
-    float q[RG][VEC];
+    QRows<KV, RG, QS> q;
     int rlen[RG];
-    float kscale_head = 1.0f;
-    if constexpr (SK == kScaleHead) kscale_head = load_uniform(p.ks + h);
-#pragma unroll
-    for (int r = 0; r < RG; ++r) {
-      const int gr = rg * RG + r;
-      if (gr < rows) {
-        const int qi = gr / p.G;
-        const int hq = h * p.G + (gr - qi * p.G);
-        const int64_t base = (int64_t)b * p.q_sb + (int64_t)qi * p.q_sq + (int64_t)hq * p.q_sh + part * VEC;
-        load_q<VEC>(p, base, p.qscale * kscale_head, q[r]);
-        rlen[r] = len - (p.Q - 1 - qi);
-      } else {
-#pragma unroll
-        for (int v = 0; v < VEC; ++v) q[r][v] = 0.0f;
-        rlen[r] = 0;
-      }
-    }
-
+    load_q_rows<KV, RG, QS>(p, q, rlen, b, h, rg, rows, part, len,
+                            SK == kScaleHead ? load_uniform(p.ks + h) : 1.0f);
     float m[RG], l[RG], acc[RG][VEC];
 #pragma unroll
     for (int r = 0; r < RG; ++r) {
@@ -430,64 +604,25 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
       for (int v = 0; v < VEC; ++v) acc[r][v] = 0.0f;
     }
 
-    // Chunks k + wave, k + wave + NW, ... of this piece, the next one's loads in flight.
-    const int64_t lane_off = (int64_t)h * p.kv_shead + part * 16;
-    // Pages are fetched one chunk ahead of the loads that use them, which run one chunk ahead of compute.
+    // Chunks k + wave, k + wave + NW, ... of this piece. A chunk's pages are fetched while the previous
+    // chunk is computed; its K/V loads are issued before that.
     {
-      ChunkRegs<CL> ca, cb;
-      ChunkPages<CL> ga, gb;
+      ChunkRegs<CL> cr;
+      ChunkPages<CL> gp;
       int kk = k + wave;
-      if (kk < k_end) {
-        fetch_pages<KV, CL, PU>(p, b, kk, len, slot, ga);
-        issue_chunk<KV, SK, CL>(p, ga, h, kk, len, slot, lane_off, ca);
-      }
-      if (kk + NW < k_end) fetch_pages<KV, CL, PU>(p, b, kk + NW, len, slot, gb);
+      if (kk < k_end) fetch_pages<KV, CL, PU>(p, b, kk, len, slot, gp);
       while (kk < k_end) {
+        issue_chunk<KV, SK, CL, PU>(p, gp, h, kk, len, slot, part, cr);
         const int kn = kk + NW;
-        const int kn2 = kn + NW;
-        if (kn < k_end) issue_chunk<KV, SK, CL>(p, gb, h, kn, len, slot, lane_off, cb);
-        if (kn2 < k_end) fetch_pages<KV, CL, PU>(p, b, kn2, len, slot, ga);
-        compute_chunk<KV, SK, RG, CL>(ca, kk, slot, q, rlen, m, l, acc);
-        if (kn >= k_end) break;
-        const int kn3 = kn2 + NW;
-        if (kn2 < k_end) issue_chunk<KV, SK, CL>(p, ga, h, kn2, len, slot, lane_off, ca);
-        if (kn3 < k_end) fetch_pages<KV, CL, PU>(p, b, kn3, len, slot, gb);
-        compute_chunk<KV, SK, RG, CL>(cb, kn, slot, q, rlen, m, l, acc);
-        kk = kn2;
+        if (kn < k_end) fetch_pages<KV, CL, PU>(p, b, kn, len, slot, gp);
+        compute_chunk<KV, SK, RG, CL, QS>(cr, kk, slot, q, rlen, m, l, acc);
+        kk = kn;
       }
     }
-
-    // Merge the slots of the wave (disjoint tokens, same channels).
-#pragma unroll
-    for (int off = LPR; off < 64; off <<= 1) {
-#pragma unroll
-      for (int r = 0; r < RG; ++r) {
-        const float mo = shfl_xor_f(m[r], off);
-        const float lo = shfl_xor_f(l[r], off);
-        const float mn = fmaxf(m[r], mo);
-        const float mu = mn == kNegInf ? 0.0f : mn;
-        const float a = fast_exp2(m[r] - mu);
-        const float e = fast_exp2(mo - mu);
-        l[r] = l[r] * a + lo * e;
-#pragma unroll
-        for (int v = 0; v < VEC; ++v) acc[r][v] = acc[r][v] * a + shfl_xor_f(acc[r][v], off) * e;
-        m[r] = mn;
-      }
-    }
-    if (slot == 0) {
-#pragma unroll
-      for (int r = 0; r < RG; ++r) {
-#pragma unroll
-        for (int v = 0; v < VEC; ++v) s_acc[wave][r][part * VEC + v] = acc[r][v];
-        if (part == 0) {
-          s_m[wave][r] = m[r];
-          s_l[wave][r] = l[r];
-        }
-      }
-    }
+    close_state<KV, RG>(m, l, acc, slot, part, &s_m[wave][0], &s_l[wave][0], &s_acc[wave][0][0]);
     __syncthreads();
 
-    // Merge the waves; write the segment's output, or this piece's partial.
+    // ---- merge the waves; write the segment's output, or this piece's partial ---------------------
     const int seg = b * HR + hr;
     const int64_t g_first = seg_c0 / per;
     const int64_t g_last = (seg_c0 + nb - 1) / per;
@@ -499,16 +634,17 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
       const int ch = idx - r * D;
       const int gr = rg * RG + r;
       if (gr >= rows) continue;
-      float M = s_m[0][r];
+      float M = kNegInf;
 #pragma unroll
-      for (int w = 1; w < NW; ++w) M = fmaxf(M, s_m[w][r]);
+      for (int w = 0; w < NW; ++w) M = fmaxf(M, s_m[w][r]);
       const float mu = M == kNegInf ? 0.0f : M;
       float L = 0.0f, A = 0.0f;
 #pragma unroll
       for (int w = 0; w < NW; ++w) {
-        const float e = fast_exp2(s_m[w][r] - mu);
-        L += s_l[w][r] * e;
-        A += s_acc[w][r][ch] * e;
+        const float lw = s_l[w][r];
+        const float e = lw > 0.0f ? fast_exp2(s_m[w][r] - mu) : 0.0f;
+        L += lw * e;
+        A += lw > 0.0f ? s_acc[w][r][ch] * e : 0.0f;
       }
       const float o = L > 0.0f ? A / L * vscale_head : 0.0f;
       if (whole) {
@@ -517,7 +653,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
         store_float(p.out, (int64_t)b * p.o_sb + (int64_t)qi * p.o_sq + (int64_t)hq * p.o_sh + ch, p.out_dtype, o);
       } else {
         ws_store(p.ws_out + (wslot * RG + r) * D + ch, o);
-        if (ch == 0) ws_store(p.ws_lse + wslot * RG + r, L > 0.0f ? M + __log2f(L) : kNegInf);
+        if (ch == 0) ws_store(p.ws_lse + wslot * RG + r, L > 0.0f ? M - kBias + __log2f(L) : kNegInf);
       }
     }
 
@@ -532,7 +668,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
         s_last = prev == npieces - 1;
       }
       __syncthreads();
-      if (s_last) {  // every piece has arrived: combine them (reference.merge_partials) and reset the counter
+      if (s_last) {  // every piece has arrived: combine them (reference.merge_partials), reset the counter
         ws_acquire();
         const int npieces = (int)(g_last - g_first + 1);
         for (int idx = tid; idx < RG * D; idx += NT) {
@@ -541,7 +677,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
           const int gr = rg * RG + r;
           if (gr >= rows) continue;
           const float* lse = p.ws_lse + ((int64_t)seg + g_first) * RG + r;
-          const float* part = p.ws_out + (((int64_t)seg + g_first) * RG + r) * D + ch;
+          const float* prt = p.ws_out + (((int64_t)seg + g_first) * RG + r) * D + ch;
           float M = kNegInf;
           for (int j = 0; j < npieces; ++j) M = fmaxf(M, ws_load(lse + (int64_t)j * RG));
           const float mu = M == kNegInf ? 0.0f : M;
@@ -552,7 +688,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
             for (int j = 0; j < 8; ++j) {
               const bool in = j0 + j < npieces;
               lv[j] = in ? ws_load(lse + (int64_t)(j0 + j) * RG) : kNegInf;
-              ov[j] = in ? ws_load(part + (int64_t)(j0 + j) * RG * D) : 0.0f;
+              ov[j] = in ? ws_load(prt + (int64_t)(j0 + j) * RG * D) : 0.0f;
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
@@ -589,10 +725,17 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
 template <int KV, int SK, int RG>
 static hipError_t launch_t(const DecodeParams& p, bool page_uniform, hipStream_t stream) {
   dim3 grid(p.grid), block(kDecodeWaves * 64);
-  if (page_uniform)
-    hipLaunchKernelGGL((decode_kernel<KV, SK, RG, true>), grid, block, 0, stream, p);
+  const size_t lds = (size_t)(p.B + 1) * sizeof(int);  // the chunk-count prefix sum
+  // A non-bf16 q needs the hi + lo split on the dot-product paths; the INT8 path reads q as floats.
+  const bool qs = KV != kKvInt8 && p.q_dtype != kFBf16;
+  if (page_uniform && !qs)
+    hipLaunchKernelGGL((decode_kernel<KV, SK, RG, true, false>), grid, block, lds, stream, p);
+  else if (page_uniform)
+    hipLaunchKernelGGL((decode_kernel<KV, SK, RG, true, KV != kKvInt8>), grid, block, lds, stream, p);
+  else if (!qs)
+    hipLaunchKernelGGL((decode_kernel<KV, SK, RG, false, false>), grid, block, lds, stream, p);
   else
-    hipLaunchKernelGGL((decode_kernel<KV, SK, RG, false>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((decode_kernel<KV, SK, RG, false, KV != kKvInt8>), grid, block, lds, stream, p);
   return hipGetLastError();
 }
 
