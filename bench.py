@@ -28,6 +28,51 @@ for _p in (ROOT, ROOT / "bytes-per-token_amd"):
 
 METRIC = "KV-read HBM GB/s (% of peak) + µs/call, FP8-KV paged decode attention"
 PEAK_GBPS = 8000.0
+PROFILES = ROOT / "profiles"
+
+
+def profiled_traffic(workload: str) -> dict | None:
+    """HBM bytes per decode launch from the committed rocprofv3 counter summary of this workload, if any.
+
+    The summary holds FETCH_SIZE and WRITE_SIZE per dispatch (two --pmc runs of `bench.py --profile`), each
+    already scaled by what the counter reads for a copy kernel of known size, as a line
+    `traffic_bytes_per_launch: N`.
+    """
+    path = PROFILES / f"decode_kernel_{workload}.md"
+    if not path.exists():
+        return None
+    import re
+
+    m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", path.read_text(), flags=re.M)
+    return {"bytes": int(m.group(1)), "source": f"profiles/{path.name}"} if m else None
+
+
+def profile_pass(args) -> int:
+    """A short run for rocprofv3: cold decode calls on the workload, then three 256 MiB copies.
+
+    The copies calibrate the FETCH_SIZE / WRITE_SIZE counters (each reads a known number of bytes).
+    """
+    import torch
+
+    from bpt_amd import measure, paged_decode_attention, workloads
+
+    torch.cuda.set_device(0)
+    w = workloads.make(args.workload, device="cuda:0", seed=0)
+    flush = measure.ReadProbe(args.flush_bytes)
+    out = torch.empty(tuple(w.q.shape), dtype=torch.bfloat16, device="cuda:0")
+    pargs, kw = w.args(), w.kwargs()
+    for _ in range(args.warmup + args.steps):
+        flush.run()
+        paged_decode_attention(*pargs, **kw, out=out)
+    torch.cuda.synchronize()
+    src = torch.ones(64 << 20, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        measure.copy_probe(dst, src, src.numel() * 4)
+    torch.cuda.synchronize()
+    log(f"profile pass: {args.warmup + args.steps} decode calls ({w.kv_bytes()} KV bytes each), "
+        f"3 copies of {src.numel() * 4} bytes")
+    return 0
 
 
 def log(msg: str) -> None:
@@ -172,6 +217,7 @@ def main() -> int:
     ap.add_argument("--no-configs", action="store_true", help="skip the five-shape table")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--profile", action="store_true", help="short run for rocprofv3 (no JSON line)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -182,6 +228,9 @@ def main() -> int:
             file=sys.stderr,
         )
         return 2
+
+    if args.profile:
+        return profile_pass(args)
 
     import torch
 
@@ -209,6 +258,7 @@ def main() -> int:
     from bpt_amd import decode_plan
 
     groups, chunk_tokens, _, _ = decode_plan(*pargs, **kw)
+    traffic = profiled_traffic(args.workload)
     result = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -220,7 +270,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "fp8_e4m3 codes; bf16/f16 dot2 with f32 accumulation",
         "data": "synthetic",
         "config": {
             "workload": args.workload,
@@ -252,7 +302,8 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(value / PEAK_GBPS, 4),
             "kernel_us": round(ms_per_step * 1e3, 2),
-            "traffic": None,
+            "traffic": traffic["bytes"] if traffic else None,
+            "traffic_source": traffic["source"] if traffic else None,
         },
     }
     del w, out, pargs, kw

@@ -10,7 +10,6 @@ Events are recorded on the current stream, which is the stream the library's ker
 from __future__ import annotations
 
 import ctypes
-import statistics
 from collections.abc import Callable
 
 import torch
@@ -64,36 +63,24 @@ def fp8_encode(x: torch.Tensor, scale: float = 1.0) -> torch.Tensor:
     return out
 
 
-def event_times_ms(
-    fn: Callable[[], object], *, warmup: int, iters: int, flush: ReadProbe | None = None, mid: bool = False
-) -> list[float] | list[tuple[float, float]]:
+def event_times_ms(fn: Callable[[], object], *, warmup: int, iters: int, flush: ReadProbe | None = None) -> list[float]:
     """Milliseconds per call with events on the current stream; one synchronize at the end.
 
-    With `flush`, the probe reads its buffer before every timed call (not timed). With `mid`, `fn` takes
-    the event to record between its two kernels and (total, first-kernel) pairs are returned.
+    With `flush`, the probe reads its buffer before every timed call (not timed).
     """
     for _ in range(warmup):
-        fn() if not mid else fn(None)
+        fn()
     torch.cuda.synchronize()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
-    mids = [torch.cuda.Event(enable_timing=True) for _ in range(iters)] if mid else None
-    if mids is not None:
-        for e in mids:  # materialize the underlying HIP events so their handles can be passed down
-            e.record()
     for i in range(iters):
         if flush is not None:
             flush.run()
         starts[i].record()
-        if mids is None:
-            fn()
-        else:
-            fn(mids[i])
+        fn()
         ends[i].record()
     torch.cuda.synchronize()
-    if mids is None:
-        return [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    return [(s.elapsed_time(e), s.elapsed_time(m)) for s, m, e in zip(starts, mids, ends)]
+    return [s.elapsed_time(e) for s, e in zip(starts, ends)]
 
 
 def graph_time_ms(fn: Callable[[], object], *, calls: int = 20, warmup: int = 3, iters: int = 20) -> list[float]:
@@ -116,12 +103,3 @@ def measured_read_gbps(nbytes: int = 4 << 30, iters: int = 10) -> float:
     times = event_times_ms(probe.run, warmup=3, iters=iters)
     del probe
     return nbytes / (min(times) / 1e3) / 1e9
-
-
-def summarize(times_ms: list[float]) -> dict[str, float]:
-    return {
-        "n": len(times_ms),
-        "median_ms": statistics.median(times_ms),
-        "mean_ms": statistics.fmean(times_ms),
-        "min_ms": min(times_ms),
-    }

@@ -106,3 +106,10 @@ def test_fp8_per_token_matches_the_w8a8_float32_formula():
     t_codes = (t / t_scale).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8)
     codes, scale = quant.per_token(x, "fp8")
     assert np.array_equal(codes, t_codes.numpy()) and np.array_equal(scale, t_scale.numpy())
+    # Fixed by the formula itself: each row's largest-magnitude element lands on ±448 (0x7E / 0xFE), and
+    # nothing saturates past it.
+    top = np.abs(x).argmax(-1)
+    rows = np.arange(x.shape[0])
+    expect = np.where(x[rows, top] > 0, 0x7E, 0xFE)
+    assert np.array_equal(codes[rows, top], expect)
+    assert np.all((codes & 0x7F) <= 0x7E)
