@@ -9,20 +9,25 @@
 // Work decomposition (stream-K): a segment is one (sequence, KV head, row group) and owns ceil(len / CHUNK)
 // chunks; segments are laid end to end (sequence-major) and the launched workgroups split that line into
 // equal contiguous ranges, so ragged batches and long contexts balance to within one chunk. Each
-// workgroup computes the chunk counts' prefix sum itself (lengths stay on the device), walks its range
-// segment by segment ("pieces"), and its waves take the piece's chunks round-robin with the next chunk's
-// 16-byte loads in flight while the current one is computed. A segment covered by one workgroup is written
-// directly; otherwise every workgroup writes its piece's normalized output and log2-sum-exp to a
-// workspace slot, bumps the segment's arrival counter, and the last arriver combines all pieces and
-// resets the counter to zero (no waiting on other workgroups anywhere).
+// workgroup computes the chunk counts' prefix sum itself and keeps it, with the lengths, in LDS (lengths
+// stay on the device), then walks its range segment by segment ("pieces"). The waves of a workgroup take
+// a piece's chunks round-robin; each chunk's block-table entries are read while the previous chunk is
+// computed. The next piece's q rows and first chunk are requested before the current piece's waves are
+// merged, so the merge overlaps their latency. A segment covered by one workgroup is written directly;
+// otherwise every workgroup writes its piece's normalized output and log2-sum-exp to a workspace slot as
+// soon as the piece is done, bumps the segment's arrival counter, and the last arriver combines all
+// pieces and resets the counter to zero (no waiting on other workgroups anywhere).
 //
 // Wave layout (D = 128, one-byte codes): lane = slot * 8 + part. `part` owns channels [16 part, 16 part + 16)
 // and loads them with one 16-byte load per token row; one load instruction covers 8 token rows. Scores are
 // summed over the 8 lanes of a slot with DPP. BF16 pools use 16 lanes per row (8 channels each).
 //
-// Scales fold out of the inner loop: a per-head K scale and sm_scale * log2(e) go into q once, a per-head V
-// scale multiplies the final output, per-token scales multiply the reduced score (K) and the softmax weight
-// (V). Softmax runs in base 2; the workspace lse is in log2 units.
+// Compute: FP8 and BF16 keys are dotted with q held as bf16 pairs (v_dot2_f32_bf16; FP8 codes convert to
+// bf16 exactly); FP8 values are decoded to f16 two tokens at a time and accumulated with v_dot2_f32_f16
+// over token pairs; INT8 uses f32 FMAs. Scales fold out of the inner loop: a per-head K scale and
+// sm_scale * log2(e) multiply the reduced score, a per-head V scale multiplies the final output, per-token
+// scales multiply the reduced score (K) and the softmax weight (V). Softmax runs in base 2 with a lazily
+// moved reference point; the workspace lse is in log2 units.
 #include "bpt_device.h"
 #include "bpt_internal.h"
 
@@ -477,6 +482,62 @@ __device__ __forceinline__ void load_q_rows(const DecodeParams& p, QRows<KV, RG,
   }
 }
 
+// Count this workgroup's arrival at segment `seg` (its partial is stored and complete); the last of its n
+// pieces (workspace slots seg + first ...) to arrive combines them, as reference.merge_partials does (base
+// 2), writes the rows and resets the counter. Called by the whole workgroup; s_flag is one LDS int.
+template <int RG, int NT>
+__device__ __forceinline__ void arrive_and_combine(const DecodeParams& p, int seg, int b, int hr, int64_t first, int n,
+                                                   int rows, int tid, int* s_flag) {
+  constexpr int D = kHeadDim;
+  if (tid == 0) {
+    const unsigned prev = __hip_atomic_fetch_add(p.counters + seg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *s_flag = prev == (unsigned)n - 1u;
+  }
+  __syncthreads();
+  if (!*s_flag) return;
+  ws_acquire();
+  const int hh = hr / p.n_rg;
+  const int rg = hr - hh * p.n_rg;
+  for (int idx = tid; idx < RG * D; idx += NT) {
+    const int r = idx / D;
+    const int ch = idx - r * D;
+    const int gr = rg * RG + r;
+    if (gr >= rows) continue;
+    const float* lse = p.ws_lse + ((int64_t)seg + first) * RG + r;
+    const float* prt = p.ws_out + (((int64_t)seg + first) * RG + r) * D + ch;
+    float M = kNegInf, W = 0.0f, O = 0.0f;  // running maximum, weight and weighted output
+    for (int j0 = 0; j0 < n; j0 += 8) {
+      float lv[8], ov[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const bool in = j0 + j < n;
+        lv[j] = in ? ws_load(lse + (int64_t)(j0 + j) * RG) : kNegInf;
+        ov[j] = in ? ws_load(prt + (int64_t)(j0 + j) * RG * D) : 0.0f;
+      }
+      float bm = lv[0];
+#pragma unroll
+      for (int j = 1; j < 8; ++j) bm = fmaxf(bm, lv[j]);
+      const float nm = fmaxf(M, bm);
+      const float mu = nm == kNegInf ? 0.0f : nm;
+      const float alpha = W > 0.0f ? fast_exp2(M - mu) : 0.0f;
+      W *= alpha;
+      O *= alpha;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float e = fast_exp2(lv[j] - mu);  // 0 for empty pieces (lse -inf)
+        W += e;
+        O = fmaf(e, ov[j], O);
+      }
+      M = nm;
+    }
+    const int qi = gr / p.G;
+    const int hq = hh * p.G + (gr - qi * p.G);
+    store_float(p.out, (int64_t)b * p.o_sb + (int64_t)qi * p.o_sq + (int64_t)hq * p.o_sh + ch, p.out_dtype,
+                W > 0.0f ? O / W : 0.0f);
+  }
+  if (tid == 0) __hip_atomic_store(p.counters + seg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int KV, int SK, int RG, bool PU, bool QS>
 __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeParams p) {
   constexpr int NW = kDecodeWaves;
@@ -487,7 +548,9 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
   constexpr int CL = decode_loads(RG);
   constexpr int CH = CL * KvTraits<KV>::kRowsPerLoad;
 
-  extern __shared__ int s_prefix[];  // [B + 1] chunks per sequence, exclusive prefix sum
+  extern __shared__ int s_dyn[];  // [B + 1] chunks per sequence (exclusive prefix sum), then [B] lengths
+  int* s_prefix = s_dyn;
+  int* s_len = s_dyn + p.B + 1;
   __shared__ int s_wsum[NW];
   __shared__ int s_last;
   __shared__ float s_m[NW][RG];
@@ -499,7 +562,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
   const int wave = sread(tid >> 6);
   const int B = p.B;
 
-  // ---- chunks per sequence and their exclusive prefix sum (the segment line), in LDS ----------------
+  // ---- lengths, chunks per sequence and their exclusive prefix sum (the segment line), in LDS ----------
   {
     const int per_thread = (B + NT - 1) / NT;
     const int lo = min(tid * per_thread, B);
@@ -508,6 +571,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
     for (int b = lo; b < hi; ++b) {
       int len = p.lens[b];
       len = len < 0 ? 0 : (len > p.len_cap ? p.len_cap : len);
+      s_len[b] = len;
       sum += (len + CH - 1) / CH;
     }
     int x = sum;
@@ -523,9 +587,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
     run += x - sum;
     for (int b = lo; b < hi; ++b) {
       s_prefix[b] = run;
-      int len = p.lens[b];
-      len = len < 0 ? 0 : (len > p.len_cap ? p.len_cap : len);
-      run += (len + CH - 1) / CH;
+      run += (s_len[b] + CH - 1) / CH;
     }
     if (tid == 0) {
       int total = 0;
@@ -556,9 +618,10 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
   if (C == 0) return;
   const int64_t per = p.per_forced > 0 ? p.per_forced : (C + gridDim.x - 1) / gridDim.x;
   const int64_t g = blockIdx.x;
-  int64_t c = g * per;
-  if (c >= C) return;
-  const int64_t c_end = min(c + per, C);
+  const int64_t c_begin = g * per;
+  if (c_begin >= C) return;
+  const int64_t c_end = min(c_begin + per, C);
+  int64_t c = c_begin;
 
   int b;
   {
@@ -581,20 +644,32 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
   const int part = lane - slot * LPR;
   const int rows = p.Q * p.G;
 
-  // ---- pieces: the parts of segments inside [c, c_end) ------------------------------------------------
+  // The first piece's q rows and first chunk are requested before the loop; every later piece's are
+  // requested while the previous piece's waves are merged, so that merge overlaps their latency.
+  QRows<KV, RG, QS> q;
+  int rlen[RG];
+  ChunkRegs<CL> cr;
+  ChunkPages<CL> gp;
+  int len = sread(s_len[b]);
+  {
+    const int h = hr / p.n_rg;
+    load_q_rows<KV, RG, QS>(p, q, rlen, b, h, hr - h * p.n_rg, rows, part, len,
+                            SK == kScaleHead ? load_uniform(p.ks + h) : 1.0f);
+    const int k_end = k + (int)(min(c_end, (int64_t)HR * s_prefix[b] + (int64_t)hr * nb + nb) - c);
+    if (k + wave < k_end) {
+      fetch_pages<KV, CL, PU>(p, b, k + wave, len, slot, gp);
+      issue_chunk<KV, SK, CL, PU>(p, gp, h, k + wave, len, slot, part, cr);
+    }
+  }
+
+  // ---- pieces: the parts of segments inside [c_begin, c_end) -------------------------------------------
   for (;;) {
     const int64_t seg_c0 = (int64_t)HR * s_prefix[b] + (int64_t)hr * nb;
     const int64_t pe = min(c_end, seg_c0 + nb);
     const int k_end = k + (int)(pe - c);
     const int h = hr / p.n_rg;
     const int rg = hr - h * p.n_rg;
-    int len = load_uniform(p.lens + b);
-    len = len < 0 ? 0 : (len > p.len_cap ? p.len_cap : len);
 
-    QRows<KV, RG, QS> q;
-    int rlen[RG];
-    load_q_rows<KV, RG, QS>(p, q, rlen, b, h, rg, rows, part, len,
-                            SK == kScaleHead ? load_uniform(p.ks + h) : 1.0f);
     float m[RG], l[RG], acc[RG][VEC];
 #pragma unroll
     for (int r = 0; r < RG; ++r) {
@@ -604,28 +679,48 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
       for (int v = 0; v < VEC; ++v) acc[r][v] = 0.0f;
     }
 
-    // Chunks k + wave, k + wave + NW, ... of this piece. A chunk's pages are fetched while the previous
-    // chunk is computed; its K/V loads are issued before that.
-    {
-      ChunkRegs<CL> cr;
-      ChunkPages<CL> gp;
-      int kk = k + wave;
-      if (kk < k_end) fetch_pages<KV, CL, PU>(p, b, kk, len, slot, gp);
-      while (kk < k_end) {
-        issue_chunk<KV, SK, CL, PU>(p, gp, h, kk, len, slot, part, cr);
-        const int kn = kk + NW;
-        if (kn < k_end) fetch_pages<KV, CL, PU>(p, b, kn, len, slot, gp);
-        compute_chunk<KV, SK, RG, CL, QS>(cr, kk, slot, q, rlen, m, l, acc);
-        kk = kn;
+    // Chunks k + wave, k + wave + NW, ... of this piece; chunk kk's loads are in flight on entry to its
+    // iteration, the next chunk's pages are fetched while it is computed, then its loads are issued.
+    for (int kk = k + wave; kk < k_end;) {
+      const int kn = kk + NW;
+      if (kn < k_end) fetch_pages<KV, CL, PU>(p, b, kn, len, slot, gp);
+      compute_chunk<KV, SK, RG, CL, QS>(cr, kk, slot, q, rlen, m, l, acc);
+      if (kn < k_end) issue_chunk<KV, SK, CL, PU>(p, gp, h, kn, len, slot, part, cr);
+      kk = kn;
+    }
+
+    // The next piece (if any): its q rows and this wave's first chunk go in flight now.
+    const int b_cur = b, hr_cur = hr, nb_cur = nb;
+    const int64_t c_next = pe;
+    if (c_next < c_end) {
+      ++hr;
+      k = 0;
+      if (hr == HR) {
+        hr = 0;
+        do {
+          ++b;
+        } while (s_prefix[b + 1] == s_prefix[b]);
+        b = sread(b);
+        nb = sread(s_prefix[b + 1] - s_prefix[b]);
+      }
+      len = sread(s_len[b]);
+      const int hn = hr / p.n_rg;
+      load_q_rows<KV, RG, QS>(p, q, rlen, b, hn, hr - hn * p.n_rg, rows, part, len,
+                              SK == kScaleHead ? load_uniform(p.ks + hn) : 1.0f);
+      const int kn_end = (int)min((int64_t)nb, c_end - c_next);
+      if (wave < kn_end) {
+        fetch_pages<KV, CL, PU>(p, b, wave, len, slot, gp);
+        issue_chunk<KV, SK, CL, PU>(p, gp, hn, wave, len, slot, part, cr);
       }
     }
+
     close_state<KV, RG>(m, l, acc, slot, part, &s_m[wave][0], &s_l[wave][0], &s_acc[wave][0][0]);
     __syncthreads();
 
     // ---- merge the waves; write the segment's output, or this piece's partial ---------------------
-    const int seg = b * HR + hr;
+    const int seg = b_cur * HR + hr_cur;
     const int64_t g_first = seg_c0 / per;
-    const int64_t g_last = (seg_c0 + nb - 1) / per;
+    const int64_t g_last = (seg_c0 + nb_cur - 1) / per;
     const bool whole = g_first == g_last;
     const int64_t wslot = (int64_t)seg + g;
     const float vscale_head = SK == kScaleHead ? load_uniform(p.vs + h) : 1.0f;
@@ -650,82 +745,30 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
       if (whole) {
         const int qi = gr / p.G;
         const int hq = h * p.G + (gr - qi * p.G);
-        store_float(p.out, (int64_t)b * p.o_sb + (int64_t)qi * p.o_sq + (int64_t)hq * p.o_sh + ch, p.out_dtype, o);
+        store_float(p.out, (int64_t)b_cur * p.o_sb + (int64_t)qi * p.o_sq + (int64_t)hq * p.o_sh + ch, p.out_dtype,
+                    o);
       } else {
         ws_store(p.ws_out + (wslot * RG + r) * D + ch, o);
         if (ch == 0) ws_store(p.ws_lse + wslot * RG + r, L > 0.0f ? M - kBias + __log2f(L) : kNegInf);
       }
     }
-
     if (!whole) {
-      // Publish this piece, then count it. Partials travel as device-coherent accesses, so the only
-      // ordering needed is that this workgroup's stores have completed before its arrival is counted.
+      // Publish the piece now: partials travel as device-coherent accesses, so the only ordering needed is
+      // that this workgroup's stores have completed before its arrival is counted.
       ws_publish();
       __syncthreads();
-      if (tid == 0) {
-        const unsigned npieces = (unsigned)(g_last - g_first + 1);
-        const unsigned prev = __hip_atomic_fetch_add(p.counters + seg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = prev == npieces - 1;
-      }
-      __syncthreads();
-      if (s_last) {  // every piece has arrived: combine them (reference.merge_partials), reset the counter
-        ws_acquire();
-        const int npieces = (int)(g_last - g_first + 1);
-        for (int idx = tid; idx < RG * D; idx += NT) {
-          const int r = idx / D;
-          const int ch = idx - r * D;
-          const int gr = rg * RG + r;
-          if (gr >= rows) continue;
-          const float* lse = p.ws_lse + ((int64_t)seg + g_first) * RG + r;
-          const float* prt = p.ws_out + (((int64_t)seg + g_first) * RG + r) * D + ch;
-          float M = kNegInf;
-          for (int j = 0; j < npieces; ++j) M = fmaxf(M, ws_load(lse + (int64_t)j * RG));
-          const float mu = M == kNegInf ? 0.0f : M;
-          float W = 0.0f, O = 0.0f;
-          for (int j0 = 0; j0 < npieces; j0 += 8) {
-            float lv[8], ov[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              const bool in = j0 + j < npieces;
-              lv[j] = in ? ws_load(lse + (int64_t)(j0 + j) * RG) : kNegInf;
-              ov[j] = in ? ws_load(prt + (int64_t)(j0 + j) * RG * D) : 0.0f;
-            }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              const float e = fast_exp2(lv[j] - mu);
-              W += e;
-              O = fmaf(e, ov[j], O);
-            }
-          }
-          const int qi = gr / p.G;
-          const int hq = h * p.G + (gr - qi * p.G);
-          store_float(p.out, (int64_t)b * p.o_sb + (int64_t)qi * p.o_sq + (int64_t)hq * p.o_sh + ch, p.out_dtype,
-                      W > 0.0f ? O / W : 0.0f);
-        }
-        if (tid == 0) __hip_atomic_store(p.counters + seg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
+      arrive_and_combine<RG, NT>(p, seg, b_cur, hr_cur, g_first, (int)(g_last - g_first + 1), rows, tid, &s_last);
     }
+    if (c_next >= c_end) break;
+    c = c_next;
     __syncthreads();  // the LDS merge buffers are rewritten by the next piece
-
-    c = pe;
-    if (c >= c_end) break;
-    ++hr;
-    k = 0;
-    if (hr == HR) {
-      hr = 0;
-      do {
-        ++b;
-      } while (s_prefix[b + 1] == s_prefix[b]);
-      b = sread(b);
-      nb = sread(s_prefix[b + 1] - s_prefix[b]);
-    }
   }
 }
 
 template <int KV, int SK, int RG>
 static hipError_t launch_t(const DecodeParams& p, bool page_uniform, hipStream_t stream) {
   dim3 grid(p.grid), block(kDecodeWaves * 64);
-  const size_t lds = (size_t)(p.B + 1) * sizeof(int);  // the chunk-count prefix sum
+  const size_t lds = (size_t)(2 * p.B + 1) * sizeof(int);  // the chunk-count prefix sum and the lengths
   // A non-bf16 q needs the hi + lo split on the dot-product paths; the INT8 path reads q as floats.
   const bool qs = KV != kKvInt8 && p.q_dtype != kFBf16;
   if (page_uniform && !qs)
