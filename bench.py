@@ -257,7 +257,10 @@ def main() -> int:
     log(f"read probe: {read_gbps:.0f} GB/s")
     from bpt_amd import decode_plan
 
+    from bpt_amd import decode_kernel_name
+
     groups, chunk_tokens, _, _ = decode_plan(*pargs, **kw)
+    kernel = decode_kernel_name(*pargs, **kw)
     traffic = profiled_traffic(args.workload)
     result = {
         "metric": METRIC,
@@ -270,7 +273,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp8_e4m3 codes; bf16/f16 dot2 with f32 accumulation",
+        "dtype": "fp8_e4m3 codes; bf16 (QK) and f16 (PV) MFMA with f32 accumulation",
         "data": "synthetic",
         "config": {
             "workload": args.workload,
@@ -296,7 +299,7 @@ def main() -> int:
         "wall_s_timed_region": round(wall, 4),
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode_kernel",
+            "kernel": kernel,
             "achieved": round(value, 1),
             "peak": PEAK_GBPS,
             "unit": "GB/s",

@@ -46,6 +46,7 @@ class DecodeArgs(ctypes.Structure):
         ("num_splits", _i32),
         ("chunk_tokens", _i32),
         ("grid_groups", _i32),
+        ("rows_per_group", _i32),
         ("sm_scale", ctypes.c_float),
         ("q", _vp),
         ("q_stride_b", _i64),
@@ -126,7 +127,7 @@ SIGNATURES = {
     "bpt_copy_probe": (_i32, [_vp, _vp, ctypes.c_uint64, _vp]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class BptError(RuntimeError):

@@ -133,10 +133,7 @@ def _decode_args(
     return a, (b, nq, hq, d)
 
 
-def decode_plan(
-    q, k_cache, v_cache, block_table, context_lens, k_scale=None, v_scale=None, *, scale, max_context, num_splits=None
-) -> tuple[int, int, int]:
-    """(workgroups, tokens per wave chunk, workspace bytes) the call would use. Host only: no GPU needed."""
+def _plan(q, k_cache, v_cache, block_table, context_lens, k_scale, v_scale, scale, max_context, num_splits):
     q4 = q if q.dim() == 4 else q[:, None]
     a, _ = _decode_args(
         q4, k_cache, v_cache, block_table, context_lens, k_scale, v_scale, scale, max_context, num_splits,
@@ -144,7 +141,25 @@ def decode_plan(
     )
     ws, cnt = ctypes.c_size_t(0), ctypes.c_size_t(0)
     _lib.check(_lib.lib().bpt_decode_plan(ctypes.byref(a), ctypes.byref(ws), ctypes.byref(cnt)))
-    return a.grid_groups, a.chunk_tokens, ws.value, cnt.value
+    return a, ws.value, cnt.value
+
+
+def decode_plan(
+    q, k_cache, v_cache, block_table, context_lens, k_scale=None, v_scale=None, *, scale, max_context, num_splits=None
+) -> tuple[int, int, int, int]:
+    """(workgroups, tokens per chunk, workspace bytes, counter bytes) the call would use. Host only."""
+    a, ws, cnt = _plan(q, k_cache, v_cache, block_table, context_lens, k_scale, v_scale, scale, max_context,
+                       num_splits)
+    return a.grid_groups, a.chunk_tokens, ws, cnt
+
+
+def decode_kernel_name(
+    q, k_cache, v_cache, block_table, context_lens, k_scale=None, v_scale=None, *, scale, max_context, num_splits=None
+) -> str:
+    """The kernel the call launches: "decode_mfma_kernel" (matrix cores) or "decode_kernel" (vector)."""
+    a, _, _ = _plan(q, k_cache, v_cache, block_table, context_lens, k_scale, v_scale, scale, max_context,
+                    num_splits)
+    return "decode_mfma_kernel" if a.rows_per_group == 16 else "decode_kernel"
 
 
 # Per (device, stream): one partials workspace and one zero-filled counter buffer. The kernel leaves the

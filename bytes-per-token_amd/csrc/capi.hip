@@ -43,6 +43,7 @@ bool aligned_to(const void* p, int64_t stride_b, int64_t stride_q, int64_t strid
 }
 
 struct Plan {
+  bool mfma;  // the matrix-core kernel (all rows of a KV head in one 16-row group)
   int rows, rows_per_group, n_rg, HR, chunk, grid, len_cap;
   int64_t per_forced;
   size_t ws_out_floats, ws_lse_floats, workspace, counters;
@@ -84,12 +85,15 @@ int make_plan(const bpt_decode_args* a, Plan* pl) {
 
   const int G = a->num_q_heads / a->num_kv_heads;
   pl->rows = a->num_queries * G;
-  pl->rows_per_group = pl->rows <= 1 ? 1 : (pl->rows <= 2 ? 2 : 4);
+  // FP8 heads with 2..16 rows go to the matrix-core kernel, which reads every page once for up to 16 rows
+  // (the vector kernel reads it once per group of at most 4) and shares its per-token work among them.
+  pl->mfma = a->kv_dtype == BPT_KV_FP8_E4M3FN && pl->rows >= bpt::kMfmaMinRows && pl->rows <= bpt::kMfmaRows;
+  pl->rows_per_group = pl->mfma ? bpt::kMfmaRows : (pl->rows <= 1 ? 1 : (pl->rows <= 2 ? 2 : 4));
   pl->n_rg = (pl->rows + pl->rows_per_group - 1) / pl->rows_per_group;
   const int64_t hr = (int64_t)a->num_kv_heads * pl->n_rg;
   if (hr > (1 << 20)) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: too many KV heads x row groups", fn);
   pl->HR = (int)hr;
-  pl->chunk = bpt::decode_chunk_tokens(a->kv_dtype, pl->rows_per_group);
+  pl->chunk = pl->mfma ? bpt::kMfmaChunk : bpt::decode_chunk_tokens(a->kv_dtype, pl->rows_per_group);
   const int64_t table_cap = (int64_t)a->max_blocks_per_seq * a->page_size;
   pl->len_cap = (int)(a->max_context < table_cap ? a->max_context : table_cap);
   const int64_t max_nb = (pl->len_cap + pl->chunk - 1) / pl->chunk;
@@ -130,6 +134,7 @@ int bpt_decode_plan(bpt_decode_args* args, size_t* workspace_bytes, size_t* coun
   if (rc) return rc;
   args->chunk_tokens = pl.chunk;
   args->grid_groups = pl.grid;
+  args->rows_per_group = pl.rows_per_group;
   if (workspace_bytes) *workspace_bytes = pl.workspace;
   if (counters_bytes) *counters_bytes = pl.counters;
   return BPT_OK;
@@ -201,7 +206,8 @@ int bpt_paged_decode(const bpt_decode_args* a, void* stream) {
   p.q_dtype = a->q_dtype;
   p.out_dtype = a->out_dtype;
   p.table_i64 = a->table_dtype == BPT_IDX_I64;
-  hipError_t e = bpt::launch_decode(p, a->kv_dtype, a->scale_kind, pl.rows_per_group, (hipStream_t)stream);
+  hipError_t e = pl.mfma ? bpt::launch_decode_mfma(p, a->scale_kind, (hipStream_t)stream)
+                         : bpt::launch_decode(p, a->kv_dtype, a->scale_kind, pl.rows_per_group, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(fn, e);
   return BPT_OK;
 }

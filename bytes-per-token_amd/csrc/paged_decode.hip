@@ -28,8 +28,7 @@
 // sm_scale * log2(e) multiply the reduced score, a per-head V scale multiplies the final output, per-token
 // scales multiply the reduced score (K) and the softmax weight (V). Softmax runs in base 2 with a lazily
 // moved reference point; the workspace lse is in log2 units.
-#include "bpt_device.h"
-#include "bpt_internal.h"
+#include "decode_common.h"
 
 namespace bpt {
 
@@ -76,61 +75,6 @@ template <int CL>
 struct ChunkPages {
   int e[CL];
 };
-
-__device__ __forceinline__ int sread(int x) { return __builtin_amdgcn_readfirstlane(x); }
-
-// Cross-workgroup exchange of split-K partials. Workgroups run on different XCDs, whose L2 caches are
-// not coherent with each other. BPT_WS_COHERENT (default): partials are stored and loaded as
-// device-scope relaxed atomics, which gfx950 performs coherently (sc1) without whole-cache maintenance,
-// and publishing only waits for this wave's stores to complete. Otherwise: plain accesses bracketed by
-// device-scope fences (an L2 writeback on the writer, an L2 invalidate on the reader).
-#ifndef BPT_WS_COHERENT
-#define BPT_WS_COHERENT 1
-#endif
-
-__device__ __forceinline__ void ws_store(float* ptr, float v) {
-#if BPT_WS_COHERENT
-  __hip_atomic_store(ptr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#else
-  *ptr = v;
-#endif
-}
-
-__device__ __forceinline__ float ws_load(const float* ptr) {
-#if BPT_WS_COHERENT
-  return __hip_atomic_load(ptr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#else
-  return *ptr;
-#endif
-}
-
-__device__ __forceinline__ void ws_publish() {
-#if BPT_WS_COHERENT
-  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-#else
-  __threadfence();
-#endif
-}
-
-__device__ __forceinline__ void ws_acquire() {
-#if BPT_WS_COHERENT
-  __asm__ volatile("" ::: "memory");
-#else
-  __threadfence();
-#endif
-}
-
-// A load the whole wave makes from one address, through the scalar cache (the data is read-only here).
-template <typename T>
-__device__ __forceinline__ T load_uniform(const T* ptr) {
-  return *(const __attribute__((address_space(4))) T*)ptr;
-}
-
-// Block-table entry `idx` of row `row`: int32 tables directly, int64 tables by their low word (page ids
-// are below 2^31; anything else is clamped into the pool by the caller).
-__device__ __forceinline__ int64_t table_word(const DecodeParams& p, int b, int idx) {
-  return ((int64_t)b * p.table_sb + idx) << p.table_i64;
-}
 
 // Physical pages of chunk kk's loads. PU: a page holds whole load rows (page_size >= rows per load), so each
 // load's page is wave-uniform and read with a scalar load; otherwise every lane reads its own row's page.
@@ -198,19 +142,6 @@ __device__ __forceinline__ void issue_chunk(const DecodeParams& p, const ChunkPa
   }
 }
 
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-
-// Softmax weights are 2^(score - m + kBias) with the reference point m kept within kSlack of the largest
-// score seen (log2 units): weights stay below 2^12, well inside f16, and small ones keep f16 precision.
-constexpr float kBias = 4.0f;
-constexpr float kSlack = 8.0f;
-
-// Round-to-nearest-even float -> bf16 pair.
-__device__ __forceinline__ bf16x2 pack_bf16(float a, float b) {
-  return bf16x2{(__bf16)a, (__bf16)b};
-}
-
 // The query rows of a piece in the form the score path consumes. Dot-product paths (FP8, BF16 caches)
 // keep q unscaled as bf16 pairs: exact for a bf16 q; for an f16 / f32 q (QS) a second pair holds the
 // rounding remainder, so hi + lo carries 16 significant bits. The INT8 path keeps floats pre-scaled.
@@ -223,47 +154,6 @@ struct QRows {
   float f[RG][kDot ? 1 : VEC];
   float scale;  // applied to each reduced score
 };
-
-// This lane's VEC query channels of row (b, qi, hq), loaded as 16-byte vectors (unscaled floats).
-template <int VEC>
-__device__ __forceinline__ void load_q(const DecodeParams& p, int64_t base, float cs, float* q) {
-  const uint8_t* src = (const uint8_t*)p.q;
-  if (p.q_dtype == kFF32) {
-    const U4* v = (const U4*)(src + base * 4);
-    U4 raw[VEC / 4];
-#pragma unroll
-    for (int j = 0; j < VEC / 4; ++j) raw[j] = v[j];
-#pragma unroll
-    for (int j = 0; j < VEC / 4; ++j) {
-      q[4 * j] = __uint_as_float(raw[j].x) * cs;
-      q[4 * j + 1] = __uint_as_float(raw[j].y) * cs;
-      q[4 * j + 2] = __uint_as_float(raw[j].z) * cs;
-      q[4 * j + 3] = __uint_as_float(raw[j].w) * cs;
-    }
-  } else {
-    const U4* v = (const U4*)(src + base * 2);
-    U4 raw[VEC / 8];
-#pragma unroll
-    for (int j = 0; j < VEC / 8; ++j) raw[j] = v[j];
-#pragma unroll
-    for (int j = 0; j < VEC / 8; ++j) {
-      const uint32_t w[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float lo, hi;
-        if (p.q_dtype == kFBf16) {
-          lo = __uint_as_float(w[e] << 16);
-          hi = __uint_as_float(w[e] & 0xffff0000u);
-        } else {
-          lo = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[e] & 0xffffu));
-          hi = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[e] >> 16));
-        }
-        q[8 * j + 2 * e] = lo * cs;
-        q[8 * j + 2 * e + 1] = hi * cs;
-      }
-    }
-  }
-}
 
 // Fold chunk kk into this lane's online-softmax state.
 template <int KV, int SK, int RG, int CL, bool QS>
@@ -482,62 +372,6 @@ __device__ __forceinline__ void load_q_rows(const DecodeParams& p, QRows<KV, RG,
   }
 }
 
-// Count this workgroup's arrival at segment `seg` (its partial is stored and complete); the last of its n
-// pieces (workspace slots seg + first ...) to arrive combines them, as reference.merge_partials does (base
-// 2), writes the rows and resets the counter. Called by the whole workgroup; s_flag is one LDS int.
-template <int RG, int NT>
-__device__ __forceinline__ void arrive_and_combine(const DecodeParams& p, int seg, int b, int hr, int64_t first, int n,
-                                                   int rows, int tid, int* s_flag) {
-  constexpr int D = kHeadDim;
-  if (tid == 0) {
-    const unsigned prev = __hip_atomic_fetch_add(p.counters + seg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *s_flag = prev == (unsigned)n - 1u;
-  }
-  __syncthreads();
-  if (!*s_flag) return;
-  ws_acquire();
-  const int hh = hr / p.n_rg;
-  const int rg = hr - hh * p.n_rg;
-  for (int idx = tid; idx < RG * D; idx += NT) {
-    const int r = idx / D;
-    const int ch = idx - r * D;
-    const int gr = rg * RG + r;
-    if (gr >= rows) continue;
-    const float* lse = p.ws_lse + ((int64_t)seg + first) * RG + r;
-    const float* prt = p.ws_out + (((int64_t)seg + first) * RG + r) * D + ch;
-    float M = kNegInf, W = 0.0f, O = 0.0f;  // running maximum, weight and weighted output
-    for (int j0 = 0; j0 < n; j0 += 8) {
-      float lv[8], ov[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const bool in = j0 + j < n;
-        lv[j] = in ? ws_load(lse + (int64_t)(j0 + j) * RG) : kNegInf;
-        ov[j] = in ? ws_load(prt + (int64_t)(j0 + j) * RG * D) : 0.0f;
-      }
-      float bm = lv[0];
-#pragma unroll
-      for (int j = 1; j < 8; ++j) bm = fmaxf(bm, lv[j]);
-      const float nm = fmaxf(M, bm);
-      const float mu = nm == kNegInf ? 0.0f : nm;
-      const float alpha = W > 0.0f ? fast_exp2(M - mu) : 0.0f;
-      W *= alpha;
-      O *= alpha;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float e = fast_exp2(lv[j] - mu);  // 0 for empty pieces (lse -inf)
-        W += e;
-        O = fmaf(e, ov[j], O);
-      }
-      M = nm;
-    }
-    const int qi = gr / p.G;
-    const int hq = hh * p.G + (gr - qi * p.G);
-    store_float(p.out, (int64_t)b * p.o_sb + (int64_t)qi * p.o_sq + (int64_t)hq * p.o_sh + ch, p.out_dtype,
-                W > 0.0f ? O / W : 0.0f);
-  }
-  if (tid == 0) __hip_atomic_store(p.counters + seg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 template <int KV, int SK, int RG, bool PU, bool QS>
 __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeParams p) {
   constexpr int NW = kDecodeWaves;
@@ -562,55 +396,8 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
   const int wave = sread(tid >> 6);
   const int B = p.B;
 
-  // ---- lengths, chunks per sequence and their exclusive prefix sum (the segment line), in LDS ----------
-  {
-    const int per_thread = (B + NT - 1) / NT;
-    const int lo = min(tid * per_thread, B);
-    const int hi = min(lo + per_thread, B);
-    int sum = 0;
-    for (int b = lo; b < hi; ++b) {
-      int len = p.lens[b];
-      len = len < 0 ? 0 : (len > p.len_cap ? p.len_cap : len);
-      s_len[b] = len;
-      sum += (len + CH - 1) / CH;
-    }
-    int x = sum;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int y = __shfl_up(x, off, 64);
-      if (lane >= off) x += y;
-    }
-    if (lane == 63) s_wsum[tid >> 6] = x;
-    __syncthreads();
-    int run = 0;
-    for (int w = 0; w < (tid >> 6); ++w) run += s_wsum[w];
-    run += x - sum;
-    for (int b = lo; b < hi; ++b) {
-      s_prefix[b] = run;
-      run += (s_len[b] + CH - 1) / CH;
-    }
-    if (tid == 0) {
-      int total = 0;
-      for (int w = 0; w < NW; ++w) total += s_wsum[w];
-      s_prefix[B] = total;
-    }
-    __syncthreads();
-  }
-
-  // ---- sequences with no tokens get zero output ---------------------------------------------------
-  {
-    const int row_elems = p.Q * p.Hq * D;
-    for (int b = blockIdx.x; b < B; b += gridDim.x) {
-      if (s_prefix[b + 1] != s_prefix[b]) continue;
-      for (int i = tid; i < row_elems; i += NT) {
-        const int ch = i % D;
-        const int hq = (i / D) % p.Hq;
-        const int qi = i / (D * p.Hq);
-        store_float(p.out, (int64_t)b * p.o_sb + (int64_t)qi * p.o_sq + (int64_t)hq * p.o_sh + ch, p.out_dtype,
-                    0.0f);
-      }
-    }
-  }
+  build_segment_line<NW, CH>(p, s_prefix, s_len, s_wsum);
+  zero_empty_sequences<NT>(p, s_prefix);
 
   // ---- this workgroup's range of chunks -----------------------------------------------------------
   const int HR = p.HR;

@@ -1,0 +1,404 @@
+// Paged decode attention on the matrix cores, for KV heads that serve 5..16 query rows per sequence (the
+// speculative-verify case: Q queries x G query heads), over an FP8 (e4m3fn) KV cache.
+//
+// Follows fastserve kernels/kv_attention.py:56-175 (G heads of one KV head per program, online softmax,
+// split-K) with engine/attention.py:12-20's causal rule for several queries, like the vector kernel; the
+// work decomposition, workspace exchange and combine are the vector kernel's (decode_common.h). What
+// differs is the chunk math: all rows of a segment go through the matrix cores together, so every page is
+// read once for all of them.
+//
+// One chunk = 32 tokens = two 16-token tiles; rows are padded to 16 (the MFMA N dimension). With
+// l = lane, n = l % 16 (this lane's row), kq = l / 16:
+//  * scores S^T = K Q^T with v_mfma_f32_16x16x32_bf16, four K-steps of 32 channels per tile. A = K rows
+//    (lane: token 16 t + n, channels 32 kq + 8 s .. + 7 at step s: 32 contiguous bytes per lane, FP8
+//    decoded to bf16 exactly); B = Q^T (lane: row n, the same channels, from registers). The result
+//    gives lane l the scores of row n for tokens 16 t + 4 kq + i (i < 4), t = 0, 1: eight per lane.
+//  * online softmax per row over those eight values; the row's four lanes agree on the maximum through
+//    two shuffles and keep partial weight sums that are added at the end.
+//  * output O^T += V^T P^T with v_mfma_f32_16x16x32_f16: the contraction index k = 8 kq + j is mapped to
+//    the lane's own score tokens (j < 4: 4 kq + j, j >= 4: 16 + 4 kq + j - 4), so P^T comes straight
+//    from this lane's weights (f16). V^T needs tokens contiguous per lane: the lane loads channels
+//    8 n' .. 8 n' + 7 (n' = l % 16) of its eight tokens (8 bytes each), transposes 4 x 4 byte blocks with
+//    v_perm and decodes FP8 -> f16 exactly; M-tile mu holds channels 8 n' + mu. The accumulator then
+//    gives lane l row n, channels 32 kq + 8 i + mu (i < 4, mu < 8): 32 contiguous channels.
+// Scales: sm_scale * log2(e) and a per-head K scale multiply the scores, per-token K / V scales the scores
+// and weights, a per-head V scale the output. Softmax is in base 2 with the same lazy reference point as
+// the vector kernel.
+#include "decode_common.h"
+
+namespace bpt {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kMRows = 16;   // rows per segment, padded: the MFMA N dimension
+constexpr int kMChunk = 32;  // tokens per chunk: two 16-token tiles
+
+// This lane's share of one chunk: K for its token of each tile, V for its eight score tokens.
+struct MChunk {
+  U4 k[2][2];          // tile t: token 16 t + n, channels 32 kq .. 32 kq + 31
+  u32x2 v[2][4];       // tile t, token 4 kq + i: channels 8 n .. 8 n + 7
+  float ks[8], vs[8];  // per-token scales of tokens 16 t + 4 kq + i (index 4 t + i)
+};
+
+__device__ __forceinline__ u32x2 load8(const uint8_t* p) { return __builtin_nontemporal_load((const u32x2*)p); }
+
+__device__ __forceinline__ int clamp_page(const DecodeParams& p, int e) {
+  return e < 0 ? 0 : (e >= p.num_blocks ? p.num_blocks - 1 : e);
+}
+
+// Issue chunk kk's loads. Tokens at or past len read the sequence's last token instead (valid memory, never
+// weighted). PU: a 16-token tile lies inside one page (page_size >= 16), whose id is read once per tile
+// with a scalar load; otherwise every token looks up its own page.
+template <int SK, bool PU>
+__device__ __forceinline__ void mfma_issue(const DecodeParams& p, int b, int h, int kk, int len, int lane, MChunk& c) {
+  const int T0 = kk * kMChunk;
+  const int kq = lane >> 4, n = lane & 15;
+  const int64_t head_off = (int64_t)h * p.kv_shead;
+  const int32_t* table = (const int32_t*)p.table;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    int e_tile = 0;
+    if constexpr (PU) e_tile = clamp_page(p, load_uniform(table + table_word(p, b, min(T0 + 16 * t, len - 1) >> p.logP)));
+    {
+      const int tok = min(T0 + 16 * t + n, len - 1);
+      const int e = PU ? e_tile : clamp_page(p, table[table_word(p, b, tok >> p.logP)]);
+      const int64_t off = (int64_t)e * p.kv_sblk + (int64_t)(tok & (p.P - 1)) * p.kv_stok + head_off + 32 * kq;
+      c.k[t][0] = load16(p.k + off);
+      c.k[t][1] = load16(p.k + off + 16);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tok = min(T0 + 16 * t + 4 * kq + i, len - 1);
+      const int e = PU ? e_tile : clamp_page(p, table[table_word(p, b, tok >> p.logP)]);
+      const int64_t row = (int64_t)e * p.kv_sblk + (int64_t)(tok & (p.P - 1)) * p.kv_stok;
+      c.v[t][i] = load8(p.v + row + head_off + 8 * n);
+      if constexpr (SK == kScaleTokenHead) {
+        const int64_t so = (int64_t)e * p.sc_sblk + (int64_t)(tok & (p.P - 1)) * p.sc_stok + (int64_t)h * p.sc_shead;
+        c.ks[4 * t + i] = p.ks[so];
+        c.vs[4 * t + i] = p.vs[so];
+      } else {
+        c.ks[4 * t + i] = 1.0f;
+        c.vs[4 * t + i] = 1.0f;
+      }
+    }
+  }
+}
+
+// 4 x 4 byte transpose: w[i] byte j -> out[j] byte i.
+__device__ __forceinline__ void transpose4(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, uint32_t (&o)[4]) {
+  const uint32_t t0 = __builtin_amdgcn_perm(w1, w0, 0x05010400u);  // w0.0 w1.0 w0.1 w1.1
+  const uint32_t t1 = __builtin_amdgcn_perm(w3, w2, 0x05010400u);  // w2.0 w3.0 w2.1 w3.1
+  const uint32_t t2 = __builtin_amdgcn_perm(w1, w0, 0x07030602u);  // w0.2 w1.2 w0.3 w1.3
+  const uint32_t t3 = __builtin_amdgcn_perm(w3, w2, 0x07030602u);  // w2.2 w3.2 w2.3 w3.3
+  o[0] = __builtin_amdgcn_perm(t1, t0, 0x05040100u);
+  o[1] = __builtin_amdgcn_perm(t1, t0, 0x07060302u);
+  o[2] = __builtin_amdgcn_perm(t3, t2, 0x05040100u);
+  o[3] = __builtin_amdgcn_perm(t3, t2, 0x07060302u);
+}
+
+__device__ __forceinline__ bf16x8 fp8x8_to_bf16(uint32_t w0, uint32_t w1) {
+  typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+  const bf16x2v a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false);
+  const bf16x2v b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true);
+  const bf16x2v c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false);
+  const bf16x2v d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true);
+  return bf16x8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+}
+
+__device__ __forceinline__ f16x8 fp8x8_to_f16(uint32_t w0, uint32_t w1) {
+  typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
+  const f16x2v a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, false);
+  const f16x2v b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, true);
+  const f16x2v c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, false);
+  const f16x2v d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, true);
+  return f16x8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+}
+
+// Fold chunk kk into this lane's state: m (row n's reference point, shared by the row's four lanes),
+// l (this lane's partial weight sum) and o[mu] (row n, channels 32 kq + 8 i + mu).
+template <int SK, bool QS>
+__device__ __forceinline__ void mfma_compute(const MChunk& c, int kk, int lane, const bf16x8 (&qb)[QS ? 8 : 4],
+                                             float qscale, int rlen, float& m, float& l, f32x4 (&o)[8]) {
+  const int T0 = kk * kMChunk;
+  const int kq = lane >> 4;
+  float sc[8];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    f32x4 st = {0.0f, 0.0f, 0.0f, 0.0f};
+    const uint32_t w[8] = {c.k[t][0].x, c.k[t][0].y, c.k[t][0].z, c.k[t][0].w,
+                           c.k[t][1].x, c.k[t][1].y, c.k[t][1].z, c.k[t][1].w};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const bf16x8 a = fp8x8_to_bf16(w[2 * s], w[2 * s + 1]);
+      st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qb[s], st, 0, 0, 0);
+      if constexpr (QS) st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qb[4 + s], st, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tok = T0 + 16 * t + 4 * kq + i;
+      float x = st[i] * qscale;
+      if constexpr (SK == kScaleTokenHead) x *= c.ks[4 * t + i];
+      sc[4 * t + i] = tok < rlen ? x : kNegInf;
+    }
+  }
+
+  // ---- online softmax of row n over this chunk's 32 tokens (8 here, 24 on the row's other lanes) -------
+  float mx = sc[0];
+#pragma unroll
+  for (int j = 1; j < 8; ++j) mx = fmaxf(mx, sc[j]);
+  mx = fmaxf(mx, shfl_xor_f(mx, 16));
+  mx = fmaxf(mx, shfl_xor_f(mx, 32));
+  const bool move = mx > m + kSlack;
+  if (__any(move)) {
+    const float mn = move ? mx : m;
+    const float alpha = move ? fast_exp2(m - mn) : 1.0f;  // 0 when m was -inf
+    l *= alpha;
+#pragma unroll
+    for (int mu = 0; mu < 8; ++mu) o[mu] *= alpha;
+    m = mn;
+  }
+  const float base = (m == kNegInf ? 0.0f : m) - kBias;
+  f16x8 pb;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float e = fast_exp2(sc[j] - base);
+    l += e;
+    pb[j] = (_Float16)(e * c.vs[j]);
+  }
+
+  // ---- O^T += V^T P^T: eight M-tiles of 16 channels (tile mu: channels 8 n' + mu) -------------------------
+  uint32_t lo[2][4], hi[2][4];  // [tile][j]: channel 8 n' + j (lo) or 8 n' + 4 + j (hi), bytes = tokens i
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    transpose4(c.v[t][0].x, c.v[t][1].x, c.v[t][2].x, c.v[t][3].x, lo[t]);
+    transpose4(c.v[t][0].y, c.v[t][1].y, c.v[t][2].y, c.v[t][3].y, hi[t]);
+  }
+#pragma unroll
+  for (int mu = 0; mu < 8; ++mu) {
+    const uint32_t d0 = mu < 4 ? lo[0][mu & 3] : hi[0][mu & 3];
+    const uint32_t d1 = mu < 4 ? lo[1][mu & 3] : hi[1][mu & 3];
+    o[mu] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp8x8_to_f16(d0, d1), pb, o[mu], 0, 0, 0);
+  }
+}
+
+// Row n's q (channels 32 kq .. 32 kq + 31) as MFMA B operands for the four K-steps; an f16 / f32 q (QS) also
+// gets the bf16 rounding remainder (steps 4 .. 7). Rows past `rows` are zero and see no tokens.
+template <bool QS>
+__device__ __forceinline__ void mfma_load_q(const DecodeParams& p, int b, int h, int rows, int len, int lane,
+                                            bf16x8 (&qb)[QS ? 8 : 4], int& rlen) {
+  const int kq = lane >> 4, n = lane & 15;
+  const bool in = n < rows;
+  const int qi = in ? n / p.G : 0;
+  const int hq = in ? h * p.G + (n - qi * p.G) : 0;
+  rlen = in ? len - (p.Q - 1 - qi) : 0;
+  const int64_t base = (int64_t)b * p.q_sb + (int64_t)qi * p.q_sq + (int64_t)hq * p.q_sh + 32 * kq;
+  if constexpr (!QS) {
+    const U4* src = (const U4*)((const uint16_t*)p.q + base);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const U4 w = src[s];
+      const U4 z = in ? w : U4{0, 0, 0, 0};
+      qb[s] = __builtin_bit_cast(bf16x8, z);
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      float f[8];
+      load_q<8>(p, base + 8 * s, 1.0f, f);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float x = in ? f[j] : 0.0f;
+        const __bf16 hbits = (__bf16)x;
+        qb[s][j] = hbits;
+        qb[4 + s][j] = (__bf16)(x - (float)hbits);
+      }
+    }
+  }
+}
+
+template <int SK, bool PU, bool QS>
+__global__ __launch_bounds__(kDecodeWaves * 64) void decode_mfma_kernel(const DecodeParams p) {
+  constexpr int NW = kDecodeWaves;
+  constexpr int NT = NW * 64;
+  constexpr int D = kHeadDim;
+  constexpr int RG = kMRows;
+
+  extern __shared__ int s_dyn[];  // [B + 1] chunks per sequence (exclusive prefix sum), then [B] lengths
+  int* s_prefix = s_dyn;
+  int* s_len = s_dyn + p.B + 1;
+  __shared__ int s_wsum[NW];
+  __shared__ int s_last;
+  __shared__ float s_m[NW][RG];
+  __shared__ float s_l[NW][RG];
+  __shared__ float s_o[NW][RG][D];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = sread(tid >> 6);
+  const int kq = lane >> 4, n = lane & 15;
+  const int B = p.B;
+
+  build_segment_line<NW, kMChunk>(p, s_prefix, s_len, s_wsum);
+  zero_empty_sequences<NT>(p, s_prefix);
+
+  // ---- this workgroup's range of chunks (segments are (sequence, KV head): HR = Hkv) ---------------------
+  const int HR = p.HR;
+  const int64_t C = (int64_t)HR * s_prefix[B];
+  if (C == 0) return;
+  const int64_t per = p.per_forced > 0 ? p.per_forced : (C + gridDim.x - 1) / gridDim.x;
+  const int64_t g = blockIdx.x;
+  const int64_t c_begin = g * per;
+  if (c_begin >= C) return;
+  const int64_t c_end = min(c_begin + per, C);
+  int64_t c = c_begin;
+
+  int b;
+  {
+    int lo = 0, hi = B - 1;  // largest b with HR * prefix[b] <= c
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if ((int64_t)HR * s_prefix[mid] <= c) lo = mid; else hi = mid - 1;
+    }
+    b = sread(lo);
+  }
+  int nb = sread(s_prefix[b + 1] - s_prefix[b]);
+  int h, k;
+  {
+    const int64_t r = c - (int64_t)HR * s_prefix[b];
+    h = sread((int)(r / nb));
+    k = sread((int)(r - (int64_t)h * nb));
+  }
+  const int rows = p.Q * p.G;
+
+  // The first piece's q rows and first chunk are requested before the loop; every later piece's while the
+  // previous piece's waves are merged.
+  bf16x8 qb[QS ? 8 : 4];
+  int rlen;
+  MChunk cr;
+  int len = sread(s_len[b]);
+  float qscale = p.qscale * (SK == kScaleHead ? load_uniform(p.ks + h) : 1.0f);
+  mfma_load_q<QS>(p, b, h, rows, len, lane, qb, rlen);
+  {
+    const int k_end = k + (int)(min(c_end, (int64_t)HR * s_prefix[b] + (int64_t)h * nb + nb) - c);
+    if (k + wave < k_end) mfma_issue<SK, PU>(p, b, h, k + wave, len, lane, cr);
+  }
+
+  for (;;) {
+    const int64_t seg_c0 = (int64_t)HR * s_prefix[b] + (int64_t)h * nb;
+    const int64_t pe = min(c_end, seg_c0 + nb);
+    const int k_end = k + (int)(pe - c);
+
+    float m = kNegInf, l = 0.0f;
+    f32x4 o[8];
+#pragma unroll
+    for (int mu = 0; mu < 8; ++mu) o[mu] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (int kk = k + wave; kk < k_end;) {
+      const int kn = kk + NW;
+      mfma_compute<SK, QS>(cr, kk, lane, qb, qscale, rlen, m, l, o);
+      if (kn < k_end) mfma_issue<SK, PU>(p, b, h, kn, len, lane, cr);
+      kk = kn;
+    }
+
+    // The next piece (if any): its q rows and this wave's first chunk go in flight now.
+    const int b_cur = b, h_cur = h, nb_cur = nb;
+    const int64_t c_next = pe;
+    if (c_next < c_end) {
+      ++h;
+      k = 0;
+      if (h == HR) {
+        h = 0;
+        do {
+          ++b;
+        } while (s_prefix[b + 1] == s_prefix[b]);
+        b = sread(b);
+        nb = sread(s_prefix[b + 1] - s_prefix[b]);
+      }
+      len = sread(s_len[b]);
+      qscale = p.qscale * (SK == kScaleHead ? load_uniform(p.ks + h) : 1.0f);
+      mfma_load_q<QS>(p, b, h, rows, len, lane, qb, rlen);
+      if (wave < (int)min((int64_t)nb, c_end - c_next)) mfma_issue<SK, PU>(p, b, h, wave, len, lane, cr);
+    }
+
+    // This wave's state of row n: the four lanes' weight sums added, stored for the workgroup merge.
+    l += shfl_xor_f(l, 16);
+    l += shfl_xor_f(l, 32);
+    if (kq == 0) {
+      s_m[wave][n] = m;
+      s_l[wave][n] = l;
+    }
+#pragma unroll
+    for (int mu = 0; mu < 8; ++mu) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s_o[wave][n][32 * kq + 8 * i + mu] = o[mu][i];
+    }
+    __syncthreads();
+
+    // ---- merge the waves; write the segment's output, or this piece's partial ---------------------
+    const int seg = b_cur * HR + h_cur;
+    const int64_t g_first = seg_c0 / per;
+    const int64_t g_last = (seg_c0 + nb_cur - 1) / per;
+    const bool whole = g_first == g_last;
+    const int64_t wslot = (int64_t)seg + g;
+    const float vscale_head = SK == kScaleHead ? load_uniform(p.vs + h_cur) : 1.0f;
+    for (int idx = tid; idx < RG * D; idx += NT) {
+      const int r = idx / D;
+      const int ch = idx - r * D;
+      if (r >= rows) continue;
+      float M = kNegInf;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) M = fmaxf(M, s_m[w][r]);
+      const float mu = M == kNegInf ? 0.0f : M;
+      float L = 0.0f, A = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const float lw = s_l[w][r];
+        const float e = lw > 0.0f ? fast_exp2(s_m[w][r] - mu) : 0.0f;
+        L += lw * e;
+        A += lw > 0.0f ? s_o[w][r][ch] * e : 0.0f;
+      }
+      const float out = L > 0.0f ? A / L * vscale_head : 0.0f;
+      if (whole) {
+        const int qi = r / p.G;
+        const int hq = h_cur * p.G + (r - qi * p.G);
+        store_float(p.out, (int64_t)b_cur * p.o_sb + (int64_t)qi * p.o_sq + (int64_t)hq * p.o_sh + ch, p.out_dtype,
+                    out);
+      } else {
+        ws_store(p.ws_out + (wslot * RG + r) * D + ch, out);
+        if (ch == 0) ws_store(p.ws_lse + wslot * RG + r, L > 0.0f ? M - kBias + __log2f(L) : kNegInf);
+      }
+    }
+    if (!whole) {
+      ws_publish();
+      __syncthreads();
+      arrive_and_combine<RG, NT>(p, seg, b_cur, h_cur, g_first, (int)(g_last - g_first + 1), rows, tid, &s_last);
+    }
+    if (c_next >= c_end) break;
+    c = c_next;
+    __syncthreads();  // the LDS merge buffers are rewritten by the next piece
+  }
+}
+
+template <int SK>
+static hipError_t launch_mfma_sk(const DecodeParams& p, bool pu, bool qs, hipStream_t stream) {
+  dim3 grid(p.grid), block(kDecodeWaves * 64);
+  const size_t lds = (size_t)(2 * p.B + 1) * sizeof(int);
+  if (pu && !qs) hipLaunchKernelGGL((decode_mfma_kernel<SK, true, false>), grid, block, lds, stream, p);
+  else if (pu) hipLaunchKernelGGL((decode_mfma_kernel<SK, true, true>), grid, block, lds, stream, p);
+  else if (!qs) hipLaunchKernelGGL((decode_mfma_kernel<SK, false, false>), grid, block, lds, stream, p);
+  else hipLaunchKernelGGL((decode_mfma_kernel<SK, false, true>), grid, block, lds, stream, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_decode_mfma(const DecodeParams& p, int scale_kind, hipStream_t stream) {
+  const bool pu = p.P >= 16;
+  const bool qs = p.q_dtype != kFBf16;
+  if (scale_kind == kScaleHead) return launch_mfma_sk<kScaleHead>(p, pu, qs, stream);
+  if (scale_kind == kScaleTokenHead) return launch_mfma_sk<kScaleTokenHead>(p, pu, qs, stream);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace bpt

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define BPT_ABI_VERSION 1
+#define BPT_ABI_VERSION 2
 
 /* return codes */
 #define BPT_OK 0
@@ -98,6 +98,8 @@ typedef struct {
   int32_t num_splits;   /* in: 0 = balance automatically, S > 0 = S partitions of a max_context sequence */
   int32_t chunk_tokens; /* out of bpt_decode_plan: tokens one wave streams per step */
   int32_t grid_groups;  /* out of bpt_decode_plan: workgroups launched */
+  int32_t rows_per_group; /* out of bpt_decode_plan: query rows computed together per KV head; 16 = the
+                             matrix-core kernel (FP8 caches, 2..16 rows), 1/2/4 = the vector kernel */
   float sm_scale;
 
   const void* q;

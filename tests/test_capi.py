@@ -57,20 +57,21 @@ def expected_counters(batch, segments_per_seq):
 
 
 def test_plan_honours_requested_splits(built_lib):
-    # 32/8 heads: 4 rows per KV head, 32-token chunks; 32768 tokens in 32 partitions of 32 chunks each.
+    # 32/8 heads: 4 rows per KV head (one 16-row matrix-core group), 32-token chunks; 32768 tokens in 32
+    # partitions of 32 chunks each.
     q, k, v, table, lens, ks, vs = cpu_case(b=4, hq=32, max_blocks=2048, nb=8192)
     grid, chunk, ws, cnt = decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=32768, num_splits=32)
     assert chunk == 32 and grid == 4 * 8 * 32
-    assert ws == expected_workspace(4, 8, 4, grid) and cnt == expected_counters(4, 8)
+    assert ws == expected_workspace(4, 8, 16, grid) and cnt == expected_counters(4, 8)
 
 
 def test_plan_auto_launches_two_groups_per_cu_at_most(built_lib):
     q, k, v, table, lens, ks, vs = cpu_case("fp8", b=32, max_blocks=256, nb=8192)
     grid, chunk, ws, cnt = decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=4096)
-    assert chunk % 8 == 0 and grid == 512 and ws == expected_workspace(32, 8, 2, 512) and cnt == expected_counters(32, 8)
+    assert chunk == 32 and grid == 512 and ws == expected_workspace(32, 8, 16, 512) and cnt == expected_counters(32, 8)
     qb, kb, vb, tb, lb, _, _ = cpu_case("bf16", b=1)
     grid, chunk_bf16, _, _ = decode_plan(qb, kb, vb, tb, lb, None, None, scale=0.1, max_context=64)
-    assert chunk_bf16 == chunk // 2  # 16 lanes per bf16 row, 8 per one-byte row: half the rows per load
+    assert chunk_bf16 == 16  # vector kernel: 4 loads of 4 rows (16 lanes per bf16 row)
     assert grid == 8 * -(-64 // chunk_bf16)  # never more groups than chunks that could exist
 
 
@@ -80,7 +81,21 @@ def test_plan_workspace_grows_with_the_launch(built_lib, max_context):
     grid, chunk, ws, cnt = decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=max_context)
     bound = 32 * 8 * -(-min(max_context, 4096 * 16) // chunk)
     assert 1 <= grid <= max(min(512, bound), 1)
-    assert ws == expected_workspace(32, 8, 2, grid) and cnt == expected_counters(32, 8)
+    assert ws == expected_workspace(32, 8, 16, grid) and cnt == expected_counters(32, 8)
+
+
+def test_plan_puts_2_to_16_fp8_rows_in_one_matrix_core_group(built_lib):
+    # 5 queries x 2 heads per KV head = 10 rows: one 16-row group per KV head, 32-token chunks.
+    q, k, v, table, lens, ks, vs = cpu_case("fp8", b=16, nq=5, max_blocks=256, nb=8192)
+    grid, chunk, ws, cnt = decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=3072)
+    assert chunk == 32 and ws == expected_workspace(16, 8, 16, grid) and cnt == expected_counters(16, 8)
+    # INT8 keeps the vector kernel: 3 groups of 4 rows per KV head; so does FP8 with one row per KV head.
+    q, k, v, table, lens, ks, vs = cpu_case("int8", b=16, nq=5, max_blocks=256, nb=8192)
+    grid, chunk, ws, cnt = decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=3072)
+    assert ws == expected_workspace(16, 24, 4, grid) and cnt == expected_counters(16, 24)
+    q, k, v, table, lens, ks, vs = cpu_case("fp8", b=16, hq=8, max_blocks=256, nb=8192)
+    grid, chunk, ws, cnt = decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=3072)
+    assert ws == expected_workspace(16, 8, 1, grid)
 
 
 def test_plan_rejects_oversized_batches(built_lib):

@@ -6,7 +6,8 @@ Covers what fastserve's kernel tests cover (tests/kernels/test_kernels_gpu.py:78
 forced split counts from one split to one chunk per split, and the maximum context; plus what the paged,
 quantized path adds: FP8 / INT8 / BF16 pools, per-head and per-token scales, int32 and int64 block tables,
 head-major pools through strides, several causal queries per sequence, and all five measured shapes at full
-size.
+size. FP8 heads with 2..16 rows take the matrix-core kernel, the others the vector kernel; both are covered
+(FP8 with one row per KV head, BF16 and INT8 exercise the vector kernel).
 """
 
 import numpy as np
@@ -260,3 +261,25 @@ def test_repeated_calls_are_deterministic():
     a = paged_decode_attention(*w.args(), **w.kwargs())
     b = paged_decode_attention(*w.args(), **w.kwargs())
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("scales", ["head", "token"])
+@pytest.mark.parametrize("nq,hq,hkv", [(1, 16, 8), (5, 16, 8), (8, 16, 8), (1, 48, 8), (4, 32, 8), (3, 20, 4)])
+def test_matrix_core_path_rows_2_to_16(scales, nq, hq, hkv):
+    """FP8 heads serving 2..16 rows (Q queries x G heads) run on the matrix cores, all rows in one pass."""
+    c = make_case("fp8", [1030, 5, 64, 2000, 33], nq=nq, hq=hq, hkv=hkv, scales=scales)
+    got, want = run_case(c)
+    check(got, want, f"Q={nq} Hq={hq} Hkv={hkv} {scales}")
+    got, want = run_case(c, num_splits=5)
+    check(got, want, f"Q={nq} Hq={hq} Hkv={hkv} {scales}, 5 splits")
+
+
+@pytest.mark.parametrize("page", [1, 8, 16, 64])
+def test_matrix_core_path_page_sizes_and_q_dtypes(page):
+    """Pages smaller than a 16-token tile take the per-token page lookup; f16 / f32 q the hi + lo split."""
+    c = make_case("fp8", [100, 257, 31, 1], nq=5, page=page)
+    got, want = run_case(c)
+    check(got, want, f"page {page}")
+    for dt in (torch.float16, torch.float32):
+        got, want = run_case(c, q=c["q"].to(dt))
+        check(got, want, f"page {page}, q {dt}")
