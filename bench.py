@@ -31,14 +31,14 @@ PEAK_GBPS = 8000.0
 PROFILES = ROOT / "profiles"
 
 
-def profiled_traffic(workload: str) -> dict | None:
-    """HBM bytes per decode launch from the committed rocprofv3 counter summary of this workload, if any.
+def profiled_traffic(kernel: str, workload: str) -> dict | None:
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter summary of this workload, if any.
 
     The summary holds FETCH_SIZE and WRITE_SIZE per dispatch (two --pmc runs of `bench.py --profile`), each
     already scaled by what the counter reads for a copy kernel of known size, as a line
     `traffic_bytes_per_launch: N`.
     """
-    path = PROFILES / f"decode_kernel_{workload}.md"
+    path = PROFILES / f"{kernel}_{workload}.md"
     if not path.exists():
         return None
     import re
@@ -261,7 +261,7 @@ def main() -> int:
 
     groups, chunk_tokens, _, _ = decode_plan(*pargs, **kw)
     kernel = decode_kernel_name(*pargs, **kw)
-    traffic = profiled_traffic(args.workload)
+    traffic = profiled_traffic(kernel, args.workload)
     result = {
         "metric": METRIC,
         "value": round(value, 1),
