@@ -19,6 +19,9 @@
 #ifndef BPT_DECODE_MFMA_MIN_ROWS
 #define BPT_DECODE_MFMA_MIN_ROWS 2
 #endif
+#ifndef BPT_DECODE_MFMA_MIN_ROWS_INT8
+#define BPT_DECODE_MFMA_MIN_ROWS_INT8 5
+#endif
 
 namespace bpt {
 
@@ -35,10 +38,11 @@ constexpr int kDecodeGroupsPerCu = BPT_DECODE_GROUPS_PER_CU;
 // twice the registers.
 constexpr int decode_loads(int rows_per_group) { return rows_per_group >= 4 ? BPT_DECODE_LOADS_RG4 : BPT_DECODE_LOADS; }
 
-// Matrix-core decode (FP8 caches): KV heads with kMfmaMinRows .. kMfmaRows rows per sequence (Q * G) are
-// computed as one 16-row group in 32-token chunks (faster than the vector kernel from 2 rows up: its
-// per-token VALU work is shared by all rows).
+// Matrix-core decode: FP8 KV heads with kMfmaMinRows .. kMfmaRows rows per sequence (Q * G), INT8 ones with
+// kMfmaMinRowsInt8 .. kMfmaRows, are computed as one 16-row group in 32-token chunks (for FP8 faster than
+// the vector kernel from 2 rows up: its per-token VALU work is shared by all rows).
 constexpr int kMfmaMinRows = BPT_DECODE_MFMA_MIN_ROWS;
+constexpr int kMfmaMinRowsInt8 = BPT_DECODE_MFMA_MIN_ROWS_INT8;
 constexpr int kMfmaRows = 16;
 constexpr int kMfmaChunk = 32;
 
@@ -88,7 +92,7 @@ struct AppendParams {
 int decode_rows_per_load(int kv_dtype);
 int decode_chunk_tokens(int kv_dtype, int rows_per_group);
 hipError_t launch_decode(const DecodeParams& p, int kv_dtype, int scale_kind, int rows_per_group, hipStream_t stream);
-hipError_t launch_decode_mfma(const DecodeParams& p, int scale_kind, hipStream_t stream);
+hipError_t launch_decode_mfma(const DecodeParams& p, int kv_dtype, int scale_kind, hipStream_t stream);
 hipError_t launch_append(const AppendParams& p, int kv_dtype, int scale_kind, int head_dim, hipStream_t stream);
 hipError_t launch_fp8_table(float* out, hipStream_t stream);
 hipError_t launch_fp8_encode(const float* x, float scale, uint8_t* out, int64_t n, hipStream_t stream);

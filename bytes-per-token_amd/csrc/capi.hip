@@ -85,9 +85,11 @@ int make_plan(const bpt_decode_args* a, Plan* pl) {
 
   const int G = a->num_q_heads / a->num_kv_heads;
   pl->rows = a->num_queries * G;
-  // FP8 heads with 2..16 rows go to the matrix-core kernel, which reads every page once for up to 16 rows
-  // (the vector kernel reads it once per group of at most 4) and shares its per-token work among them.
-  pl->mfma = a->kv_dtype == BPT_KV_FP8_E4M3FN && pl->rows >= bpt::kMfmaMinRows && pl->rows <= bpt::kMfmaRows;
+  // The matrix-core kernel reads every page once for up to 16 rows (the vector kernel once per group of at
+  // most 4) and shares its per-token work among them: FP8 heads with 2..16 rows go there, INT8 heads only
+  // from 5 rows on (with fewer, the vector kernel reads each page once too and its INT8 decode is cheaper).
+  pl->mfma = pl->rows <= bpt::kMfmaRows && ((a->kv_dtype == BPT_KV_FP8_E4M3FN && pl->rows >= bpt::kMfmaMinRows) ||
+                                            (a->kv_dtype == BPT_KV_INT8 && pl->rows >= bpt::kMfmaMinRowsInt8));
   pl->rows_per_group = pl->mfma ? bpt::kMfmaRows : (pl->rows <= 1 ? 1 : (pl->rows <= 2 ? 2 : 4));
   pl->n_rg = (pl->rows + pl->rows_per_group - 1) / pl->rows_per_group;
   const int64_t hr = (int64_t)a->num_kv_heads * pl->n_rg;
@@ -206,7 +208,7 @@ int bpt_paged_decode(const bpt_decode_args* a, void* stream) {
   p.q_dtype = a->q_dtype;
   p.out_dtype = a->out_dtype;
   p.table_i64 = a->table_dtype == BPT_IDX_I64;
-  hipError_t e = pl.mfma ? bpt::launch_decode_mfma(p, a->scale_kind, (hipStream_t)stream)
+  hipError_t e = pl.mfma ? bpt::launch_decode_mfma(p, a->kv_dtype, a->scale_kind, (hipStream_t)stream)
                          : bpt::launch_decode(p, a->kv_dtype, a->scale_kind, pl.rows_per_group, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(fn, e);
   return BPT_OK;

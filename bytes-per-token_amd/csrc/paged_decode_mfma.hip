@@ -1,5 +1,5 @@
-// Paged decode attention on the matrix cores, for KV heads that serve 5..16 query rows per sequence (the
-// speculative-verify case: Q queries x G query heads), over an FP8 (e4m3fn) KV cache.
+// Paged decode attention on the matrix cores, for KV heads that serve 2..16 query rows per sequence (G query
+// heads x Q queries, up to the speculative-verify case), over an FP8 (e4m3fn) KV cache.
 //
 // Follows fastserve kernels/kv_attention.py:56-175 (G heads of one KV head per program, online softmax,
 // split-K) with engine/attention.py:12-20's causal rule for several queries, like the vector kernel; the
@@ -24,6 +24,8 @@
 // Scales: sm_scale * log2(e) and a per-head K scale multiply the scores, per-token K / V scales the scores
 // and weights, a per-head V scale the output. Softmax is in base 2 with the same lazy reference point as
 // the vector kernel.
+#include <type_traits>
+
 #include "decode_common.h"
 
 namespace bpt {
@@ -49,30 +51,43 @@ __device__ __forceinline__ int clamp_page(const DecodeParams& p, int e) {
   return e < 0 ? 0 : (e >= p.num_blocks ? p.num_blocks - 1 : e);
 }
 
-// Issue chunk kk's loads. Tokens at or past len read the sequence's last token instead (valid memory, never
-// weighted). PU: a 16-token tile lies inside one page (page_size >= 16), whose id is read once per tile
-// with a scalar load; otherwise every token looks up its own page.
-template <int SK, bool PU>
-__device__ __forceinline__ void mfma_issue(const DecodeParams& p, int b, int h, int kk, int len, int lane, MChunk& c) {
+// Issue chunk kk's K loads (mfma_issue_k) or V loads and per-token scales (mfma_issue_v). Tokens at or past
+// len read the sequence's last token instead (valid memory, never weighted). PU: a 16-token tile lies
+// inside one page (page_size >= 16), whose id is read once per tile with a scalar load; otherwise every
+// token looks up its own page.
+template <bool PU>
+__device__ __forceinline__ int mfma_page(const DecodeParams& p, int b, int tile_first, int tok, int len) {
+  const int32_t* table = (const int32_t*)p.table;
+  if constexpr (PU) return clamp_page(p, load_uniform(table + table_word(p, b, min(tile_first, len - 1) >> p.logP)));
+  return clamp_page(p, table[table_word(p, b, tok >> p.logP)]);
+}
+
+template <bool PU>
+__device__ __forceinline__ void mfma_issue_k(const DecodeParams& p, int b, int h, int kk, int len, int lane, MChunk& c) {
   const int T0 = kk * kMChunk;
   const int kq = lane >> 4, n = lane & 15;
   const int64_t head_off = (int64_t)h * p.kv_shead;
-  const int32_t* table = (const int32_t*)p.table;
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    int e_tile = 0;
-    if constexpr (PU) e_tile = clamp_page(p, load_uniform(table + table_word(p, b, min(T0 + 16 * t, len - 1) >> p.logP)));
-    {
-      const int tok = min(T0 + 16 * t + n, len - 1);
-      const int e = PU ? e_tile : clamp_page(p, table[table_word(p, b, tok >> p.logP)]);
-      const int64_t off = (int64_t)e * p.kv_sblk + (int64_t)(tok & (p.P - 1)) * p.kv_stok + head_off + 32 * kq;
-      c.k[t][0] = load16(p.k + off);
-      c.k[t][1] = load16(p.k + off + 16);
-    }
+    const int tok = min(T0 + 16 * t + n, len - 1);
+    const int e = mfma_page<PU>(p, b, T0 + 16 * t, tok, len);
+    const int64_t off = (int64_t)e * p.kv_sblk + (int64_t)(tok & (p.P - 1)) * p.kv_stok + head_off + 32 * kq;
+    c.k[t][0] = load16(p.k + off);
+    c.k[t][1] = load16(p.k + off + 16);
+  }
+}
+
+template <int SK, bool PU>
+__device__ __forceinline__ void mfma_issue_v(const DecodeParams& p, int b, int h, int kk, int len, int lane, MChunk& c) {
+  const int T0 = kk * kMChunk;
+  const int kq = lane >> 4, n = lane & 15;
+  const int64_t head_off = (int64_t)h * p.kv_shead;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int tok = min(T0 + 16 * t + 4 * kq + i, len - 1);
-      const int e = PU ? e_tile : clamp_page(p, table[table_word(p, b, tok >> p.logP)]);
+      const int e = mfma_page<PU>(p, b, T0 + 16 * t, tok, len);
       const int64_t row = (int64_t)e * p.kv_sblk + (int64_t)(tok & (p.P - 1)) * p.kv_stok;
       c.v[t][i] = load8(p.v + row + head_off + 8 * n);
       if constexpr (SK == kScaleTokenHead) {
@@ -85,6 +100,12 @@ __device__ __forceinline__ void mfma_issue(const DecodeParams& p, int b, int h, 
       }
     }
   }
+}
+
+template <int SK, bool PU>
+__device__ __forceinline__ void mfma_issue(const DecodeParams& p, int b, int h, int kk, int len, int lane, MChunk& c) {
+  mfma_issue_k<PU>(p, b, h, kk, len, lane, c);
+  mfma_issue_v<SK, PU>(p, b, h, kk, len, lane, c);
 }
 
 // 4 x 4 byte transpose: w[i] byte j -> out[j] byte i.
@@ -117,11 +138,37 @@ __device__ __forceinline__ f16x8 fp8x8_to_f16(uint32_t w0, uint32_t w1) {
   return f16x8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
 }
 
+// Eight int8 codes (bytes of w0 then w1) -> f16, exactly: the bits 0x6400 | (b ^ 0x80) are the f16 value
+// 1152 + b, from which 1152 is subtracted.
+__device__ __forceinline__ f16x8 int8x8_to_f16(uint32_t w0, uint32_t w1) {
+  typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
+  const f16x2v bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+  const f16x2v a = __builtin_bit_cast(f16x2v, __builtin_amdgcn_perm(0u, w0, 0x0c010c00u) ^ 0x64806480u) - bias;
+  const f16x2v b = __builtin_bit_cast(f16x2v, __builtin_amdgcn_perm(0u, w0, 0x0c030c02u) ^ 0x64806480u) - bias;
+  const f16x2v c = __builtin_bit_cast(f16x2v, __builtin_amdgcn_perm(0u, w1, 0x0c010c00u) ^ 0x64806480u) - bias;
+  const f16x2v d = __builtin_bit_cast(f16x2v, __builtin_amdgcn_perm(0u, w1, 0x0c030c02u) ^ 0x64806480u) - bias;
+  return f16x8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+}
+
+// The q operand of the score MFMAs: bf16 for FP8 codes (exact bf16 values), f16 for INT8 codes (exact f16
+// values); hi parts for the four K-steps, plus the rounding remainders (lo, QS) when q carries more bits
+// than that type: an f16 / f32 q on the bf16 path, an f32 q on the f16 path. (A bf16 q converts to f16
+// exactly in f16's normal range; below 2^-14 the dropped remainder is at most 2^-25.)
+template <int KV, bool QS>
+struct MQ {
+  static constexpr bool kF16 = KV == kKvInt8;
+  static constexpr int kOps = QS ? 8 : 4;
+  typedef typename std::conditional<kF16, f16x8, bf16x8>::type T;
+};
+
 // Fold chunk kk into this lane's state: m (row n's reference point, shared by the row's four lanes),
 // l (this lane's partial weight sum) and o[mu] (row n, channels 32 kq + 8 i + mu).
-template <int SK, bool QS>
-__device__ __forceinline__ void mfma_compute(const MChunk& c, int kk, int lane, const bf16x8 (&qb)[QS ? 8 : 4],
-                                             float qscale, int rlen, float& m, float& l, f32x4 (&o)[8]) {
+// `after_scores` runs once the chunk's K registers are consumed (the caller issues the next chunk's K loads
+// there, so they fly during this chunk's softmax and value products).
+template <int KV, int SK, bool QS, typename AfterScores>
+__device__ __forceinline__ void mfma_compute(MChunk& c, int kk, int lane, const typename MQ<KV, QS>::T (&qb)[MQ<KV, QS>::kOps],
+                                             float qscale, int rlen, float& m, float& l, f32x4 (&o)[8],
+                                             AfterScores after_scores) {
   const int T0 = kk * kMChunk;
   const int kq = lane >> 4;
   float sc[8];
@@ -132,9 +179,15 @@ __device__ __forceinline__ void mfma_compute(const MChunk& c, int kk, int lane, 
                            c.k[t][1].x, c.k[t][1].y, c.k[t][1].z, c.k[t][1].w};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const bf16x8 a = fp8x8_to_bf16(w[2 * s], w[2 * s + 1]);
-      st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qb[s], st, 0, 0, 0);
-      if constexpr (QS) st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qb[4 + s], st, 0, 0, 0);
+      if constexpr (MQ<KV, QS>::kF16) {
+        const f16x8 a = int8x8_to_f16(w[2 * s], w[2 * s + 1]);
+        st = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[s], st, 0, 0, 0);
+        if constexpr (QS) st = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[4 + s], st, 0, 0, 0);
+      } else {
+        const bf16x8 a = fp8x8_to_bf16(w[2 * s], w[2 * s + 1]);
+        st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qb[s], st, 0, 0, 0);
+        if constexpr (QS) st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qb[4 + s], st, 0, 0, 0);
+      }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -144,6 +197,7 @@ __device__ __forceinline__ void mfma_compute(const MChunk& c, int kk, int lane, 
       sc[4 * t + i] = tok < rlen ? x : kNegInf;
     }
   }
+  after_scores();
 
   // ---- online softmax of row n over this chunk's 32 tokens (8 here, 24 on the row's other lanes) -------
   float mx = sc[0];
@@ -180,28 +234,32 @@ __device__ __forceinline__ void mfma_compute(const MChunk& c, int kk, int lane, 
   for (int mu = 0; mu < 8; ++mu) {
     const uint32_t d0 = mu < 4 ? lo[0][mu & 3] : hi[0][mu & 3];
     const uint32_t d1 = mu < 4 ? lo[1][mu & 3] : hi[1][mu & 3];
-    o[mu] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp8x8_to_f16(d0, d1), pb, o[mu], 0, 0, 0);
+    const f16x8 a = KV == kKvInt8 ? int8x8_to_f16(d0, d1) : fp8x8_to_f16(d0, d1);
+    o[mu] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb, o[mu], 0, 0, 0);
   }
 }
 
 // Row n's q (channels 32 kq .. 32 kq + 31) as MFMA B operands for the four K-steps; an f16 / f32 q (QS) also
 // gets the bf16 rounding remainder (steps 4 .. 7). Rows past `rows` are zero and see no tokens.
-template <bool QS>
+template <int KV, bool QS>
 __device__ __forceinline__ void mfma_load_q(const DecodeParams& p, int b, int h, int rows, int len, int lane,
-                                            bf16x8 (&qb)[QS ? 8 : 4], int& rlen) {
+                                            typename MQ<KV, QS>::T (&qb)[MQ<KV, QS>::kOps], int& rlen) {
+  typedef typename MQ<KV, QS>::T T;
+  typedef typename std::remove_reference<decltype(qb[0][0])>::type E;
   const int kq = lane >> 4, n = lane & 15;
   const bool in = n < rows;
   const int qi = in ? n / p.G : 0;
   const int hq = in ? h * p.G + (n - qi * p.G) : 0;
   rlen = in ? len - (p.Q - 1 - qi) : 0;
   const int64_t base = (int64_t)b * p.q_sb + (int64_t)qi * p.q_sq + (int64_t)hq * p.q_sh + 32 * kq;
-  if constexpr (!QS) {
+  if constexpr (!QS && !MQ<KV, QS>::kF16) {
+    // bf16 q on the bf16 path: the words already are the operands.
     const U4* src = (const U4*)((const uint16_t*)p.q + base);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const U4 w = src[s];
       const U4 z = in ? w : U4{0, 0, 0, 0};
-      qb[s] = __builtin_bit_cast(bf16x8, z);
+      qb[s] = __builtin_bit_cast(T, z);
     }
   } else {
 #pragma unroll
@@ -211,15 +269,15 @@ __device__ __forceinline__ void mfma_load_q(const DecodeParams& p, int b, int h,
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float x = in ? f[j] : 0.0f;
-        const __bf16 hbits = (__bf16)x;
+        const E hbits = (E)x;
         qb[s][j] = hbits;
-        qb[4 + s][j] = (__bf16)(x - (float)hbits);
+        if constexpr (QS) qb[4 + s][j] = (E)(x - (float)hbits);
       }
     }
   }
 }
 
-template <int SK, bool PU, bool QS>
+template <int KV, int SK, bool PU, bool QS>
 __global__ __launch_bounds__(kDecodeWaves * 64) void decode_mfma_kernel(const DecodeParams p) {
   constexpr int NW = kDecodeWaves;
   constexpr int NT = NW * 64;
@@ -275,12 +333,12 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_mfma_kernel(const De
 
   // The first piece's q rows and first chunk are requested before the loop; every later piece's while the
   // previous piece's waves are merged.
-  bf16x8 qb[QS ? 8 : 4];
+  typename MQ<KV, QS>::T qb[MQ<KV, QS>::kOps];
   int rlen;
   MChunk cr;
   int len = sread(s_len[b]);
   float qscale = p.qscale * (SK == kScaleHead ? load_uniform(p.ks + h) : 1.0f);
-  mfma_load_q<QS>(p, b, h, rows, len, lane, qb, rlen);
+  mfma_load_q<KV, QS>(p, b, h, rows, len, lane, qb, rlen);
   {
     const int k_end = k + (int)(min(c_end, (int64_t)HR * s_prefix[b] + (int64_t)h * nb + nb) - c);
     if (k + wave < k_end) mfma_issue<SK, PU>(p, b, h, k + wave, len, lane, cr);
@@ -296,10 +354,14 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_mfma_kernel(const De
 #pragma unroll
     for (int mu = 0; mu < 8; ++mu) o[mu] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
+    // Chunks k + wave, k + wave + NW, ... of this piece: chunk kk is in flight on entry to its iteration;
+    // the next chunk's K loads are issued as soon as kk's scores are done, its V loads after kk's values.
     for (int kk = k + wave; kk < k_end;) {
       const int kn = kk + NW;
-      mfma_compute<SK, QS>(cr, kk, lane, qb, qscale, rlen, m, l, o);
-      if (kn < k_end) mfma_issue<SK, PU>(p, b, h, kn, len, lane, cr);
+      mfma_compute<KV, SK, QS>(cr, kk, lane, qb, qscale, rlen, m, l, o, [&]() {
+        if (kn < k_end) mfma_issue_k<PU>(p, b, h, kn, len, lane, cr);
+      });
+      if (kn < k_end) mfma_issue_v<SK, PU>(p, b, h, kn, len, lane, cr);
       kk = kn;
     }
 
@@ -319,7 +381,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_mfma_kernel(const De
       }
       len = sread(s_len[b]);
       qscale = p.qscale * (SK == kScaleHead ? load_uniform(p.ks + h) : 1.0f);
-      mfma_load_q<QS>(p, b, h, rows, len, lane, qb, rlen);
+      mfma_load_q<KV, QS>(p, b, h, rows, len, lane, qb, rlen);
       if (wave < (int)min((int64_t)nb, c_end - c_next)) mfma_issue<SK, PU>(p, b, h, wave, len, lane, cr);
     }
 
@@ -382,22 +444,27 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_mfma_kernel(const De
   }
 }
 
-template <int SK>
+template <int KV, int SK>
 static hipError_t launch_mfma_sk(const DecodeParams& p, bool pu, bool qs, hipStream_t stream) {
   dim3 grid(p.grid), block(kDecodeWaves * 64);
   const size_t lds = (size_t)(2 * p.B + 1) * sizeof(int);
-  if (pu && !qs) hipLaunchKernelGGL((decode_mfma_kernel<SK, true, false>), grid, block, lds, stream, p);
-  else if (pu) hipLaunchKernelGGL((decode_mfma_kernel<SK, true, true>), grid, block, lds, stream, p);
-  else if (!qs) hipLaunchKernelGGL((decode_mfma_kernel<SK, false, false>), grid, block, lds, stream, p);
-  else hipLaunchKernelGGL((decode_mfma_kernel<SK, false, true>), grid, block, lds, stream, p);
+  if (pu && !qs) hipLaunchKernelGGL((decode_mfma_kernel<KV, SK, true, false>), grid, block, lds, stream, p);
+  else if (pu) hipLaunchKernelGGL((decode_mfma_kernel<KV, SK, true, true>), grid, block, lds, stream, p);
+  else if (!qs) hipLaunchKernelGGL((decode_mfma_kernel<KV, SK, false, false>), grid, block, lds, stream, p);
+  else hipLaunchKernelGGL((decode_mfma_kernel<KV, SK, false, true>), grid, block, lds, stream, p);
   return hipGetLastError();
 }
 
-hipError_t launch_decode_mfma(const DecodeParams& p, int scale_kind, hipStream_t stream) {
+hipError_t launch_decode_mfma(const DecodeParams& p, int kv_dtype, int scale_kind, hipStream_t stream) {
   const bool pu = p.P >= 16;
-  const bool qs = p.q_dtype != kFBf16;
-  if (scale_kind == kScaleHead) return launch_mfma_sk<kScaleHead>(p, pu, qs, stream);
-  if (scale_kind == kScaleTokenHead) return launch_mfma_sk<kScaleTokenHead>(p, pu, qs, stream);
+  // q needs the hi + lo split when it carries more bits than the score MFMA's type.
+  const bool qs = kv_dtype == kKvInt8 ? p.q_dtype == kFF32 : p.q_dtype != kFBf16;
+  if (kv_dtype == kKvFp8 && scale_kind == kScaleHead) return launch_mfma_sk<kKvFp8, kScaleHead>(p, pu, qs, stream);
+  if (kv_dtype == kKvFp8 && scale_kind == kScaleTokenHead)
+    return launch_mfma_sk<kKvFp8, kScaleTokenHead>(p, pu, qs, stream);
+  if (kv_dtype == kKvInt8 && scale_kind == kScaleHead) return launch_mfma_sk<kKvInt8, kScaleHead>(p, pu, qs, stream);
+  if (kv_dtype == kKvInt8 && scale_kind == kScaleTokenHead)
+    return launch_mfma_sk<kKvInt8, kScaleTokenHead>(p, pu, qs, stream);
   return hipErrorInvalidValue;
 }
 

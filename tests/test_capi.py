@@ -84,18 +84,26 @@ def test_plan_workspace_grows_with_the_launch(built_lib, max_context):
     assert ws == expected_workspace(32, 8, 16, grid) and cnt == expected_counters(32, 8)
 
 
-def test_plan_puts_2_to_16_fp8_rows_in_one_matrix_core_group(built_lib):
+@pytest.mark.parametrize("fmt", ["fp8", "int8"])
+def test_plan_puts_2_to_16_quantized_rows_in_one_matrix_core_group(built_lib, fmt):
     # 5 queries x 2 heads per KV head = 10 rows: one 16-row group per KV head, 32-token chunks.
-    q, k, v, table, lens, ks, vs = cpu_case("fp8", b=16, nq=5, max_blocks=256, nb=8192)
+    q, k, v, table, lens, ks, vs = cpu_case(fmt, b=16, nq=5, max_blocks=256, nb=8192)
     grid, chunk, ws, cnt = decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=3072)
     assert chunk == 32 and ws == expected_workspace(16, 8, 16, grid) and cnt == expected_counters(16, 8)
-    # INT8 keeps the vector kernel: 3 groups of 4 rows per KV head; so does FP8 with one row per KV head.
-    q, k, v, table, lens, ks, vs = cpu_case("int8", b=16, nq=5, max_blocks=256, nb=8192)
-    grid, chunk, ws, cnt = decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=3072)
-    assert ws == expected_workspace(16, 24, 4, grid) and cnt == expected_counters(16, 24)
-    q, k, v, table, lens, ks, vs = cpu_case("fp8", b=16, hq=8, max_blocks=256, nb=8192)
+    # One row per KV head keeps the vector kernel; so do INT8 heads with 2..4 rows.
+    q, k, v, table, lens, ks, vs = cpu_case(fmt, b=16, hq=8, max_blocks=256, nb=8192)
     grid, chunk, ws, cnt = decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=3072)
     assert ws == expected_workspace(16, 8, 1, grid)
+    q, k, v, table, lens, ks, vs = cpu_case(fmt, b=16, max_blocks=256, nb=8192)
+    grid, chunk, ws, cnt = decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=3072)
+    assert ws == expected_workspace(16, 8, 16 if fmt == "fp8" else 2, grid)
+
+
+def test_plan_keeps_bf16_on_the_vector_kernel(built_lib):
+    # BF16: 3 groups of 4 rows per KV head for 10 rows.
+    q, k, v, table, lens, _, _ = cpu_case("bf16", b=16, nq=5, max_blocks=256, nb=8192)
+    grid, chunk, ws, cnt = decode_plan(q, k, v, table, lens, None, None, scale=0.1, max_context=3072)
+    assert ws == expected_workspace(16, 24, 4, grid) and cnt == expected_counters(16, 24)
 
 
 def test_plan_rejects_oversized_batches(built_lib):

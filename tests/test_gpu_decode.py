@@ -163,6 +163,16 @@ def test_page_sizes(page):
     check(got, want, f"page {page}")
 
 
+@pytest.mark.parametrize("fmt,scales", [("int8", "token"), ("int8", "head"), ("fp8", "head"), ("bf16", None)])
+def test_vector_path_one_row_per_kv_head(fmt, scales):
+    """Hq = Hkv: one row per KV head, the vector kernel for every format."""
+    c = make_case(fmt, [700, 3, 128, 2049], hq=8, hkv=8, scales=scales)
+    got, want = run_case(c)
+    check(got, want, f"{fmt} one row")
+    got, want = run_case(c, q=c["q"].float(), num_splits=4)
+    check(got, want, f"{fmt} one row, f32 q, 4 splits")
+
+
 def test_head_major_pool_int64_table_f32_out_and_q_dtypes():
     c = make_case("int8", [700, 3, 128], scales="token", head_major=True, table_dtype=torch.int64)
     got, want = run_case(c)
@@ -263,21 +273,23 @@ def test_repeated_calls_are_deterministic():
     assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("scales", ["head", "token"])
+@pytest.mark.parametrize("fmt,scales", [("fp8", "head"), ("fp8", "token"), ("int8", "token"), ("int8", "head")])
 @pytest.mark.parametrize("nq,hq,hkv", [(1, 16, 8), (5, 16, 8), (8, 16, 8), (1, 48, 8), (4, 32, 8), (3, 20, 4)])
-def test_matrix_core_path_rows_2_to_16(scales, nq, hq, hkv):
-    """FP8 heads serving 2..16 rows (Q queries x G heads) run on the matrix cores, all rows in one pass."""
-    c = make_case("fp8", [1030, 5, 64, 2000, 33], nq=nq, hq=hq, hkv=hkv, scales=scales)
+def test_matrix_core_path_rows_2_to_16(fmt, scales, nq, hq, hkv):
+    """FP8 heads serving 2..16 rows (Q queries x G heads) and INT8 heads serving 5..16 run on the matrix
+    cores, all rows at once (INT8 with 2..4 rows on the vector kernel)."""
+    c = make_case(fmt, [1030, 5, 64, 2000, 33], nq=nq, hq=hq, hkv=hkv, scales=scales)
     got, want = run_case(c)
     check(got, want, f"Q={nq} Hq={hq} Hkv={hkv} {scales}")
     got, want = run_case(c, num_splits=5)
     check(got, want, f"Q={nq} Hq={hq} Hkv={hkv} {scales}, 5 splits")
 
 
+@pytest.mark.parametrize("fmt,scales", [("fp8", "head"), ("int8", "token")])
 @pytest.mark.parametrize("page", [1, 8, 16, 64])
-def test_matrix_core_path_page_sizes_and_q_dtypes(page):
-    """Pages smaller than a 16-token tile take the per-token page lookup; f16 / f32 q the hi + lo split."""
-    c = make_case("fp8", [100, 257, 31, 1], nq=5, page=page)
+def test_matrix_core_path_page_sizes_and_q_dtypes(fmt, scales, page):
+    """Pages smaller than a 16-token tile take the per-token page lookup; wider q dtypes the hi + lo split."""
+    c = make_case(fmt, [100, 257, 31, 1], nq=5, page=page, scales=scales)
     got, want = run_case(c)
     check(got, want, f"page {page}")
     for dt in (torch.float16, torch.float32):
