@@ -6,6 +6,16 @@ with a thin PyTorch-ROCm host layer. Importing needs no GPU; the library loads o
 it has not been built.
 """
 
+from .kv_cache import OutOfBlocksError, PagedMeta, PagedQuantKVCache
 from .paged_attention import decode_kernel_name, decode_plan, kv_read_bytes, paged_decode_attention, quantize_append
 
-__all__ = ["decode_kernel_name", "decode_plan", "kv_read_bytes", "paged_decode_attention", "quantize_append"]
+__all__ = [
+    "OutOfBlocksError",
+    "PagedMeta",
+    "PagedQuantKVCache",
+    "decode_kernel_name",
+    "decode_plan",
+    "kv_read_bytes",
+    "paged_decode_attention",
+    "quantize_append",
+]

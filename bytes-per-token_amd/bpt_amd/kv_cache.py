@@ -1,0 +1,185 @@
+"""A paged KV cache that stores FP8 / INT8 / BF16 codes and attends over them with the HIP kernels.
+
+The drop-in for fastserve's engine (paths relative to its src/fastserve/):
+
+* Memory management is PagedKVCache's (engine/kv_cache.py:98-138): one pool of fixed-size blocks per layer,
+  a block table per sequence, `reserve` / `can_reserve` / `free`, block 0 handed out first, freed blocks
+  reused, `OutOfBlocksError` when the pool is empty.
+* `prepare(rows, positions)` builds the per-forward metadata once for all layers (engine/kv_cache.py:140-156:
+  write blocks and offsets by position, block tables padded with block 0) plus each row's context length.
+* `attend(layer, q, k, v, meta, scale)` is the cache-owned attention hook the model calls when a cache has
+  one (engine/model.py:72-74, contract of integration/kv_cache.py:160-168): the step's keys and values are
+  quantized into their slots first (store before attend), then one fused paged decode attention reads the
+  codes; a query at position p sees the slots 0..p of its row (engine/attention.py:12-20), so decode steps
+  (Q = 1), speculative verify steps (Q = k + 1) and prefill chunks all go through the same kernel.
+* `update` raises, as QuantizedKVCache.update does (integration/kv_cache.py:136-137): the cache never hands
+  out float keys and values.
+
+Formats: FP8 e4m3fn with static per-(layer, KV head) scales (default 1.0, fastserve kv/quant.py:16 stores
+FP8 unscaled), INT8 with dynamic per-(token, head) scales amax/127 paged like the codes, or plain BF16.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Any
+
+import torch
+
+from .paged_attention import paged_decode_attention, quantize_append
+
+_FORMATS = {torch.float8_e4m3fn: "fp8", torch.int8: "int8", torch.bfloat16: "bf16"}
+
+
+class OutOfBlocksError(RuntimeError):
+    """The pool has no free block: the scheduler must wait for sequences to finish (or preempt one)."""
+
+
+@dataclass(frozen=True)
+class PagedMeta:
+    write_blocks: torch.Tensor  # [batch, q_len] int32: physical block receiving each new token
+    write_offsets: torch.Tensor  # [batch, q_len] int32: slot inside that block
+    block_table: torch.Tensor  # [batch, n_blocks] int32: physical blocks of logical blocks 0 .. n_blocks - 1
+    context_lens: torch.Tensor  # [batch] int32: tokens in the cache once this step is written
+    kv_len: int  # the longest row's context length
+
+
+class PagedQuantKVCache:
+    """Paged, quantized KV cache with fused attention (see the module docstring).
+
+    `cfg` is any object with num_layers, num_kv_heads and head_dim (fastserve's ModelConfig); the three can
+    also be given directly. `k_scale` / `v_scale` (FP8 only): float32 [num_layers, num_kv_heads].
+    """
+
+    def __init__(
+        self,
+        cfg: Any = None,
+        *,
+        num_blocks: int,
+        block_size: int,
+        kv_dtype: torch.dtype = torch.float8_e4m3fn,
+        device: torch.device | str,
+        num_layers: int | None = None,
+        num_kv_heads: int | None = None,
+        head_dim: int | None = None,
+        k_scale: torch.Tensor | None = None,
+        v_scale: torch.Tensor | None = None,
+    ):
+        if kv_dtype not in _FORMATS:
+            raise ValueError(f"kv_dtype must be float8_e4m3fn, int8 or bfloat16, got {kv_dtype}")
+        self.num_layers = num_layers if cfg is None else cfg.num_layers
+        self.num_kv_heads = num_kv_heads if cfg is None else cfg.num_kv_heads
+        self.head_dim = head_dim if cfg is None else cfg.head_dim
+        if None in (self.num_layers, self.num_kv_heads, self.head_dim):
+            raise ValueError("give cfg, or num_layers, num_kv_heads and head_dim")
+        if block_size < 1 or block_size & (block_size - 1):
+            raise ValueError(f"block_size {block_size} must be a power of two")
+        self.kv_dtype = kv_dtype
+        self.format = _FORMATS[kv_dtype]
+        self.block_size = block_size
+        self.num_blocks = num_blocks
+        self.device = torch.device(device)
+        shape = (num_blocks, block_size, self.num_kv_heads, self.head_dim)  # [block, slot, kv_heads, head_dim]
+        self.k = [torch.zeros(shape, dtype=kv_dtype, device=self.device) for _ in range(self.num_layers)]
+        self.v = [torch.zeros(shape, dtype=kv_dtype, device=self.device) for _ in range(self.num_layers)]
+        if self.format == "fp8":
+            hs = (self.num_layers, self.num_kv_heads)
+            ks = torch.ones(hs) if k_scale is None else k_scale
+            vs = torch.ones(hs) if v_scale is None else v_scale
+            for s in (ks, vs):
+                if tuple(s.shape) != hs:
+                    raise ValueError(f"FP8 scales must be [{hs[0]}, {hs[1]}], got {tuple(s.shape)}")
+            self.k_scale = [ks[i].to(self.device, torch.float32).contiguous() for i in range(self.num_layers)]
+            self.v_scale = [vs[i].to(self.device, torch.float32).contiguous() for i in range(self.num_layers)]
+        elif self.format == "int8":
+            if k_scale is not None or v_scale is not None:
+                raise ValueError("INT8 scales are per token and computed on write: pass none")
+            ss = (num_blocks, block_size, self.num_kv_heads)
+            self.k_scale = [torch.zeros(ss, dtype=torch.float32, device=self.device) for _ in range(self.num_layers)]
+            self.v_scale = [torch.zeros(ss, dtype=torch.float32, device=self.device) for _ in range(self.num_layers)]
+        else:
+            if k_scale is not None or v_scale is not None:
+                raise ValueError("a bfloat16 cache takes no scales")
+            self.k_scale = self.v_scale = [None] * self.num_layers
+        self.free_blocks = list(range(num_blocks - 1, -1, -1))  # a stack: pop() hands out block 0 first
+        self.tables: dict[Any, list[int]] = {}  # sequence id -> its block table
+
+    # -- memory management (host side) -----------------------------------------------------------------------
+
+    def blocks_needed(self, num_tokens: int) -> int:
+        return math.ceil(num_tokens / self.block_size)
+
+    def can_reserve(self, seq_id: Any, num_tokens: int) -> bool:
+        have = len(self.tables.get(seq_id, []))
+        return self.blocks_needed(num_tokens) - have <= len(self.free_blocks)
+
+    def reserve(self, seq_id: Any, num_tokens: int) -> None:
+        """Make sure `seq_id` owns enough blocks to hold positions [0, num_tokens)."""
+        table = self.tables.setdefault(seq_id, [])
+        missing = self.blocks_needed(num_tokens) - len(table)
+        if missing > len(self.free_blocks):
+            raise OutOfBlocksError(f"need {missing} blocks, {len(self.free_blocks)} free")
+        table.extend(self.free_blocks.pop() for _ in range(missing))
+
+    def free(self, seq_id: Any) -> None:
+        """Return a finished sequence's blocks to the pool."""
+        self.free_blocks.extend(reversed(self.tables.pop(seq_id, [])))
+
+    def bytes_per_token(self) -> int:
+        """Bytes one token occupies across all layers and KV heads (codes, plus INT8's per-token scales)."""
+        elem = 2 if self.format == "bf16" else 1
+        per_head = 2 * (self.head_dim * elem + (4 if self.format == "int8" else 0))
+        return self.num_layers * self.num_kv_heads * per_head
+
+    # -- the per-forward metadata and the attention hook ------------------------------------------------------
+
+    def prepare(self, rows: list[Any], positions: torch.Tensor) -> PagedMeta:
+        """Metadata for one forward pass. positions: [batch, q_len], consecutive within each row."""
+        pos = positions.detach().to("cpu", torch.int64)
+        if pos.dim() != 2 or pos.shape[0] != len(rows):
+            raise ValueError(f"positions must be [{len(rows)}, q_len], got {tuple(pos.shape)}")
+        if pos.shape[1] > 1 and not bool((pos[:, 1:] - pos[:, :-1] == 1).all()):
+            raise ValueError("the positions of a row must be consecutive (one new token after another)")
+        if bool((pos < 0).any()):
+            raise ValueError("positions must be non-negative")
+        kv_len = int(pos.max()) + 1
+        n_blocks = self.blocks_needed(kv_len)
+        tables = []
+        for i, seq_id in enumerate(rows):
+            table = self.tables.get(seq_id, [])
+            if len(table) * self.block_size < int(pos[i].max()) + 1:
+                raise ValueError(f"sequence {seq_id!r} has too few blocks: call reserve() first")
+            tables.append(table[:n_blocks] + [0] * (n_blocks - len(table)))  # pad; padded slots are never read
+        block_table = torch.tensor(tables, dtype=torch.int64)
+        write_blocks = torch.gather(block_table, 1, pos // self.block_size)
+        dev = self.device
+        return PagedMeta(
+            write_blocks=write_blocks.to(dev, torch.int32),
+            write_offsets=(pos % self.block_size).to(dev, torch.int32),
+            block_table=block_table.to(dev, torch.int32),
+            context_lens=(pos[:, -1] + 1).to(dev, torch.int32),
+            kv_len=kv_len,
+        )
+
+    def update(self, layer: int, k: torch.Tensor, v: torch.Tensor, meta: PagedMeta):
+        raise NotImplementedError("a quantized cache never returns float keys and values: use attend()")
+
+    def attend(
+        self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, meta: PagedMeta, scale: float
+    ) -> torch.Tensor:
+        """Store this step's k, v [B, Hkv, Q, D] in their slots, then attend: q [B, Hq, Q, D] -> [B, Hq, Q, D]."""
+        b, hq, nq, d = q.shape
+        if tuple(k.shape) != (b, self.num_kv_heads, nq, d) or k.shape != v.shape:
+            raise ValueError(f"k and v must be [{b}, {self.num_kv_heads}, {nq}, {d}]")
+        if tuple(meta.write_blocks.shape) != (b, nq):
+            raise ValueError(f"meta was prepared for {tuple(meta.write_blocks.shape)} tokens, not {(b, nq)}")
+        quantize_append(
+            k.transpose(1, 2), v.transpose(1, 2), self.k[layer], self.v[layer], self.k_scale[layer],
+            self.v_scale[layer], meta.write_blocks, meta.write_offsets,
+        )
+        out = paged_decode_attention(
+            q.transpose(1, 2), self.k[layer], self.v[layer], meta.block_table, meta.context_lens,
+            self.k_scale[layer], self.v_scale[layer], scale=scale, max_context=meta.kv_len,
+        )  # [B, Q, Hq, D] bf16
+        return out.transpose(1, 2).to(q.dtype)
