@@ -1,11 +1,13 @@
-"""bpt_amd — MI355X (gfx950) paged decode attention over FP8 / INT8 / BF16 KV caches.
+"""bpt_amd — MI355X (gfx950) decode attention over quantized KV caches.
 
 The decode hot path of fastserve (kernels/kv_attention.py, engine/kv_cache.py, integration/kv_cache.py),
 re-implemented as hand-written HIP kernels behind a C ABI (include/bpt_amd.h, built into libbpt_amd.so)
-with a thin PyTorch-ROCm host layer. Importing needs no GPU; the library loads on first use and raises if
+with a thin PyTorch-ROCm host layer: paged FP8 / INT8 / BF16 pools (paged_attention, kv_cache) and
+contiguous KIVI caches (kivi: fastserve's kernels/kv_attention.py call surface). Importing needs no GPU; the library loads on first use and raises if
 it has not been built.
 """
 
+from . import kivi
 from .kv_cache import OutOfBlocksError, PagedMeta, PagedQuantKVCache
 from .paged_attention import decode_kernel_name, decode_plan, kv_read_bytes, paged_decode_attention, quantize_append
 
@@ -15,6 +17,7 @@ __all__ = [
     "PagedQuantKVCache",
     "decode_kernel_name",
     "decode_plan",
+    "kivi",
     "kv_read_bytes",
     "paged_decode_attention",
     "quantize_append",

@@ -111,6 +111,58 @@ class AppendArgs(ctypes.Structure):
     ]
 
 
+KIVI_INT4, KIVI_INT8, KIVI_F16, KIVI_BF16 = 0, 1, 2, 3
+
+
+class KiviArgs(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("format", _i32),
+        ("q_dtype", _i32),
+        ("batch", _i32),
+        ("num_q_heads", _i32),
+        ("num_kv_heads", _i32),
+        ("head_dim", _i32),
+        ("tokens", _i32),
+        ("group", _i32),
+        ("num_groups", _i32),
+        ("split", _i32),
+        ("num_splits", _i32),
+        ("grid_groups", _i32),
+        ("sm_scale", ctypes.c_float),
+        ("q", _vp),
+        ("q_stride_b", _i64),
+        ("q_stride_h", _i64),
+        ("k_codes", _vp),
+        ("v_codes", _vp),
+        ("code_stride_b", _i64),
+        ("code_stride_h", _i64),
+        ("code_stride_t", _i64),
+        ("k_scale", _vp),
+        ("k_zero", _vp),
+        ("kgrid_stride_b", _i64),
+        ("kgrid_stride_h", _i64),
+        ("kgrid_stride_g", _i64),
+        ("v_scale", _vp),
+        ("v_zero", _vp),
+        ("vgrid_stride_b", _i64),
+        ("vgrid_stride_h", _i64),
+        ("lengths", _vp),
+        ("out", _vp),
+        ("out_stride_b", _i64),
+        ("out_stride_h", _i64),
+        ("out_stride_s", _i64),
+        ("lse", _vp),
+        ("lse_stride_b", _i64),
+        ("lse_stride_h", _i64),
+        ("lse_stride_s", _i64),
+        ("workspace", _vp),
+        ("workspace_bytes", ctypes.c_size_t),
+        ("counters", _vp),
+        ("counters_bytes", ctypes.c_size_t),
+    ]
+
+
 # Every symbol include/bpt_amd.h declares, with its ctypes signature.
 SIGNATURES = {
     "bpt_decode_plan": (
@@ -119,6 +171,11 @@ SIGNATURES = {
     ),
     "bpt_paged_decode": (_i32, [ctypes.POINTER(DecodeArgs), _vp]),
     "bpt_quant_append": (_i32, [ctypes.POINTER(AppendArgs), _vp]),
+    "bpt_kivi_plan": (
+        _i32,
+        [ctypes.POINTER(KiviArgs), ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)],
+    ),
+    "bpt_kivi_decode": (_i32, [ctypes.POINTER(KiviArgs), _vp]),
     "bpt_last_error": (ctypes.c_char_p, []),
     "bpt_abi_version": (_i32, []),
     "bpt_fp8_decode_table": (_i32, [_vp, _vp]),
@@ -127,7 +184,7 @@ SIGNATURES = {
     "bpt_copy_probe": (_i32, [_vp, _vp, ctypes.c_uint64, _vp]),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class BptError(RuntimeError):

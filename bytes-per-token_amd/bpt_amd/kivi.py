@@ -1,0 +1,178 @@
+"""Decode attention over a KIVI-quantized KV cache, on HIP: fastserve's kernel-2 call surface.
+
+Mirrors fastserve's kernels/kv_attention.py (paths relative to its src/fastserve/):
+
+* `decode_attention(q, kv, lengths, scale, *, tokens=None, split=None, num_warps=1)` -> (out, lse) is the
+  launcher of :190-245: one partial attention per `split` tokens, out float32 [B, Hq, S, D], lse float32
+  [B, Hq, S] (natural log), S = max(ceil(tokens / split), 1); `split` defaults to `default_split` (:178-187)
+  and must be a multiple of the key group (ValueError otherwise, as :216-217). It is the `DecodeFn` that
+  integration/kv_cache.py:39 injects into QuantizedKVCache.
+* `attend(q, kv, lengths, scale, **launch)` is :248-252 (merge_partials of the above). Here it is one
+  launch that writes the merged result directly (the splits of one row are combined inside the kernel).
+* `kv` is anything with QuantKV's fields (kernels/reference.py:66-100): bits 4 / 8 with uint8 codes
+  [B, Hkv, T, D] (bits 4: [B, Hkv, T, D/2], channel d low nibble, d + D/2 high) and float16 grids
+  k_scale / k_zero [B, Hkv, T/group, D], v_scale / v_zero [B, Hkv, T]; or bits 16 with float16 / bfloat16
+  keys and values and no grids. fastserve's own QuantKV objects work unchanged.
+
+`num_warps` is accepted for signature parity and ignored: the launch shape is the library's. Limits: head
+dim 128, at most 16 query heads per KV head, key group and split multiples of 32 tokens, bits-16 caches in
+float16 or bfloat16.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Any
+
+import torch
+
+from . import _lib
+from ._lib import F_BF16, F_F16, F_F32, KIVI_BF16, KIVI_F16, KIVI_INT4, KIVI_INT8
+from .paged_attention import cached_buffer
+
+_Q_CODES = {torch.bfloat16: F_BF16, torch.float16: F_F16, torch.float32: F_F32}
+
+
+def default_split(batch: int, kv_heads: int, tokens: int, group: int = 32, max_programs: int = 16384) -> int:
+    """kernels/kv_attention.py:178-187: tokens per split, 4 key groups or more once that passes
+    `max_programs` (sequence, KV head, split) units; a power of two."""
+    per_program = max(tokens * batch * kv_heads // max_programs, 4 * group)
+    return max(group, 1 << (per_program.bit_length() - 1))
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _format(kv: Any) -> int:
+    if kv.bits == 4:
+        return KIVI_INT4
+    if kv.bits == 8:
+        return KIVI_INT8
+    if kv.bits == 16:
+        if kv.k_codes.dtype == torch.float16:
+            return KIVI_F16
+        if kv.k_codes.dtype == torch.bfloat16:
+            return KIVI_BF16
+        raise ValueError(f"a bits-16 cache must hold float16 or bfloat16 keys and values, got {kv.k_codes.dtype}")
+    raise ValueError(f"bits must be 4, 8 or 16, got {kv.bits}")
+
+
+def _launch(q, kv, lengths, scale, split, n_splits, out, lse) -> None:
+    fmt = _format(kv)
+    b, hq, d = q.shape
+    kc, vc = kv.k_codes, kv.v_codes
+    _require(kc.dim() == 4 and kc.shape == vc.shape, "k_codes and v_codes must be [B, Hkv, T, E] of one shape")
+    _require(kc.shape[0] == b, f"the cache holds {kc.shape[0]} sequences, q {b}")
+    hkv, t_max = kc.shape[1], kc.shape[2]
+    quant = fmt in (KIVI_INT4, KIVI_INT8)
+    if quant:
+        _require(kc.dtype == torch.uint8 and vc.dtype == torch.uint8, "4- and 8-bit codes must be uint8")
+        _require(kc.shape[3] * (2 if fmt == KIVI_INT4 else 1) == d, f"codes hold {kc.shape[3]} bytes per token, q has D={d}")
+    else:
+        _require(vc.dtype == kc.dtype and kc.shape[3] == d, "bits-16 keys and values must share q's head dim and a dtype")
+    _require(q.dtype in _Q_CODES, f"q must be bfloat16, float16 or float32, got {q.dtype}")
+    _require(q.stride(-1) == 1 and kc.stride(-1) == 1 and vc.stride() == kc.stride(), "channels must be contiguous")
+    _require(lengths.dtype == torch.int32 and tuple(lengths.shape) == (b,) and lengths.is_contiguous(),
+             f"lengths must be int32 [{b}]")
+    dev = q.device
+    _require(dev.type == "cuda", "decode_attention runs on a GPU: q must be a cuda tensor")
+    grids = (kv.k_scale, kv.k_zero, kv.v_scale, kv.v_zero) if quant else ()
+    for t in (kc, vc, lengths, *grids):
+        _require(t.device == dev, f"every tensor must be on {dev}")
+
+    a = _lib.KiviArgs()
+    a.struct_size = ctypes.sizeof(_lib.KiviArgs)
+    a.format, a.q_dtype = fmt, _Q_CODES[q.dtype]
+    a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim = b, hq, hkv, d
+    a.tokens, a.group = t_max, kv.group
+    a.split, a.num_splits = split, n_splits
+    a.sm_scale = float(scale)
+    a.q, a.q_stride_b, a.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
+    a.k_codes, a.v_codes = kc.data_ptr(), vc.data_ptr()
+    a.code_stride_b, a.code_stride_h, a.code_stride_t = kc.stride(0), kc.stride(1), kc.stride(2)
+    if quant:
+        ks, kz, vs, vz = grids
+        for name, g in (("k_scale", ks), ("k_zero", kz), ("v_scale", vs), ("v_zero", vz)):
+            _require(g.dtype == torch.float16, f"{name} must be float16, got {g.dtype}")
+        _require(ks.dim() == 4 and ks.shape == kz.shape and tuple(ks.shape[:2]) == (b, hkv) and ks.shape[3] == d,
+                 f"k_scale / k_zero must be [{b}, {hkv}, groups, {d}]")
+        _require(ks.stride() == kz.stride() and ks.stride(-1) == 1, "k_scale and k_zero must share contiguous channels")
+        _require(tuple(vs.shape) == (b, hkv, t_max) and vs.shape == vz.shape and vs.stride() == vz.stride()
+                 and vs.stride(-1) == 1, f"v_scale / v_zero must be [{b}, {hkv}, {t_max}] with unit token stride")
+        a.num_groups = ks.shape[2]
+        a.k_scale, a.k_zero = ks.data_ptr(), kz.data_ptr()
+        a.kgrid_stride_b, a.kgrid_stride_h, a.kgrid_stride_g = ks.stride(0), ks.stride(1), ks.stride(2)
+        a.v_scale, a.v_zero = vs.data_ptr(), vz.data_ptr()
+        a.vgrid_stride_b, a.vgrid_stride_h = vs.stride(0), vs.stride(1)
+    a.lengths = lengths.data_ptr()
+    a.out = out.data_ptr()
+    a.out_stride_b, a.out_stride_h, a.out_stride_s = out.stride(0), out.stride(1), out.stride(2)
+    a.lse = lse.data_ptr()
+    a.lse_stride_b, a.lse_stride_h, a.lse_stride_s = lse.stride(0), lse.stride(1), lse.stride(2)
+    lib = _lib.lib()
+    ws_bytes, cnt_bytes = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    _lib.check(lib.bpt_kivi_plan(ctypes.byref(a), ctypes.byref(ws_bytes), ctypes.byref(cnt_bytes)))
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    workspace = cached_buffer("partials", dev, stream, ws_bytes.value)
+    counters = cached_buffer("counters", dev, stream, cnt_bytes.value)
+    a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel()
+    a.counters, a.counters_bytes = counters.data_ptr(), counters.numel()
+    _lib.check(lib.bpt_kivi_decode(ctypes.byref(a), ctypes.c_void_p(stream)))
+
+
+def decode_attention(
+    q: torch.Tensor,
+    kv: Any,
+    lengths: torch.Tensor,
+    scale: float,
+    *,
+    tokens: int | None = None,
+    split: int | None = None,
+    num_warps: int = 1,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Partial attentions of one query per head over a KIVI cache, one per split (kv_attention.py:190-245).
+
+    q [B, Hq, D] (bf16 / f16 / f32); lengths [B] int32 on q's device. `tokens` (the longest row's length,
+    when the caller knows it) sizes the splits without a device read. Returns (out float32 [B, Hq, S, D],
+    lse float32 [B, Hq, S]); `merge_partials` of the two is the attention.
+    """
+    del num_warps  # launch shape is the library's
+    b, hq, d = q.shape
+    hkv, t_max = kv.k_codes.shape[1], kv.k_codes.shape[2]
+    tokens = t_max if tokens is None else tokens
+    if split is None:
+        split = default_split(b, hkv, tokens, kv.group)
+    if split % kv.group:
+        raise ValueError(f"split {split} must be a multiple of the key group {kv.group}")
+    n_splits = max(-(-tokens // split), 1)
+    out = torch.empty((b, hq, n_splits, d), dtype=torch.float32, device=q.device)
+    lse = torch.empty((b, hq, n_splits), dtype=torch.float32, device=q.device)
+    _launch(q, kv, lengths, scale, split, n_splits, out, lse)
+    return out, lse
+
+
+def attend(q: torch.Tensor, kv: Any, lengths: torch.Tensor, scale: float, **launch: int | None) -> torch.Tensor:
+    """Decode attention over a KIVI cache: [B, Hq, D] float32 (kv_attention.py:248-252).
+
+    The result does not depend on the split; a given `split` is still checked against the key group. The
+    tokens past `tokens` (when given) are not read, as in decode_attention.
+    """
+    b, hq, d = q.shape
+    t_max = kv.k_codes.shape[2]
+    tokens = launch.get("tokens")
+    tokens = t_max if tokens is None else tokens
+    split = launch.get("split")
+    if split is None:
+        split = default_split(b, kv.k_codes.shape[1], tokens, kv.group)
+    if split % kv.group:
+        raise ValueError(f"split {split} must be a multiple of the key group {kv.group}")
+    reach = max(-(-tokens // split), 1) * split  # the tokens decode_attention's splits would cover
+    step = kv.group * 32 // math.gcd(kv.group, 32)
+    whole = max(-(-reach // step), 1) * step  # one split covering all of them
+    out = torch.empty((b, hq, 1, d), dtype=torch.float32, device=q.device)
+    lse = torch.empty((b, hq, 1), dtype=torch.float32, device=q.device)
+    _launch(q, kv, lengths, scale, whole, 1, out, lse)
+    return out[:, :, 0]

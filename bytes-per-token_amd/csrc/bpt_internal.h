@@ -89,10 +89,48 @@ struct AppendParams {
   int src_dtype, slot_i64;
 };
 
+// Launch-ready form of bpt_kivi_args: decode attention over a KIVI cache (asymmetric 4/8-bit codes with
+// float16 grids, or float16 / bfloat16 keys and values), one partial result per split.
+struct KiviParams {
+  const void* q;
+  int64_t q_sb, q_sh;  // elements
+  const uint8_t* kc;
+  const uint8_t* vc;
+  int64_t c_sb, c_sh, c_st;  // bytes
+  const uint16_t* ks;        // float16 key grid [B, Hkv, groups, D]
+  const uint16_t* kz;
+  int64_t g_sb, g_sh, g_sg;  // elements
+  const uint16_t* vs;        // float16 value grid [B, Hkv, T]
+  const uint16_t* vz;
+  int64_t t_sb, t_sh;  // elements
+  const int32_t* lens;
+  float* out;  // [B, Hq, S, D]
+  int64_t o_sb, o_sh, o_ss;
+  float* lse;  // [B, Hq, S]
+  int64_t l_sb, l_sh, l_ss;
+  float* ws_out;       // [2 * grid, G, D] normalized partials
+  float* ws_lse;       // [2 * grid, G] their log2-sum-exp
+  unsigned* counters;  // [B * Hkv * S] arrivals per (sequence, KV head, split); zero between calls
+  int B, Hq, Hkv, G, S;
+  int cps;      // chunks per split
+  int gpc;      // chunks per key group
+  int len_cap;  // lengths are clamped to this (the laid-out tokens, and the splits' reach)
+  int grid;
+  float qscale;  // sm_scale * log2(e)
+  int q_dtype;
+};
+
+// KIVI storage formats of bpt_kivi_args.bits / kv_dtype.
+constexpr int kKivi4 = 0;
+constexpr int kKivi8 = 1;
+constexpr int kKiviF16 = 2;
+constexpr int kKiviBf16 = 3;
+
 int decode_rows_per_load(int kv_dtype);
 int decode_chunk_tokens(int kv_dtype, int rows_per_group);
 hipError_t launch_decode(const DecodeParams& p, int kv_dtype, int scale_kind, int rows_per_group, hipStream_t stream);
 hipError_t launch_decode_mfma(const DecodeParams& p, int kv_dtype, int scale_kind, hipStream_t stream);
+hipError_t launch_kivi(const KiviParams& p, int fmt, hipStream_t stream);
 hipError_t launch_append(const AppendParams& p, int kv_dtype, int scale_kind, int head_dim, hipStream_t stream);
 hipError_t launch_fp8_table(float* out, hipStream_t stream);
 hipError_t launch_fp8_encode(const float* x, float scale, uint8_t* out, int64_t n, hipStream_t stream);

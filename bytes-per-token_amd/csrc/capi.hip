@@ -122,6 +122,74 @@ int make_plan(const bpt_decode_args* a, Plan* pl) {
   return BPT_OK;
 }
 
+struct KiviPlan {
+  int G, grid, len_cap, eb;
+  size_t ws_out_floats, ws_lse_floats, workspace, counters;
+};
+
+int make_kivi_plan(const bpt_kivi_args* a, KiviPlan* pl) {
+  const char* fn = "bpt_kivi_plan";
+  if (!a) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: args is NULL", fn);
+  if (a->struct_size != sizeof(bpt_kivi_args))
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: struct_size %u != %zu (stale binding)", fn, a->struct_size,
+                sizeof(bpt_kivi_args));
+  if (a->format < BPT_KIVI_INT4 || a->format > BPT_KIVI_BF16)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: unknown format %d", fn, a->format);
+  if (a->q_dtype < BPT_F_BF16 || a->q_dtype > BPT_F_F32)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: q_dtype must be bf16, f16 or f32", fn);
+  if (a->batch < 0 || a->num_q_heads < 1 || a->num_kv_heads < 1 || a->tokens < 0)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: batch, tokens >= 0 and num_q_heads, num_kv_heads >= 1", fn);
+  if (a->batch > bpt::kMaxBatch)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: batch %d exceeds %d", fn, a->batch, bpt::kMaxBatch);
+  if (a->num_q_heads % a->num_kv_heads)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: %d query heads are not a multiple of %d KV heads", fn,
+                a->num_q_heads, a->num_kv_heads);
+  pl->G = a->num_q_heads / a->num_kv_heads;
+  if (pl->G > 16)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: %d query heads per KV head (at most 16)", fn, pl->G);
+  if (a->head_dim != bpt::kHeadDim)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: head_dim %d not supported (128)", fn, a->head_dim);
+  const bool quant = a->format == BPT_KIVI_INT4 || a->format == BPT_KIVI_INT8;
+  if (a->group < 1 || a->split < 1 || a->split % a->group)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: split %d must be a multiple of the key group %d", fn, a->split,
+                a->group);
+  if (a->split % bpt::kMfmaChunk)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: split %d must be a multiple of %d tokens", fn, a->split,
+                bpt::kMfmaChunk);
+  if (a->num_splits < 1) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: num_splits must be >= 1", fn);
+  if (quant) {
+    if (a->group % bpt::kMfmaChunk)
+      return fail(BPT_ERR_INVALID_ARGUMENT, "%s: key group %d must be a multiple of %d tokens", fn, a->group,
+                  bpt::kMfmaChunk);
+    if (a->tokens % a->group)
+      return fail(BPT_ERR_INVALID_ARGUMENT, "%s: %d tokens are not a whole number of groups of %d", fn, a->tokens,
+                  a->group);
+    if ((int64_t)a->num_groups * a->group < a->tokens)
+      return fail(BPT_ERR_INVALID_ARGUMENT, "%s: %d key groups do not cover %d tokens", fn, a->num_groups,
+                  a->tokens);
+  }
+  if (!std::isfinite(a->sm_scale)) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: sm_scale must be finite", fn);
+  pl->eb = quant ? 1 : 2;
+  const int64_t reach = (int64_t)a->num_splits * a->split;
+  pl->len_cap = (int)(reach < a->tokens ? reach : a->tokens);
+  const int64_t max_nb = (pl->len_cap + bpt::kMfmaChunk - 1) / bpt::kMfmaChunk;
+  const int64_t seq_chunks = (int64_t)a->batch * max_nb;
+  if (seq_chunks > 0x7fffffffLL / a->num_kv_heads)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: batch x tokens x heads too large", fn);
+  const int64_t segs = (int64_t)a->batch * a->num_kv_heads * a->num_splits;
+  if (segs > 0x7fffffffLL) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: batch x heads x splits too large", fn);
+  int64_t grid = (int64_t)bpt::kComputeUnits * bpt::kDecodeGroupsPerCu;
+  const int64_t bound_c = seq_chunks * a->num_kv_heads;
+  if (bound_c < grid) grid = bound_c;
+  pl->grid = (int)(grid < 1 ? 1 : grid);
+  const size_t slots = 2 * (size_t)pl->grid;
+  pl->ws_out_floats = slots * pl->G * a->head_dim;
+  pl->ws_lse_floats = slots * pl->G;
+  pl->workspace = align256((pl->ws_out_floats + pl->ws_lse_floats) * sizeof(float));
+  pl->counters = align256((size_t)segs * sizeof(unsigned));
+  return BPT_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -210,6 +278,88 @@ int bpt_paged_decode(const bpt_decode_args* a, void* stream) {
   p.table_i64 = a->table_dtype == BPT_IDX_I64;
   hipError_t e = pl.mfma ? bpt::launch_decode_mfma(p, a->kv_dtype, a->scale_kind, (hipStream_t)stream)
                          : bpt::launch_decode(p, a->kv_dtype, a->scale_kind, pl.rows_per_group, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(fn, e);
+  return BPT_OK;
+}
+
+int bpt_kivi_plan(bpt_kivi_args* args, size_t* workspace_bytes, size_t* counters_bytes) {
+  KiviPlan pl;
+  int rc = make_kivi_plan(args, &pl);
+  if (rc) return rc;
+  args->grid_groups = pl.grid;
+  if (workspace_bytes) *workspace_bytes = pl.workspace;
+  if (counters_bytes) *counters_bytes = pl.counters;
+  return BPT_OK;
+}
+
+int bpt_kivi_decode(const bpt_kivi_args* a, void* stream) {
+  const char* fn = "bpt_kivi_decode";
+  KiviPlan pl;
+  int rc = make_kivi_plan(a, &pl);
+  if (rc) return rc;
+  if (a->batch == 0) return BPT_OK;
+  const bool quant = a->format == BPT_KIVI_INT4 || a->format == BPT_KIVI_INT8;
+  if (!a->q || !a->k_codes || !a->v_codes || !a->lengths || !a->out || !a->lse)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: q, codes, lengths, out and lse must be non-NULL", fn);
+  if (quant && (!a->k_scale || !a->k_zero || !a->v_scale || !a->v_zero))
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: 4- and 8-bit codes need their key and value grids", fn);
+  if (!aligned16(a->k_codes) || !aligned16(a->v_codes) || (a->code_stride_b * pl.eb) % 16 ||
+      (a->code_stride_h * pl.eb) % 16 || (a->code_stride_t * pl.eb) % 16)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: code tensors and their strides must be 16-byte aligned", fn);
+  if (quant && (!aligned16(a->k_scale) || !aligned16(a->k_zero) || !aligned16(a->v_scale) || !aligned16(a->v_zero) ||
+                a->kgrid_stride_b % 8 || a->kgrid_stride_h % 8 || a->kgrid_stride_g % 8 || a->vgrid_stride_b % 4 ||
+                a->vgrid_stride_h % 4))
+    return fail(BPT_ERR_INVALID_ARGUMENT,
+                "%s: grids must be 16-byte aligned, key-grid strides multiples of 8 and value-grid strides of 4", fn);
+  if (!a->workspace || a->workspace_bytes < pl.workspace || ((uintptr_t)a->workspace & 255u))
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: a 256-byte aligned workspace of %zu bytes is required (got %zu)", fn,
+                pl.workspace, a->workspace_bytes);
+  if (!a->counters || a->counters_bytes < pl.counters || ((uintptr_t)a->counters & 3u))
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: a zeroed counter buffer of %zu bytes is required (got %zu)", fn,
+                pl.counters, a->counters_bytes);
+
+  bpt::KiviParams p;
+  p.q = a->q;
+  p.q_sb = a->q_stride_b;
+  p.q_sh = a->q_stride_h;
+  p.kc = (const uint8_t*)a->k_codes;
+  p.vc = (const uint8_t*)a->v_codes;
+  p.c_sb = a->code_stride_b * pl.eb;
+  p.c_sh = a->code_stride_h * pl.eb;
+  p.c_st = a->code_stride_t * pl.eb;
+  p.ks = (const uint16_t*)a->k_scale;
+  p.kz = (const uint16_t*)a->k_zero;
+  p.g_sb = a->kgrid_stride_b;
+  p.g_sh = a->kgrid_stride_h;
+  p.g_sg = a->kgrid_stride_g;
+  p.vs = (const uint16_t*)a->v_scale;
+  p.vz = (const uint16_t*)a->v_zero;
+  p.t_sb = a->vgrid_stride_b;
+  p.t_sh = a->vgrid_stride_h;
+  p.lens = a->lengths;
+  p.out = a->out;
+  p.o_sb = a->out_stride_b;
+  p.o_sh = a->out_stride_h;
+  p.o_ss = a->out_stride_s;
+  p.lse = a->lse;
+  p.l_sb = a->lse_stride_b;
+  p.l_sh = a->lse_stride_h;
+  p.l_ss = a->lse_stride_s;
+  p.ws_out = (float*)a->workspace;
+  p.ws_lse = (float*)a->workspace + pl.ws_out_floats;
+  p.counters = (unsigned*)a->counters;
+  p.B = a->batch;
+  p.Hq = a->num_q_heads;
+  p.Hkv = a->num_kv_heads;
+  p.G = pl.G;
+  p.S = a->num_splits;
+  p.cps = a->split / bpt::kMfmaChunk;
+  p.gpc = quant ? a->group / bpt::kMfmaChunk : 1;
+  p.len_cap = pl.len_cap;
+  p.grid = pl.grid;
+  p.qscale = a->sm_scale * bpt::kLog2e;
+  p.q_dtype = a->q_dtype;
+  hipError_t e = bpt::launch_kivi(p, a->format, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(fn, e);
   return BPT_OK;
 }

@@ -117,9 +117,10 @@ __device__ __forceinline__ void load_q(const DecodeParams& p, int64_t base, floa
 
 // Lengths (clamped to the launch's cap), chunks per sequence and their exclusive prefix sum over the batch
 // (the segment line: sequence b's segments start at chunk HR * prefix[b]), computed by the whole workgroup
-// into LDS: s_prefix[B + 1], s_len[B]; s_wsum holds one int per wave.
-template <int NW, int CH>
-__device__ __forceinline__ void build_segment_line(const DecodeParams& p, int* s_prefix, int* s_len, int* s_wsum) {
+// into LDS: s_prefix[B + 1], s_len[B]; s_wsum holds one int per wave. Params: any parameter block with B,
+// lens and len_cap.
+template <int NW, int CH, typename Params>
+__device__ __forceinline__ void build_segment_line(const Params& p, int* s_prefix, int* s_len, int* s_wsum) {
   constexpr int NT = NW * 64;
   const int tid = threadIdx.x;
   const int lane = tid & 63;

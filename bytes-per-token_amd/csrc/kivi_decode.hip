@@ -1,0 +1,747 @@
+// Decode attention over a KIVI cache on the matrix cores: asymmetric 4- or 8-bit codes with float16 grids
+// (keys: one (scale, zero) per channel per key group of tokens; values: one per token), or float16 /
+// bfloat16 keys and values (the unquantized control). One query per head, the G query heads of a KV head
+// computed together so every cached byte is read once; one partial result per split of the tokens.
+//
+// Follows fastserve kernels/kv_attention.py:56-175 (decode_attention_kernel: grids folded out of the inner
+// product, online softmax, one partial (out, lse) per split) and :190-245 (the launcher's split rule), over
+// the format of kernels/reference.py:66-160. The work is cut differently: the tokens of every (sequence,
+// KV head) are a line of 32-token chunks that the launched workgroups share out evenly (stream-K), so the
+// chip fills whatever the caller's split; a split covered by several workgroups is combined exactly
+// (kernels/reference.py:205-211's algebra) by the last one to finish.
+//
+// Chunk math (l = lane, n = l % 16, kq = l / 16; rows padded to 16, the MFMA N dimension):
+//  * scores S^T = K Q^T with 16x16x32 f16 (bf16 for a bfloat16 cache) MFMAs, four K-steps per 16-token
+//    tile. A = this lane's token 16 t + n: the codes turned into f16 (1024 + code, by placing the code
+//    under the f16 exponent of 1024) minus (1024 + zero) of their channel, i.e. code - zero exactly.
+//    B = q * key scale, folded once per chunk (its key group) in a compact layout (RP rows x 128
+//    channels over 64 lanes), scaled by a power of two so its largest element sits in [2^13, 2^14), split
+//    into an f16 high part and the f16 rounding remainder (22 significant bits), and handed to the MFMA
+//    layout through LDS. Each row's score is the MFMA result times sm_scale * log2(e) / that power of two.
+//  * online softmax in base 2 per row (the row's four lanes agree through two shuffles). Each token's value
+//    scale is folded into its weight, w = 2^(s - base) * vscale; the reference point tracks the largest
+//    s + log2(vscale) bound, so every w stays below 2^12 (inside f16) whatever the value scales.
+//  * output O^T += V^T W^T, contraction over the lane's own eight score tokens. V^T comes from 4 x 4 byte
+//    (or 2 x 2 half) transposes, turned into code - value zero exactly as for keys; W = f16 high part plus
+//    remainder, two MFMAs per M-tile.
+#include <type_traits>
+
+#include "decode_common.h"
+
+namespace bpt {
+
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kChunk = 32;  // tokens per chunk: two 16-token tiles
+
+template <int FMT>
+struct KF {
+  static constexpr bool kQuant = FMT == kKivi4 || FMT == kKivi8;
+  static constexpr bool kBf16 = FMT == kKiviBf16;
+  static constexpr int kKU4 = FMT == kKivi4 ? 1 : (FMT == kKivi8 ? 2 : 4);  // 16-byte K loads per lane per tile
+  static constexpr int kVWords = FMT == kKivi4 ? 1 : (FMT == kKivi8 ? 2 : 4);  // V dwords per lane per token
+  typedef typename std::conditional<kBf16, bf16x8, f16x8>::type T;  // MFMA operand
+  typedef typename std::conditional<kBf16, __bf16, _Float16>::type E;
+};
+
+// Position of channel c in the score contraction order (k = 32 kq + 8 s + i). Byte-wide formats use the
+// identity (lane kq reads channels 32 kq .. 32 kq + 31); 4-bit codes pair channel d with d + 64 in a byte,
+// so lane kq's 16 bytes hold channels 16 kq + j and 64 + 16 kq + j, and K-step s takes byte word s:
+// [16 kq + 4 s + 0..3 (low nibbles), 64 + 16 kq + 4 s + 0..3 (high nibbles)].
+template <int FMT>
+__device__ __forceinline__ int kpos(int c) {
+  if constexpr (FMT == kKivi4) {
+    const int cc = c & 63;
+    return 2 * (cc & ~3) + (c >= 64 ? 4 : 0) + (cc & 3);
+  }
+  return c;
+}
+
+// Output channel held by lane (kq, i) in M-tile mu of the value product.
+template <int FMT>
+__device__ __forceinline__ int out_channel(int kq, int i, int mu) {
+  if constexpr (FMT == kKivi4) return (mu < 4 ? 0 : 64) + 16 * kq + 4 * i + (mu & 3);
+  return 32 * kq + 8 * i + mu;
+}
+
+template <int FMT, int CPL>
+struct KChunk {
+  U4 k[2][KF<FMT>::kKU4];                 // tile t: token 16 t + n
+  uint32_t v[2][4][KF<FMT>::kVWords];     // tile t, token 16 t + 4 kq + i
+  u32x2 vs[2], vz[2];                     // f16 value grids of tokens 16 t + 4 kq + 0..3
+  uint32_t gs[CPL / 2], gz[CPL / 2];      // f16 key grid of this lane's fold channels
+};
+
+__device__ __forceinline__ f32x4 mfma(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Bytes 0, 1 (pair_lo) or 2, 3 (pair_hi) of w as the f16 pair (1024 + b0, 1024 + b1): exact for 0..255.
+__device__ __forceinline__ uint32_t pair_lo(uint32_t w) { return __builtin_amdgcn_perm(0x64006400u, w, 0x07010500u); }
+__device__ __forceinline__ uint32_t pair_hi(uint32_t w) { return __builtin_amdgcn_perm(0x64006400u, w, 0x07030502u); }
+
+__device__ __forceinline__ f16x8 bytes8_minus(uint32_t w0, uint32_t w1, f16x8 z) {
+  const u32x4 r = {pair_lo(w0), pair_hi(w0), pair_lo(w1), pair_hi(w1)};
+  return __builtin_bit_cast(f16x8, r) - z;
+}
+
+// 4 x 4 byte transpose: w[i] byte j -> o[j] byte i.
+__device__ __forceinline__ void transpose4(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, uint32_t (&o)[4]) {
+  const uint32_t t0 = __builtin_amdgcn_perm(w1, w0, 0x05010400u);
+  const uint32_t t1 = __builtin_amdgcn_perm(w3, w2, 0x05010400u);
+  const uint32_t t2 = __builtin_amdgcn_perm(w1, w0, 0x07030602u);
+  const uint32_t t3 = __builtin_amdgcn_perm(w3, w2, 0x07030602u);
+  o[0] = __builtin_amdgcn_perm(t1, t0, 0x05040100u);
+  o[1] = __builtin_amdgcn_perm(t1, t0, 0x07060302u);
+  o[2] = __builtin_amdgcn_perm(t3, t2, 0x05040100u);
+  o[3] = __builtin_amdgcn_perm(t3, t2, 0x07060302u);
+}
+
+template <int FMT, int CPL>
+__device__ __forceinline__ int64_t head_codes(const KiviParams& p, int b, int h) {
+  return (int64_t)b * p.c_sb + (int64_t)h * p.c_sh;
+}
+
+// Chunk kk's key-grid, K and value-grid loads (issued together, in the order they are consumed) and its V
+// loads. Tokens at or past len read the row's last token instead (valid memory; their weights are zero).
+template <int FMT, int RP, int CPL>
+__device__ __forceinline__ void issue_k(const KiviParams& p, int b, int h, int kk, int len, int lane, KChunk<FMT, CPL>& c) {
+  typedef KF<FMT> F;
+  constexpr int LPR = 64 / RP;
+  const int T0 = kk * kChunk;
+  const int kq = lane >> 4, n = lane & 15;
+  if constexpr (F::kQuant) {
+    const int grp = kk / p.gpc;
+    const int64_t go = (int64_t)b * p.g_sb + (int64_t)h * p.g_sh + (int64_t)grp * p.g_sg + (lane % LPR) * CPL;
+    if constexpr (CPL == 4) {
+      const u32x2 s = *(const u32x2*)(p.ks + go);
+      const u32x2 z = *(const u32x2*)(p.kz + go);
+      c.gs[0] = s.x; c.gs[1] = s.y;
+      c.gz[0] = z.x; c.gz[1] = z.y;
+    } else {
+#pragma unroll
+      for (int j = 0; j < CPL / 8; ++j) {
+        const u32x4 s = *(const u32x4*)(p.ks + go + 8 * j);
+        const u32x4 z = *(const u32x4*)(p.kz + go + 8 * j);
+        c.gs[4 * j] = s.x; c.gs[4 * j + 1] = s.y; c.gs[4 * j + 2] = s.z; c.gs[4 * j + 3] = s.w;
+        c.gz[4 * j] = z.x; c.gz[4 * j + 1] = z.y; c.gz[4 * j + 2] = z.z; c.gz[4 * j + 3] = z.w;
+      }
+    }
+  }
+  const uint8_t* base = p.kc + head_codes<FMT, CPL>(p, b, h) + kq * (16 * F::kKU4);
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int tok = min(T0 + 16 * t + n, len - 1);
+#pragma unroll
+    for (int j = 0; j < F::kKU4; ++j) c.k[t][j] = load16(base + (int64_t)tok * p.c_st + 16 * j);
+  }
+  if constexpr (F::kQuant) {
+    const int64_t to = (int64_t)b * p.t_sb + (int64_t)h * p.t_sh + T0 + 4 * kq;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      c.vs[t] = *(const u32x2*)(p.vs + to + 16 * t);
+      c.vz[t] = *(const u32x2*)(p.vz + to + 16 * t);
+    }
+  }
+}
+
+template <int FMT, int CPL>
+__device__ __forceinline__ void issue_v(const KiviParams& p, int b, int h, int kk, int len, int lane, KChunk<FMT, CPL>& c) {
+  typedef KF<FMT> F;
+  const int T0 = kk * kChunk;
+  const int kq = lane >> 4, n = lane & 15;
+  const uint8_t* base = p.vc + head_codes<FMT, CPL>(p, b, h) + n * (4 * F::kVWords);
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tok = min(T0 + 16 * t + 4 * kq + i, len - 1);
+      const uint8_t* src = base + (int64_t)tok * p.c_st;
+      if constexpr (F::kVWords == 1) {
+        c.v[t][i][0] = __builtin_nontemporal_load((const uint32_t*)src);
+      } else if constexpr (F::kVWords == 2) {
+        const u32x2 x = __builtin_nontemporal_load((const u32x2*)src);
+        c.v[t][i][0] = x.x;
+        c.v[t][i][1] = x.y;
+      } else {
+        const U4 x = load16(src);
+        c.v[t][i][0] = x.x;
+        c.v[t][i][1] = x.y;
+        c.v[t][i][2] = x.z;
+        c.v[t][i][3] = x.w;
+      }
+    }
+  }
+}
+
+// The compact fold: lane l covers row fr = l / LPR, channels fc .. fc + CPL - 1 (fc = (l % LPR) * CPL).
+// x = q * key scale (1 for the unquantized formats); the row's largest |x| picks the power of two f; the
+// f-scaled x goes to LDS as high part + remainder at its contraction position, 1024 + key zero goes to
+// s_kz (row 0's lanes), qscale / f to s_inv.
+template <int FMT, int RP, int CPL>
+__device__ __forceinline__ void fold(const float (&qf)[CPL], const uint32_t (&gs)[CPL / 2], const uint32_t (&gz)[CPL / 2],
+                                     float qscale, int lane, uint16_t (*s_qh)[kHeadDim], uint16_t (*s_ql)[kHeadDim],
+                                     uint16_t* s_kz, float* s_inv) {
+  typedef KF<FMT> F;
+  typedef typename F::E E;
+  constexpr int LPR = 64 / RP;
+  const int fr = lane / LPR;
+  const int fc = (lane % LPR) * CPL;
+  float x[CPL];
+  float mx = 0.0f;
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    float s = 1.0f;
+    if constexpr (F::kQuant) {
+      const uint32_t w = gs[c >> 1];
+      s = (float)__builtin_bit_cast(_Float16, (uint16_t)((c & 1) ? (w >> 16) : (w & 0xffffu)));
+    }
+    x[c] = qf[c] * s;
+    mx = fmaxf(mx, fabsf(x[c]));
+  }
+#pragma unroll
+  for (int off = 1; off < LPR; off <<= 1) mx = fmaxf(mx, shfl_xor_f(mx, off));
+  int e = 0;
+  if (mx > 0.0f) (void)frexpf(mx, &e);
+  e = e < -100 ? -100 : e;
+  const float f = ldexpf(1.0f, 14 - e);
+#pragma unroll
+  for (int c0 = 0; c0 < CPL; c0 += 4) {
+    uint16_t hb[4], lb[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float y = x[c0 + c] * f;
+      const E hi = (E)y;
+      const E lo = (E)(y - (float)hi);
+      hb[c] = __builtin_bit_cast(uint16_t, hi);
+      lb[c] = __builtin_bit_cast(uint16_t, lo);
+    }
+    const int pos = kpos<FMT>(fc + c0);  // four consecutive channels stay consecutive
+    *(u32x2*)&s_qh[fr][pos] = u32x2{hb[0] | ((uint32_t)hb[1] << 16), hb[2] | ((uint32_t)hb[3] << 16)};
+    *(u32x2*)&s_ql[fr][pos] = u32x2{lb[0] | ((uint32_t)lb[1] << 16), lb[2] | ((uint32_t)lb[3] << 16)};
+    if constexpr (F::kQuant) {
+      if (fr == 0) {
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        const h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+        const h2 z0 = __builtin_bit_cast(h2, gz[c0 >> 1]) + k1024;
+        const h2 z1 = __builtin_bit_cast(h2, gz[(c0 >> 1) + 1]) + k1024;
+        *(u32x2*)&s_kz[pos] = u32x2{__builtin_bit_cast(uint32_t, z0), __builtin_bit_cast(uint32_t, z1)};
+      }
+    }
+  }
+  if ((lane % LPR) == 0) s_inv[fr] = qscale / f;
+}
+
+// Row n's score operands for the four K-steps (zero past the G rows) and, for codes, 1024 + key zero in
+// this lane's contraction order.
+template <int FMT, int RP>
+__device__ __forceinline__ void read_fold(int n, int kq, int G, const uint16_t (*s_qh)[kHeadDim],
+                                          const uint16_t (*s_ql)[kHeadDim], const uint16_t* s_kz, const float* s_inv,
+                                          typename KF<FMT>::T (&qh)[4], typename KF<FMT>::T (&ql)[4], f16x8 (&kzp)[4],
+                                          float& inv) {
+  typedef typename KF<FMT>::T T;
+  const bool in = n < G;
+  const int r = in ? n : 0;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const u32x4 h = *(const u32x4*)&s_qh[r][32 * kq + 8 * s];
+    const u32x4 l = *(const u32x4*)&s_ql[r][32 * kq + 8 * s];
+    const u32x4 zero = {0u, 0u, 0u, 0u};
+    qh[s] = __builtin_bit_cast(T, in ? h : zero);
+    ql[s] = __builtin_bit_cast(T, in ? l : zero);
+    if constexpr (KF<FMT>::kQuant) kzp[s] = *(const f16x8*)&s_kz[32 * kq + 8 * s];
+  }
+  inv = in ? s_inv[r] : 0.0f;
+}
+
+// Score operand A of K-step s, tile t: code - zero (quantized) or the stored halves.
+template <int FMT, int CPL>
+__device__ __forceinline__ typename KF<FMT>::T k_operand(const KChunk<FMT, CPL>& c, int t, int s, f16x8 kz) {
+  typedef typename KF<FMT>::T T;
+  if constexpr (FMT == kKivi8) {
+    const U4 q = c.k[t][s >> 1];
+    const uint32_t w0 = (s & 1) ? q.z : q.x;
+    const uint32_t w1 = (s & 1) ? q.w : q.y;
+    return bytes8_minus(w0, w1, kz);
+  } else if constexpr (FMT == kKivi4) {
+    const U4 q = c.k[t][0];
+    const uint32_t w = s == 0 ? q.x : (s == 1 ? q.y : (s == 2 ? q.z : q.w));
+    return bytes8_minus(w & 0x0F0F0F0Fu, (w >> 4) & 0x0F0F0F0Fu, kz);
+  } else {
+    return __builtin_bit_cast(T, c.k[t][s]);
+  }
+}
+
+// Fold chunk kk into this lane's state: m (row n's reference point, shared by its four lanes), l (this
+// lane's partial weight sum), o[mu] (row n, channels out_channel(kq, i, mu)).
+template <int FMT, int CPL, typename AfterScores>
+__device__ __forceinline__ void compute(KChunk<FMT, CPL>& c, int kk, int len, int lane, const typename KF<FMT>::T (&qh)[4],
+                                        const typename KF<FMT>::T (&ql)[4], const f16x8 (&kzp)[4], float inv, float& m,
+                                        float& l, f32x4 (&o)[8], AfterScores after_scores) {
+  typedef KF<FMT> F;
+  typedef typename F::T T;
+  typedef typename F::E E;
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const int T0 = kk * kChunk;
+  const int kq = lane >> 4;
+  float sc[8];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    f32x4 st = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const T a = k_operand<FMT, CPL>(c, t, s, kzp[s]);
+      st = mfma(a, qh[s], st);
+      st = mfma(a, ql[s], st);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sc[4 * t + i] = T0 + 16 * t + 4 * kq + i < len ? st[i] * inv : kNegInf;
+  }
+
+  // Value grids of the lane's eight tokens (j < 4: tile 0, token 4 kq + j; j >= 4: tile 1, 4 kq + j - 4).
+  float vsf[8], ev[8];
+  f16x8 vzp;
+  if constexpr (F::kQuant) {
+    const h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+    uint32_t sw[4] = {c.vs[0].x, c.vs[0].y, c.vs[1].x, c.vs[1].y};
+    uint32_t zw[4] = {c.vz[0].x, c.vz[0].y, c.vz[1].x, c.vz[1].y};
+    if (T0 + kChunk > len) {  // the row's last chunk: grids past the end may hold anything
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (T0 + 16 * (j >> 2) + 4 * kq + (j & 3) >= len) {
+          const uint32_t keep = (j & 1) ? 0x0000ffffu : 0xffff0000u;
+          sw[j >> 1] &= keep;
+          zw[j >> 1] &= keep;
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t bits = (j & 1) ? (sw[j >> 1] >> 16) : (sw[j >> 1] & 0xffffu);
+      vsf[j] = (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+      ev[j] = (float)((int)((bits >> 10) & 31u) - 14);  // vscale < 2^ev
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const h2 z = __builtin_bit_cast(h2, zw[j]) + k1024;
+      vzp[2 * j] = z.x;
+      vzp[2 * j + 1] = z.y;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      vsf[j] = 1.0f;
+      ev[j] = 0.0f;
+    }
+  }
+  after_scores();
+
+  // ---- online softmax of row n over this chunk (8 scores here, 24 on the row's other lanes) -------------
+  float mx = kNegInf;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) mx = fmaxf(mx, sc[j] + ev[j]);
+  mx = fmaxf(mx, shfl_xor_f(mx, 16));
+  mx = fmaxf(mx, shfl_xor_f(mx, 32));
+  const bool move = mx > m + kSlack;
+  if (__any(move)) {
+    const float mn = move ? mx : m;
+    const float alpha = move ? fast_exp2(m - mn) : 1.0f;  // 0 when m was -inf
+    l *= alpha;
+#pragma unroll
+    for (int mu = 0; mu < 8; ++mu) o[mu] *= alpha;
+    m = mn;
+  }
+  const float base = (m == kNegInf ? 0.0f : m) - kBias;
+  T ph, pl;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float e = fast_exp2(sc[j] - base);
+    l += e;
+    const float w = e * vsf[j];
+    const E hi = (E)w;
+    ph[j] = hi;
+    pl[j] = (E)(w - (float)hi);
+  }
+
+  // ---- O^T += V^T W^T: eight M-tiles -------------------------------------------------------------------
+  if constexpr (FMT == kKivi8) {
+    uint32_t lo[2][4], hi[2][4];  // [tile][j]: channel 8 n' + j (lo) or 8 n' + 4 + j (hi); bytes = tokens
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      transpose4(c.v[t][0][0], c.v[t][1][0], c.v[t][2][0], c.v[t][3][0], lo[t]);
+      transpose4(c.v[t][0][1], c.v[t][1][1], c.v[t][2][1], c.v[t][3][1], hi[t]);
+    }
+#pragma unroll
+    for (int mu = 0; mu < 8; ++mu) {
+      const uint32_t d0 = mu < 4 ? lo[0][mu & 3] : hi[0][mu & 3];
+      const uint32_t d1 = mu < 4 ? lo[1][mu & 3] : hi[1][mu & 3];
+      const f16x8 a = bytes8_minus(d0, d1, vzp);
+      o[mu] = mfma(a, ph, o[mu]);
+      o[mu] = mfma(a, pl, o[mu]);
+    }
+  } else if constexpr (FMT == kKivi4) {
+    uint32_t tr[2][4];  // [tile][j]: byte 4 n' + j of the tile's four tokens (channels 4 n' + j, 64 + 4 n' + j)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) transpose4(c.v[t][0][0], c.v[t][1][0], c.v[t][2][0], c.v[t][3][0], tr[t]);
+#pragma unroll
+    for (int mu = 0; mu < 8; ++mu) {
+      const uint32_t d0 = mu < 4 ? tr[0][mu] & 0x0F0F0F0Fu : (tr[0][mu & 3] >> 4) & 0x0F0F0F0Fu;
+      const uint32_t d1 = mu < 4 ? tr[1][mu] & 0x0F0F0F0Fu : (tr[1][mu & 3] >> 4) & 0x0F0F0F0Fu;
+      const f16x8 a = bytes8_minus(d0, d1, vzp);
+      o[mu] = mfma(a, ph, o[mu]);
+      o[mu] = mfma(a, pl, o[mu]);
+    }
+  } else {
+    // Halves: token pair (i, i + 1) of tile t at channel 8 n' + mu, as one dword.
+#pragma unroll
+    for (int mu = 0; mu < 8; ++mu) {
+      const uint32_t sel = (mu & 1) ? 0x07060302u : 0x05040100u;
+      const int wd = mu >> 1;
+      const u32x4 r = {__builtin_amdgcn_perm(c.v[0][1][wd], c.v[0][0][wd], sel),
+                       __builtin_amdgcn_perm(c.v[0][3][wd], c.v[0][2][wd], sel),
+                       __builtin_amdgcn_perm(c.v[1][1][wd], c.v[1][0][wd], sel),
+                       __builtin_amdgcn_perm(c.v[1][3][wd], c.v[1][2][wd], sel)};
+      const T a = __builtin_bit_cast(T, r);
+      o[mu] = mfma(a, ph, o[mu]);
+      o[mu] = mfma(a, pl, o[mu]);
+    }
+  }
+}
+
+// This lane's fold inputs: q of row fr (h * G + fr), channels fc .. fc + CPL - 1, unscaled; zero past G.
+template <int RP, int CPL>
+__device__ __forceinline__ void load_q_fold(const KiviParams& p, int b, int h, int lane, float (&qf)[CPL]) {
+  constexpr int LPR = 64 / RP;
+  const int fr = lane / LPR;
+  const bool in = fr < p.G;
+  const int64_t base = (int64_t)b * p.q_sb + (int64_t)(h * p.G + (in ? fr : 0)) * p.q_sh + (lane % LPR) * CPL;
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const float x = load_float(p.q, base + c, p.q_dtype);
+    qf[c] = in ? x : 0.0f;
+  }
+}
+
+__device__ __forceinline__ int64_t out_index(const KiviParams& p, int b, int hq, int j) {
+  return (int64_t)b * p.o_sb + (int64_t)hq * p.o_sh + (int64_t)j * p.o_ss;
+}
+
+__device__ __forceinline__ int64_t lse_index(const KiviParams& p, int b, int hq, int j) {
+  return (int64_t)b * p.l_sb + (int64_t)hq * p.l_sh + (int64_t)j * p.l_ss;
+}
+
+constexpr float kLn2 = 0.69314718055994531f;
+
+// Splits past a row's length: out 0, lse -inf (workgroups take the rows round-robin).
+template <int NT>
+__device__ __forceinline__ void zero_empty_splits(const KiviParams& p, const int* s_prefix) {
+  constexpr int D = kHeadDim;
+  for (int b = blockIdx.x; b < p.B; b += gridDim.x) {
+    const int nb = s_prefix[b + 1] - s_prefix[b];
+    const int active = (nb + p.cps - 1) / p.cps;
+    const int per_head = (p.S - active) * D;
+    for (int i = threadIdx.x; i < p.Hq * per_head; i += NT) {
+      const int hq = i / per_head;
+      const int r = i - hq * per_head;
+      const int j = active + r / D;
+      const int ch = r % D;
+      p.out[out_index(p, b, hq, j) + ch] = 0.0f;
+      if (ch == 0) p.lse[lse_index(p, b, hq, j)] = kNegInf;
+    }
+  }
+}
+
+// Count this workgroup's arrival at split segment `seg`; the last of its n pieces to arrive combines them
+// (slots: the piece of workgroup gg is in slot 2 gg if it was that workgroup's first piece, else 2 gg + 1),
+// writes the split's out and lse (natural log) and resets the counter.
+template <int NT>
+__device__ __forceinline__ void arrive_and_combine(const KiviParams& p, int seg, int b, int h, int j, int64_t sc0,
+                                                   int64_t per, int64_t g_first, int n, int tid, int* s_flag) {
+  constexpr int D = kHeadDim;
+  if (tid == 0) {
+    const unsigned prev = __hip_atomic_fetch_add(p.counters + seg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *s_flag = prev == (unsigned)n - 1u;
+  }
+  __syncthreads();
+  if (!*s_flag) return;
+  ws_acquire();
+  const int G = p.G;
+  for (int idx = tid; idx < G * D; idx += NT) {
+    const int r = idx / D;
+    const int ch = idx - r * D;
+    float M = kNegInf, W = 0.0f, O = 0.0f;
+    for (int i0 = 0; i0 < n; i0 += 4) {
+      float lv[4], ov[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t gg = g_first + i0 + i;
+        const int64_t slot = (i0 + i == 0 && sc0 != gg * per) ? 2 * gg + 1 : 2 * gg;
+        const bool in = i0 + i < n;
+        lv[i] = in ? ws_load(p.ws_lse + slot * G + r) : kNegInf;
+        ov[i] = in ? ws_load(p.ws_out + (slot * G + r) * D + ch) : 0.0f;
+      }
+      float bm = fmaxf(fmaxf(lv[0], lv[1]), fmaxf(lv[2], lv[3]));
+      const float nm = fmaxf(M, bm);
+      const float mu = nm == kNegInf ? 0.0f : nm;
+      const float alpha = W > 0.0f ? fast_exp2(M - mu) : 0.0f;
+      W *= alpha;
+      O *= alpha;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float e = fast_exp2(lv[i] - mu);
+        W += e;
+        O = fmaf(e, ov[i], O);
+      }
+      M = nm;
+    }
+    const int hq = h * G + r;
+    p.out[out_index(p, b, hq, j) + ch] = W > 0.0f ? O / W : 0.0f;
+    if (ch == 0) p.lse[lse_index(p, b, hq, j)] = W > 0.0f ? (M + __log2f(W)) * kLn2 : kNegInf;
+  }
+  if (tid == 0) __hip_atomic_store(p.counters + seg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace
+
+template <int FMT, int RP>
+__global__ __launch_bounds__(kDecodeWaves * 64, 2) void kivi_decode_kernel(const KiviParams p) {
+  constexpr int NW = kDecodeWaves;
+  constexpr int NT = NW * 64;
+  constexpr int D = kHeadDim;
+  constexpr int LPR = 64 / RP;
+  constexpr int CPL = D / LPR;
+  typedef KF<FMT> F;
+  typedef typename F::T T;
+
+  extern __shared__ int s_dyn[];  // [B + 1] chunks per sequence (exclusive prefix sum), then [B] lengths
+  int* s_prefix = s_dyn;
+  int* s_len = s_dyn + p.B + 1;
+  __shared__ int s_wsum[NW];
+  __shared__ int s_last;
+  __shared__ __align__(16) uint16_t s_qh[NW][RP][D];  // score operands, high parts, contraction order
+  __shared__ __align__(16) uint16_t s_ql[NW][RP][D];  // and remainders
+  __shared__ __align__(16) uint16_t s_kz[NW][D];      // 1024 + key zero (f16), contraction order
+  __shared__ float s_inv[NW][RP];
+  __shared__ float s_m[NW][RP];
+  __shared__ float s_l[NW][RP];
+  __shared__ float s_o[NW][RP][D];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = sread(tid >> 6);
+  const int kq = lane >> 4, n = lane & 15;
+  const int B = p.B;
+  const int HR = p.Hkv;
+  const int G = p.G;
+
+  build_segment_line<NW, kChunk>(p, s_prefix, s_len, s_wsum);
+  zero_empty_splits<NT>(p, s_prefix);
+
+  // ---- this workgroup's range of chunks on the line of (sequence, KV head) segments ---------------------
+  const int64_t C = (int64_t)HR * s_prefix[B];
+  if (C == 0) return;
+  const int64_t per = (C + gridDim.x - 1) / gridDim.x;
+  const int64_t g = blockIdx.x;
+  const int64_t c_begin = g * per;
+  if (c_begin >= C) return;
+  const int64_t c_end = min(c_begin + per, C);
+  int64_t c = c_begin;
+
+  int b;
+  {
+    int lo = 0, hi = B - 1;  // largest b with HR * prefix[b] <= c
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if ((int64_t)HR * s_prefix[mid] <= c) lo = mid; else hi = mid - 1;
+    }
+    b = sread(lo);
+  }
+  int nb = sread(s_prefix[b + 1] - s_prefix[b]);
+  int h, k;
+  {
+    const int64_t r = c - (int64_t)HR * s_prefix[b];
+    h = sread((int)(r / nb));
+    k = sread((int)(r - (int64_t)h * nb));
+  }
+
+  // Chunks [k, k_end) of (b, h) form this piece: up to the split's end, the segment's end or the range's.
+  auto piece_end = [&](int k0, int64_t c0) {
+    const int split_end = min((k0 / p.cps + 1) * p.cps, nb);
+    const int64_t seg_c0 = (int64_t)HR * s_prefix[b] + (int64_t)h * nb;
+    return k0 + (int)(min(c_end, seg_c0 + split_end) - c0);
+  };
+
+  float qf[CPL];
+  KChunk<FMT, CPL> cr;
+  int len = sread(s_len[b]);
+  load_q_fold<RP, CPL>(p, b, h, lane, qf);
+  {
+    const int k_end = piece_end(k, c);
+    if (k + wave < k_end) {
+      issue_k<FMT, RP, CPL>(p, b, h, k + wave, len, lane, cr);
+      issue_v<FMT, CPL>(p, b, h, k + wave, len, lane, cr);
+    }
+  }
+
+  for (;;) {
+    const int j_cur = k / p.cps;
+    const int k_end = piece_end(k, c);
+    const int64_t seg_c0 = (int64_t)HR * s_prefix[b] + (int64_t)h * nb;
+    const int split_end = min((j_cur + 1) * p.cps, nb);
+
+    float m = kNegInf, l = 0.0f;
+    f32x4 o[8];
+#pragma unroll
+    for (int mu = 0; mu < 8; ++mu) o[mu] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    T qh[4], ql[4];
+    f16x8 kzp[4];
+    float inv = 0.0f;
+    if constexpr (!F::kQuant) {  // unquantized: one fold serves the whole piece
+      const uint32_t unit[CPL / 2] = {};
+      fold<FMT, RP, CPL>(qf, unit, unit, p.qscale, lane, s_qh[wave], s_ql[wave], s_kz[wave], s_inv[wave]);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      read_fold<FMT, RP>(n, kq, G, s_qh[wave], s_ql[wave], s_kz[wave], s_inv[wave], qh, ql, kzp, inv);
+    }
+
+    // Chunks k + wave, k + wave + NW, ... of this piece: chunk kk is in flight on entry to its iteration; the
+    // next chunk's grids and K go out once kk's scores are done, its V after kk's value products.
+    for (int kk = k + wave; kk < k_end;) {
+      const int kn = kk + NW;
+      if constexpr (F::kQuant) {
+        fold<FMT, RP, CPL>(qf, cr.gs, cr.gz, p.qscale, lane, s_qh[wave], s_ql[wave], s_kz[wave], s_inv[wave]);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        read_fold<FMT, RP>(n, kq, G, s_qh[wave], s_ql[wave], s_kz[wave], s_inv[wave], qh, ql, kzp, inv);
+      }
+      compute<FMT, CPL>(cr, kk, len, lane, qh, ql, kzp, inv, m, l, o, [&]() {
+        if (kn < k_end) issue_k<FMT, RP, CPL>(p, b, h, kn, len, lane, cr);
+      });
+      if (kn < k_end) issue_v<FMT, CPL>(p, b, h, kn, len, lane, cr);
+      kk = kn;
+      if constexpr (F::kQuant) __builtin_amdgcn_wave_barrier();  // the LDS fold buffers are rewritten next
+    }
+
+    // The next piece (if any): its first chunk (and q rows, for a new KV head) go in flight now.
+    const int b_cur = b, h_cur = h;
+    const int64_t c_piece = c;
+    const int64_t c_next = c + (k_end - k);
+    if (c_next < c_end) {
+      if (k_end < nb) {
+        k = k_end;  // the same (sequence, KV head): the next split
+      } else {
+        ++h;
+        k = 0;
+        if (h == HR) {
+          h = 0;
+          do {
+            ++b;
+          } while (s_prefix[b + 1] == s_prefix[b]);
+          b = sread(b);
+          nb = sread(s_prefix[b + 1] - s_prefix[b]);
+        }
+        len = sread(s_len[b]);
+        load_q_fold<RP, CPL>(p, b, h, lane, qf);
+      }
+      const int k_next_end = piece_end(k, c_next);
+      if (k + wave < k_next_end) {
+        issue_k<FMT, RP, CPL>(p, b, h, k + wave, len, lane, cr);
+        issue_v<FMT, CPL>(p, b, h, k + wave, len, lane, cr);
+      }
+    }
+
+    // This wave's state of row n: the four lanes' weight sums added, stored for the workgroup merge.
+    l += shfl_xor_f(l, 16);
+    l += shfl_xor_f(l, 32);
+    if (n < RP) {
+      if (kq == 0) {
+        s_m[wave][n] = m;
+        s_l[wave][n] = l;
+      }
+#pragma unroll
+      for (int mu = 0; mu < 8; ++mu) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s_o[wave][n][out_channel<FMT>(kq, i, mu)] = o[mu][i];
+      }
+    }
+    __syncthreads();
+
+    // ---- merge the waves; write the split's result, or this piece's partial ---------------------------
+    const int seg = (b_cur * HR + h_cur) * p.S + j_cur;
+    const int64_t sc0 = seg_c0 + (int64_t)j_cur * p.cps;
+    const int64_t g_first = sc0 / per;
+    const int64_t g_last = (seg_c0 + split_end - 1) / per;
+    const bool whole = g_first == g_last;
+    const int64_t slot = c_piece == c_begin ? 2 * g : 2 * g + 1;
+    for (int idx = tid; idx < RP * D; idx += NT) {
+      const int r = idx / D;
+      const int ch = idx - r * D;
+      if (r >= G) continue;
+      float M = kNegInf;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) M = fmaxf(M, s_m[w][r]);
+      const float mu = M == kNegInf ? 0.0f : M;
+      float L = 0.0f, A = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const float lw = s_l[w][r];
+        const float e = lw > 0.0f ? fast_exp2(s_m[w][r] - mu) : 0.0f;
+        L += lw * e;
+        A += lw > 0.0f ? s_o[w][r][ch] * e : 0.0f;
+      }
+      const float out = L > 0.0f ? A / L : 0.0f;
+      const float lse2 = L > 0.0f ? M - kBias + __log2f(L) : kNegInf;
+      if (whole) {
+        const int hq = h_cur * G + r;
+        p.out[out_index(p, b_cur, hq, j_cur) + ch] = out;
+        if (ch == 0) p.lse[lse_index(p, b_cur, hq, j_cur)] = L > 0.0f ? lse2 * kLn2 : kNegInf;
+      } else {
+        ws_store(p.ws_out + (slot * G + r) * D + ch, out);
+        if (ch == 0) ws_store(p.ws_lse + slot * G + r, lse2);
+      }
+    }
+    if (!whole) {
+      ws_publish();
+      __syncthreads();
+      arrive_and_combine<NT>(p, seg, b_cur, h_cur, j_cur, sc0, per, g_first, (int)(g_last - g_first + 1), tid, &s_last);
+    }
+    if (c_next >= c_end) break;
+    c = c_next;
+    __syncthreads();  // the LDS merge buffers are rewritten by the next piece
+  }
+}
+
+template <int FMT>
+static hipError_t launch_fmt(const KiviParams& p, hipStream_t stream) {
+  dim3 grid(p.grid), block(kDecodeWaves * 64);
+  const size_t lds = (size_t)(2 * p.B + 1) * sizeof(int);
+  if (p.G <= 2) hipLaunchKernelGGL((kivi_decode_kernel<FMT, 2>), grid, block, lds, stream, p);
+  else if (p.G <= 4) hipLaunchKernelGGL((kivi_decode_kernel<FMT, 4>), grid, block, lds, stream, p);
+  else if (p.G <= 8) hipLaunchKernelGGL((kivi_decode_kernel<FMT, 8>), grid, block, lds, stream, p);
+  else hipLaunchKernelGGL((kivi_decode_kernel<FMT, 16>), grid, block, lds, stream, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_kivi(const KiviParams& p, int fmt, hipStream_t stream) {
+  if (p.G < 1 || p.G > 16) return hipErrorInvalidValue;
+  switch (fmt) {
+    case kKivi4: return launch_fmt<kKivi4>(p, stream);
+    case kKivi8: return launch_fmt<kKivi8>(p, stream);
+    case kKiviF16: return launch_fmt<kKiviF16>(p, stream);
+    case kKiviBf16: return launch_fmt<kKiviBf16>(p, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace bpt

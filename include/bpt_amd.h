@@ -18,6 +18,11 @@
  *                        quant/w8a8.py:55-74 / kernels/reference.py:44-55 (per-token INT8, amax/127).
  *   bpt_decode_plan      kernels/kv_attention.py:178-187 default_split (tokens per program) and the
  *                        out/lse allocation of :218-220, as a host-only planning call.
+ *   bpt_kivi_decode      kernels/kv_attention.py:190-245 decode_attention (launcher) and :56-175 (the
+ *                        kernel) over kernels/reference.py:66-160's QuantKV (KIVI asymmetric 4/8-bit codes
+ *                        with float16 grids, or float16 / bfloat16 keys and values): one partial
+ *                        (out, lse) per split, as that launcher returns them.
+ *   bpt_kivi_plan        the workspace / counter sizing for bpt_kivi_decode (host only).
  */
 #ifndef BPT_AMD_H
 #define BPT_AMD_H
@@ -29,7 +34,7 @@
 extern "C" {
 #endif
 
-#define BPT_ABI_VERSION 2
+#define BPT_ABI_VERSION 3
 
 /* return codes */
 #define BPT_OK 0
@@ -151,6 +156,73 @@ typedef struct {
   int64_t scale_stride_block, scale_stride_token, scale_stride_head;
 } bpt_append_args;
 
+/* storage format of a KIVI cache (kernels/reference.py:66-100 QuantKV; bits 4, 8 or 16) */
+typedef enum {
+  BPT_KIVI_INT4 = 0, /* uint8 [B, Hkv, T, D/2]: channel d in the low nibble, d + D/2 in the high one      */
+  BPT_KIVI_INT8 = 1, /* uint8 [B, Hkv, T, D]                                                           */
+  BPT_KIVI_F16 = 2,  /* bits 16: float16 keys and values [B, Hkv, T, D], no grids                      */
+  BPT_KIVI_BF16 = 3  /* bits 16: bfloat16 keys and values, no grids                                    */
+} bpt_kivi_format;
+
+/*
+ * Decode attention of one query per head over a KIVI cache, one partial result per split.
+ *
+ *   q            [B, Hq, D] (strides q_stride_{b,h}; channel stride 1), BF16 / F16 / F32
+ *   k/v_codes    [B, Hkv, T, D] codes (INT4: D/2 bytes per token), strides code_stride_{b,h,t} in elements
+ *                of the stored type (bytes for INT4 / INT8, halves for F16 / BF16); channel stride 1
+ *   k_scale/zero float16 [B, Hkv, num_groups, D], strides kgrid_stride_{b,h,g}: the key grid of tokens
+ *                g*group .. g*group + group - 1 (INT4 / INT8 only); key = scale * (code - zero)
+ *   v_scale/zero float16 [B, Hkv, T], strides vgrid_stride_{b,h}: one grid per token; value likewise
+ *   lengths      [B] int32: tokens visible to each row's query (clamped to T and to num_splits * split)
+ *   out          float32 [B, Hq, S, D] (strides out_stride_{b,h,s}): split s's softmax-weighted average of
+ *                the values of tokens s*split .. min((s+1)*split, length) - 1, 0 for an empty split
+ *   lse          float32 [B, Hq, S] (strides lse_stride_{b,h,s}): log sum exp (natural log) of that split's
+ *                scores sm_scale * q.k, -inf for an empty split
+ *
+ * D = 128; Hq a multiple of Hkv with at most 16 query heads per KV head; split a multiple of 32 (and of
+ * group); for INT4 / INT8, group a multiple of 32, T a multiple of group and num_groups * group >= T.
+ * Every cached byte is read once for all query heads of its KV head. The tokens are shared out over the
+ * launched workgroups regardless of the split; a split that several workgroups cover is combined exactly
+ * in the same launch. Buffers: as for bpt_paged_decode (bpt_kivi_plan gives the sizes; counters zero
+ * before the first call and left zero by every call). Code tensors and grids must be 16-byte aligned,
+ * code strides multiples of 16 bytes, key-grid strides multiples of 8 elements and value-grid strides
+ * multiples of 4 elements.
+ */
+typedef struct {
+  uint32_t struct_size; /* sizeof(bpt_kivi_args) */
+  int32_t format;       /* bpt_kivi_format */
+  int32_t q_dtype;      /* bpt_float_dtype */
+  int32_t batch, num_q_heads, num_kv_heads, head_dim;
+  int32_t tokens;       /* T: tokens laid out per (sequence, KV head) */
+  int32_t group;        /* tokens per key grid */
+  int32_t num_groups;   /* key grids laid out per (sequence, KV head) */
+  int32_t split;        /* tokens per split */
+  int32_t num_splits;   /* S >= 1 */
+  int32_t grid_groups;  /* out of bpt_kivi_plan: workgroups launched */
+  float sm_scale;
+
+  const void* q;
+  int64_t q_stride_b, q_stride_h;
+  const void* k_codes;
+  const void* v_codes;
+  int64_t code_stride_b, code_stride_h, code_stride_t;
+  const void* k_scale; /* float16 */
+  const void* k_zero;
+  int64_t kgrid_stride_b, kgrid_stride_h, kgrid_stride_g;
+  const void* v_scale; /* float16 */
+  const void* v_zero;
+  int64_t vgrid_stride_b, vgrid_stride_h;
+  const int32_t* lengths;
+  float* out;
+  int64_t out_stride_b, out_stride_h, out_stride_s;
+  float* lse;
+  int64_t lse_stride_b, lse_stride_h, lse_stride_s;
+  void* workspace;
+  size_t workspace_bytes;
+  void* counters;
+  size_t counters_bytes;
+} bpt_kivi_args;
+
 /* ---- entry points ------------------------------------------------------------------------------- */
 
 /* Host-only: validate args, fill chunk_tokens / grid_groups, report the workspace and counter sizes in
@@ -162,6 +234,12 @@ int bpt_paged_decode(const bpt_decode_args* args, void* stream);
 
 /* Quantize-on-write of new K/V rows into their (page, slot). */
 int bpt_quant_append(const bpt_append_args* args, void* stream);
+
+/* Host-only: validate a KIVI call, fill grid_groups, report workspace and counter sizes in bytes. */
+int bpt_kivi_plan(bpt_kivi_args* args, size_t* workspace_bytes, size_t* counters_bytes);
+
+/* Decode attention over a KIVI cache: one launch, every split's (out, lse) written. */
+int bpt_kivi_decode(const bpt_kivi_args* args, void* stream);
 
 /* Thread-local message of the last failing call ("" when none). */
 const char* bpt_last_error(void);
