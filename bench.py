@@ -7,8 +7,9 @@ resident in HBM and the L2 / Infinity Cache evicted by a 1 GiB streaming read be
 the timed events). `value` = algorithmic KV bytes read per call / mean event-timed call duration.
 
 Also reported: the dominant kernel's roofline (HBM-bound; algorithmic bytes / its event-timed duration
-against 8 TB/s), the oracle timed on the host CPU over a bounded sample of the same workload, and
-µs/call + GB/s for all five measured shapes. Prints ONE JSON line.
+against 8 TB/s), the oracle timed on the host CPU over a bounded sample of the same workload, µs/call +
+GB/s for all five measured shapes, and the KIVI (contiguous 4/8/16-bit cache) decode at the shapes of
+fastserve's kernel-2 benchmark. Prints ONE JSON line.
 """
 
 from __future__ import annotations
@@ -57,20 +58,33 @@ def profile_pass(args) -> int:
     from bpt_amd import measure, paged_decode_attention, workloads
 
     torch.cuda.set_device(0)
-    w = workloads.make(args.workload, device="cuda:0", seed=0)
     flush = measure.ReadProbe(args.flush_bytes)
-    out = torch.empty(tuple(w.q.shape), dtype=torch.bfloat16, device="cuda:0")
-    pargs, kw = w.args(), w.kwargs()
-    for _ in range(args.warmup + args.steps):
-        flush.run()
-        paged_decode_attention(*pargs, **kw, out=out)
+    if args.workload.startswith("kivi-"):  # kivi-<int4|int8|bf16>-<batch>x<context>
+        from bpt_amd import kivi
+
+        fmt, shape = args.workload.split("-")[1:]
+        batch, context = (int(x) for x in shape.split("x"))
+        w = workloads.make_kivi(batch, context, {"int4": 4, "int8": 8, "bf16": 16}[fmt], device="cuda:0",
+                                seed=batch + context)
+        for _ in range(args.warmup + args.steps):
+            flush.run()
+            kivi.attend(w.q, w, w.lengths, workloads.HEAD_DIM**-0.5, tokens=context)
+        nbytes = w.cache_bytes()
+    else:
+        w = workloads.make(args.workload, device="cuda:0", seed=0)
+        out = torch.empty(tuple(w.q.shape), dtype=torch.bfloat16, device="cuda:0")
+        pargs, kw = w.args(), w.kwargs()
+        for _ in range(args.warmup + args.steps):
+            flush.run()
+            paged_decode_attention(*pargs, **kw, out=out)
+        nbytes = w.kv_bytes()
     torch.cuda.synchronize()
     src = torch.ones(64 << 20, dtype=torch.float32, device="cuda:0")
     dst = torch.empty_like(src)
     for _ in range(3):
         measure.copy_probe(dst, src, src.numel() * 4)
     torch.cuda.synchronize()
-    log(f"profile pass: {args.warmup + args.steps} decode calls ({w.kv_bytes()} KV bytes each), "
+    log(f"profile pass: {args.warmup + args.steps} decode calls ({nbytes} KV bytes each), "
         f"3 copies of {src.numel() * 4} bytes")
     return 0
 
@@ -159,6 +173,39 @@ def measure_workload(name: str, flush, iters: int, warmup: int) -> dict:
     return row
 
 
+def measure_kivi(flush, iters: int, warmup: int) -> dict:
+    """µs/call and GB/s of KIVI decode attention (attend: one launch, splits combined inside) at the shapes
+    and bit widths of fastserve's kernel-2 benchmark, cold caches, `tokens` known to the caller."""
+    import torch
+
+    from bpt_amd import kivi, workloads
+
+    table = {}
+    for batch, context in workloads.KIVI_SHAPES:
+        for bits in workloads.KIVI_BITS:
+            name = workloads.kivi_name(batch, context, bits)
+            w = workloads.make_kivi(batch, context, bits, device="cuda:0", seed=batch + context)
+            scale = workloads.HEAD_DIM**-0.5
+
+            def call():
+                kivi.attend(w.q, w, w.lengths, scale, tokens=context)
+
+            total, _ = timed_calls(call, flush, iters, warmup)
+            ms = statistics.fmean(total)
+            nbytes = w.cache_bytes()
+            table[name] = {
+                "us_per_call": round(ms * 1e3, 2),
+                "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                "pct_of_peak": round(100 * nbytes / (ms * 1e-3) / 1e9 / PEAK_GBPS, 1),
+                "cache_bytes": nbytes,
+                "split": kivi.default_split(batch, 8, context),
+            }
+            log(f"{name}: {table[name]['us_per_call']} us, {table[name]['gbps']} GB/s")
+            del w
+            torch.cuda.empty_cache()
+    return table
+
+
 def cpu_baseline(name: str, budget_s: float) -> dict:
     """The oracle (numpy float32) on the host over the first sequences of the same workload."""
     import numpy as np
@@ -215,6 +262,7 @@ def main() -> int:
     ap.add_argument("--workload", default="qwen3-1.7b-fp8")
     ap.add_argument("--flush-bytes", type=int, default=1 << 30)
     ap.add_argument("--no-configs", action="store_true", help="skip the five-shape table")
+    ap.add_argument("--no-kivi", action="store_true", help="skip the KIVI (contiguous 4/8/16-bit cache) table")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--profile", action="store_true", help="short run for rocprofv3 (no JSON line)")
@@ -318,6 +366,8 @@ def main() -> int:
             log(f"shape {name}")
             table[name] = measure_workload(name, flush, iters=20, warmup=5)
         result["configs"] = table
+    if not args.no_kivi:
+        result["kivi"] = measure_kivi(flush, iters=20, warmup=5)
     if not args.no_cpu_baseline:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(args.workload, args.cpu_seconds)

@@ -243,3 +243,74 @@ def to_oracle(w: Workload) -> dict:
         kv_format=fmt,
         scale=w.sm_scale,
     )
+
+
+# ---- KIVI caches (contiguous, fastserve's kernel-2 format) ------------------------------------------------
+
+# The shapes of fastserve's kernel-2 benchmark (experiments/m7.py:210-290, one Qwen3-1.7B attention layer:
+# 16 query / 8 KV heads, head dim 128), as (batch, context).
+KIVI_SHAPES = ((1, 32768), (4, 32768), (16, 2048), (64, 8192))
+KIVI_BITS = (4, 8, 16)
+
+
+@dataclass
+class KiviWorkload:
+    """A KIVI cache with QuantKV's fields (kernels/reference.py:66-100) plus the decode call's inputs."""
+
+    bits: int
+    group: int
+    k_codes: torch.Tensor
+    v_codes: torch.Tensor
+    k_scale: torch.Tensor | None
+    k_zero: torch.Tensor | None
+    v_scale: torch.Tensor | None
+    v_zero: torch.Tensor | None
+    q: torch.Tensor  # [B, Hq, D] bf16
+    lengths: torch.Tensor  # [B] int32, every row full
+    context: int
+
+    def cache_bytes(self) -> int:
+        """Bytes the cache occupies for `context` tokens per row, grids included: what one call reads
+        (experiments/m7.py:207-208 cache_bytes)."""
+        ts = [self.k_codes, self.v_codes, self.k_scale, self.k_zero, self.v_scale, self.v_zero]
+        return sum(t.numel() * t.element_size() for t in ts if t is not None)
+
+
+def kivi_name(batch: int, context: int, bits: int) -> str:
+    return f"kivi-{'int4' if bits == 4 else 'int8' if bits == 8 else 'bf16'}-{batch}x{context}"
+
+
+def make_kivi(batch: int, context: int, bits: int, device="cuda", seed: int = 0, q_heads: int = 16,
+              kv_heads: int = 8, group: int = 32) -> KiviWorkload:
+    """Random codes and grids of the right format (timing input; parity is tested on quantized data).
+
+    bits 4 / 8: uniform codes, key scales U[0.01, 0.1] per channel per group with integer zero points, value
+    scales likewise per token; bits 16: bfloat16 N(0, 1) keys and values.
+    """
+    gen = torch.Generator(device=device).manual_seed(seed)
+    d = HEAD_DIM
+    shape = (batch, kv_heads, context, d)
+    q = torch.randn((batch, q_heads, d), generator=gen, device=device).to(torch.bfloat16)
+    lengths = torch.full((batch,), context, dtype=torch.int32, device=device)
+    if bits == 16:
+        k = torch.randn(shape, generator=gen, device=device).to(torch.bfloat16)
+        v = torch.randn(shape, generator=gen, device=device).to(torch.bfloat16)
+        return KiviWorkload(16, group, k, v, None, None, None, None, q, lengths, context)
+    levels = 2**bits
+    width = d // 2 if bits == 4 else d
+    codes = lambda: torch.randint(0, 256, (batch, kv_heads, context, width), generator=gen, device=device,  # noqa: E731
+                                  dtype=torch.uint8)
+    groups = context // group
+
+    def scale(*s):
+        return (torch.rand(s, generator=gen, device=device) * 0.09 + 0.01).to(torch.float16)
+
+    def zero(*s):
+        return torch.randint(0, levels, s, generator=gen, device=device).to(torch.float16)
+
+    return KiviWorkload(
+        bits, group, codes(), codes(),
+        scale(batch, kv_heads, groups, d), zero(batch, kv_heads, groups, d),
+        scale(batch, kv_heads, context), zero(batch, kv_heads, context),
+        q, lengths, context,
+    )

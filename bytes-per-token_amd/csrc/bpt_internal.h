@@ -113,7 +113,7 @@ struct KiviParams {
   unsigned* counters;  // [B * Hkv * S] arrivals per (sequence, KV head, split); zero between calls
   int B, Hq, Hkv, G, S;
   int cps;      // chunks per split
-  int gpc;      // chunks per key group
+  int gshift;   // log2(chunks per key group)
   int len_cap;  // lengths are clamped to this (the laid-out tokens, and the splits' reach)
   int grid;
   float qscale;  // sm_scale * log2(e)

@@ -157,10 +157,13 @@ int make_kivi_plan(const bpt_kivi_args* a, KiviPlan* pl) {
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: split %d must be a multiple of %d tokens", fn, a->split,
                 bpt::kMfmaChunk);
   if (a->num_splits < 1) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: num_splits must be >= 1", fn);
+  if (a->tokens % bpt::kMfmaChunk)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: the cache's %d tokens must be a multiple of %d", fn, a->tokens,
+                bpt::kMfmaChunk);
   if (quant) {
-    if (a->group % bpt::kMfmaChunk)
-      return fail(BPT_ERR_INVALID_ARGUMENT, "%s: key group %d must be a multiple of %d tokens", fn, a->group,
-                  bpt::kMfmaChunk);
+    if (a->group % bpt::kMfmaChunk || !is_pow2(a->group))
+      return fail(BPT_ERR_INVALID_ARGUMENT, "%s: key group %d must be a power of two of at least %d tokens", fn,
+                  a->group, bpt::kMfmaChunk);
     if (a->tokens % a->group)
       return fail(BPT_ERR_INVALID_ARGUMENT, "%s: %d tokens are not a whole number of groups of %d", fn, a->tokens,
                   a->group);
@@ -311,6 +314,10 @@ int bpt_kivi_decode(const bpt_kivi_args* a, void* stream) {
                 a->vgrid_stride_h % 4))
     return fail(BPT_ERR_INVALID_ARGUMENT,
                 "%s: grids must be 16-byte aligned, key-grid strides multiples of 8 and value-grid strides of 4", fn);
+  // One (sequence, KV head)'s codes and grids are addressed with 32-bit offsets.
+  if ((int64_t)a->tokens * a->code_stride_t * pl.eb >= (int64_t)1 << 31 ||
+      (quant && (int64_t)a->num_groups * a->kgrid_stride_g >= (int64_t)1 << 30))
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: one KV head's codes or grids span 2 GiB or more", fn);
   if (!a->workspace || a->workspace_bytes < pl.workspace || ((uintptr_t)a->workspace & 255u))
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: a 256-byte aligned workspace of %zu bytes is required (got %zu)", fn,
                 pl.workspace, a->workspace_bytes);
@@ -354,7 +361,7 @@ int bpt_kivi_decode(const bpt_kivi_args* a, void* stream) {
   p.G = pl.G;
   p.S = a->num_splits;
   p.cps = a->split / bpt::kMfmaChunk;
-  p.gpc = quant ? a->group / bpt::kMfmaChunk : 1;
+  p.gshift = quant ? log2i(a->group / bpt::kMfmaChunk) : 0;
   p.len_cap = pl.len_cap;
   p.grid = pl.grid;
   p.qscale = a->sm_scale * bpt::kLog2e;

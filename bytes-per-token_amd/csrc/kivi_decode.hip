@@ -20,7 +20,8 @@
 //    layout through LDS. Each row's score is the MFMA result times sm_scale * log2(e) / that power of two.
 //  * online softmax in base 2 per row (the row's four lanes agree through two shuffles). Each token's value
 //    scale is folded into its weight, w = 2^(s - base) * vscale; the reference point tracks the largest
-//    s + log2(vscale) bound, so every w stays below 2^12 (inside f16) whatever the value scales.
+//    score plus a power-of-two bound on the chunk's value scales, so every w stays below 2^12 (inside f16)
+//    whatever the value scales.
 //  * output O^T += V^T W^T, contraction over the lane's own eight score tokens. V^T comes from 4 x 4 byte
 //    (or 2 x 2 half) transposes, turned into code - value zero exactly as for keys; W = f16 high part plus
 //    remainder, two MFMAs per M-tile.
@@ -89,9 +90,18 @@ __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
 __device__ __forceinline__ uint32_t pair_lo(uint32_t w) { return __builtin_amdgcn_perm(0x64006400u, w, 0x07010500u); }
 __device__ __forceinline__ uint32_t pair_hi(uint32_t w) { return __builtin_amdgcn_perm(0x64006400u, w, 0x07030502u); }
 
-__device__ __forceinline__ f16x8 bytes8_minus(uint32_t w0, uint32_t w1, f16x8 z) {
-  const u32x4 r = {pair_lo(w0), pair_hi(w0), pair_lo(w1), pair_hi(w1)};
-  return __builtin_bit_cast(f16x8, r) - z;
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t sub_h2(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, a) - __builtin_bit_cast(h2, b));
+}
+
+// (1024 + byte) - z, pair by pair (packed f16 subtractions): the code minus its zero point, exactly. The zero
+// points z travel as f16 pairs in plain dwords.
+__device__ __forceinline__ f16x8 bytes8_minus(uint32_t w0, uint32_t w1, const uint32_t (&z)[4]) {
+  const u32x4 r = {sub_h2(pair_lo(w0), z[0]), sub_h2(pair_hi(w0), z[1]), sub_h2(pair_lo(w1), z[2]),
+                   sub_h2(pair_hi(w1), z[3])};
+  return __builtin_bit_cast(f16x8, r);
 }
 
 // 4 x 4 byte transpose: w[i] byte j -> o[j] byte i.
@@ -106,66 +116,89 @@ __device__ __forceinline__ void transpose4(uint32_t w0, uint32_t w1, uint32_t w2
   o[3] = __builtin_amdgcn_perm(t3, t2, 0x07060302u);
 }
 
-template <int FMT, int CPL>
-__device__ __forceinline__ int64_t head_codes(const KiviParams& p, int b, int h) {
-  return (int64_t)b * p.c_sb + (int64_t)h * p.c_sh;
+// The (sequence, KV head)'s tensors (wave-uniform) and this lane's constant offsets into them (32-bit:
+// one head's codes and grids span less than 2 GiB, checked on the host).
+struct Head {
+  const uint8_t* k;
+  const uint8_t* v;
+  const uint16_t* ks;
+  const uint16_t* kz;
+  const uint16_t* vs;
+  const uint16_t* vz;
+};
+
+struct LaneOffsets {
+  uint32_t k, v;  // bytes: K row of token n at byte 16 kq * (K loads); V row of token 4 kq at byte n * (V bytes)
+  uint32_t g;     // elements: this lane's fold channels in a key grid
+  uint32_t t;     // elements: token 4 kq in a value grid
+};
+
+__device__ __forceinline__ Head head_of(const KiviParams& p, int b, int h) {
+  const int64_t c = (int64_t)b * p.c_sb + (int64_t)h * p.c_sh;
+  const int64_t g = (int64_t)b * p.g_sb + (int64_t)h * p.g_sh;
+  const int64_t t = (int64_t)b * p.t_sb + (int64_t)h * p.t_sh;
+  return Head{p.kc + c, p.vc + c, p.ks + g, p.kz + g, p.vs + t, p.vz + t};
+}
+
+template <int FMT, int RP, int CPL>
+__device__ __forceinline__ LaneOffsets lane_offsets(const KiviParams& p, int lane) {
+  typedef KF<FMT> F;
+  const uint32_t st = (uint32_t)p.c_st;
+  const int kq = lane >> 4, n = lane & 15;
+  return LaneOffsets{n * st + kq * (16 * F::kKU4), 4 * kq * st + n * (4 * F::kVWords), (uint32_t)((lane % (64 / RP)) * CPL),
+                     (uint32_t)(4 * kq)};
 }
 
 // Chunk kk's key-grid, K and value-grid loads (issued together, in the order they are consumed) and its V
-// loads. Tokens at or past len read the row's last token instead (valid memory; their weights are zero).
-template <int FMT, int RP, int CPL>
-__device__ __forceinline__ void issue_k(const KiviParams& p, int b, int h, int kk, int len, int lane, KChunk<FMT, CPL>& c) {
+// loads. The chunk's 32 tokens all lie inside the laid-out T (a multiple of 32); those at or past the
+// row's length are masked after loading.
+template <int FMT, int CPL>
+__device__ __forceinline__ void issue_k(const KiviParams& p, const Head& hd, const LaneOffsets& lo, int kk, KChunk<FMT, CPL>& c) {
   typedef KF<FMT> F;
-  constexpr int LPR = 64 / RP;
-  const int T0 = kk * kChunk;
-  const int kq = lane >> 4, n = lane & 15;
+  const uint32_t T0 = (uint32_t)kk * kChunk;
+  const uint32_t st = (uint32_t)p.c_st;
   if constexpr (F::kQuant) {
-    const int grp = kk / p.gpc;
-    const int64_t go = (int64_t)b * p.g_sb + (int64_t)h * p.g_sh + (int64_t)grp * p.g_sg + (lane % LPR) * CPL;
+    const uint32_t go = (uint32_t)(kk >> p.gshift) * (uint32_t)p.g_sg + lo.g;
     if constexpr (CPL == 4) {
-      const u32x2 s = *(const u32x2*)(p.ks + go);
-      const u32x2 z = *(const u32x2*)(p.kz + go);
+      const u32x2 s = *(const u32x2*)(hd.ks + go);
+      const u32x2 z = *(const u32x2*)(hd.kz + go);
       c.gs[0] = s.x; c.gs[1] = s.y;
       c.gz[0] = z.x; c.gz[1] = z.y;
     } else {
 #pragma unroll
       for (int j = 0; j < CPL / 8; ++j) {
-        const u32x4 s = *(const u32x4*)(p.ks + go + 8 * j);
-        const u32x4 z = *(const u32x4*)(p.kz + go + 8 * j);
+        const u32x4 s = *(const u32x4*)(hd.ks + go + 8 * j);
+        const u32x4 z = *(const u32x4*)(hd.kz + go + 8 * j);
         c.gs[4 * j] = s.x; c.gs[4 * j + 1] = s.y; c.gs[4 * j + 2] = s.z; c.gs[4 * j + 3] = s.w;
         c.gz[4 * j] = z.x; c.gz[4 * j + 1] = z.y; c.gz[4 * j + 2] = z.z; c.gz[4 * j + 3] = z.w;
       }
     }
   }
-  const uint8_t* base = p.kc + head_codes<FMT, CPL>(p, b, h) + kq * (16 * F::kKU4);
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    const int tok = min(T0 + 16 * t + n, len - 1);
+    const uint32_t off = lo.k + (T0 + 16 * t) * st;
 #pragma unroll
-    for (int j = 0; j < F::kKU4; ++j) c.k[t][j] = load16(base + (int64_t)tok * p.c_st + 16 * j);
+    for (int j = 0; j < F::kKU4; ++j) c.k[t][j] = load16(hd.k + off + 16 * j);
   }
   if constexpr (F::kQuant) {
-    const int64_t to = (int64_t)b * p.t_sb + (int64_t)h * p.t_sh + T0 + 4 * kq;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      c.vs[t] = *(const u32x2*)(p.vs + to + 16 * t);
-      c.vz[t] = *(const u32x2*)(p.vz + to + 16 * t);
+      c.vs[t] = *(const u32x2*)(hd.vs + T0 + 16 * t + lo.t);
+      c.vz[t] = *(const u32x2*)(hd.vz + T0 + 16 * t + lo.t);
     }
   }
 }
 
 template <int FMT, int CPL>
-__device__ __forceinline__ void issue_v(const KiviParams& p, int b, int h, int kk, int len, int lane, KChunk<FMT, CPL>& c) {
+__device__ __forceinline__ void issue_v(const KiviParams& p, const Head& hd, const LaneOffsets& lo, int kk, KChunk<FMT, CPL>& c) {
   typedef KF<FMT> F;
-  const int T0 = kk * kChunk;
-  const int kq = lane >> 4, n = lane & 15;
-  const uint8_t* base = p.vc + head_codes<FMT, CPL>(p, b, h) + n * (4 * F::kVWords);
+  const uint32_t T0 = (uint32_t)kk * kChunk;
+  const uint32_t st = (uint32_t)p.c_st;
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int tok = min(T0 + 16 * t + 4 * kq + i, len - 1);
-      const uint8_t* src = base + (int64_t)tok * p.c_st;
+      const uint8_t* src = hd.v + (lo.v + (T0 + 16 * t + i) * st);
       if constexpr (F::kVWords == 1) {
         c.v[t][i][0] = __builtin_nontemporal_load((const uint32_t*)src);
       } else if constexpr (F::kVWords == 2) {
@@ -241,31 +274,34 @@ __device__ __forceinline__ void fold(const float (&qf)[CPL], const uint32_t (&gs
   if ((lane % LPR) == 0) s_inv[fr] = qscale / f;
 }
 
-// Row n's score operands for the four K-steps (zero past the G rows) and, for codes, 1024 + key zero in
-// this lane's contraction order.
+// Row n's score operands for the four K-steps, its score factor (0 past the G rows) and, for codes,
+// 1024 + key zero in this lane's contraction order.
 template <int FMT, int RP>
 __device__ __forceinline__ void read_fold(int n, int kq, int G, const uint16_t (*s_qh)[kHeadDim],
                                           const uint16_t (*s_ql)[kHeadDim], const uint16_t* s_kz, const float* s_inv,
-                                          typename KF<FMT>::T (&qh)[4], typename KF<FMT>::T (&ql)[4], f16x8 (&kzp)[4],
-                                          float& inv) {
+                                          typename KF<FMT>::T (&qh)[4], typename KF<FMT>::T (&ql)[4],
+                                          uint32_t (&kzp)[4][4], float& inv) {
   typedef typename KF<FMT>::T T;
   const bool in = n < G;
-  const int r = in ? n : 0;
+  const int r = in ? n : 0;  // padded rows compute row 0's scores, scaled by 0 and never stored
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    const u32x4 h = *(const u32x4*)&s_qh[r][32 * kq + 8 * s];
-    const u32x4 l = *(const u32x4*)&s_ql[r][32 * kq + 8 * s];
-    const u32x4 zero = {0u, 0u, 0u, 0u};
-    qh[s] = __builtin_bit_cast(T, in ? h : zero);
-    ql[s] = __builtin_bit_cast(T, in ? l : zero);
-    if constexpr (KF<FMT>::kQuant) kzp[s] = *(const f16x8*)&s_kz[32 * kq + 8 * s];
+    qh[s] = *(const T*)&s_qh[r][32 * kq + 8 * s];
+    ql[s] = *(const T*)&s_ql[r][32 * kq + 8 * s];
+    if constexpr (KF<FMT>::kQuant) {
+      const u32x4 z = *(const u32x4*)&s_kz[32 * kq + 8 * s];
+      kzp[s][0] = z.x;
+      kzp[s][1] = z.y;
+      kzp[s][2] = z.z;
+      kzp[s][3] = z.w;
+    }
   }
   inv = in ? s_inv[r] : 0.0f;
 }
 
 // Score operand A of K-step s, tile t: code - zero (quantized) or the stored halves.
 template <int FMT, int CPL>
-__device__ __forceinline__ typename KF<FMT>::T k_operand(const KChunk<FMT, CPL>& c, int t, int s, f16x8 kz) {
+__device__ __forceinline__ typename KF<FMT>::T k_operand(const KChunk<FMT, CPL>& c, int t, int s, const uint32_t (&kz)[4]) {
   typedef typename KF<FMT>::T T;
   if constexpr (FMT == kKivi8) {
     const U4 q = c.k[t][s >> 1];
@@ -285,12 +321,11 @@ __device__ __forceinline__ typename KF<FMT>::T k_operand(const KChunk<FMT, CPL>&
 // lane's partial weight sum), o[mu] (row n, channels out_channel(kq, i, mu)).
 template <int FMT, int CPL, typename AfterScores>
 __device__ __forceinline__ void compute(KChunk<FMT, CPL>& c, int kk, int len, int lane, const typename KF<FMT>::T (&qh)[4],
-                                        const typename KF<FMT>::T (&ql)[4], const f16x8 (&kzp)[4], float inv, float& m,
+                                        const typename KF<FMT>::T (&ql)[4], const uint32_t (&kzp)[4][4], float inv, float& m,
                                         float& l, f32x4 (&o)[8], AfterScores after_scores) {
   typedef KF<FMT> F;
   typedef typename F::T T;
   typedef typename F::E E;
-  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
   const int T0 = kk * kChunk;
   const int kq = lane >> 4;
   float sc[8];
@@ -304,51 +339,60 @@ __device__ __forceinline__ void compute(KChunk<FMT, CPL>& c, int kk, int len, in
       st = mfma(a, ql[s], st);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sc[4 * t + i] = T0 + 16 * t + 4 * kq + i < len ? st[i] * inv : kNegInf;
+    for (int i = 0; i < 4; ++i) sc[4 * t + i] = st[i] * inv;
   }
 
   // Value grids of the lane's eight tokens (j < 4: tile 0, token 4 kq + j; j >= 4: tile 1, 4 kq + j - 4).
-  float vsf[8], ev[8];
-  f16x8 vzp;
+  uint32_t sw[4] = {0u, 0u, 0u, 0u}, zw[4] = {0u, 0u, 0u, 0u};
   if constexpr (F::kQuant) {
-    const h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
-    uint32_t sw[4] = {c.vs[0].x, c.vs[0].y, c.vs[1].x, c.vs[1].y};
-    uint32_t zw[4] = {c.vz[0].x, c.vz[0].y, c.vz[1].x, c.vz[1].y};
-    if (T0 + kChunk > len) {  // the row's last chunk: grids past the end may hold anything
+    sw[0] = c.vs[0].x; sw[1] = c.vs[0].y; sw[2] = c.vs[1].x; sw[3] = c.vs[1].y;
+    zw[0] = c.vz[0].x; zw[1] = c.vz[0].y; zw[2] = c.vz[1].x; zw[3] = c.vz[1].y;
+  }
+  if (T0 + kChunk > len) {  // the row's last chunk: tokens past its length are loaded but may hold anything
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        if (T0 + 16 * (j >> 2) + 4 * kq + (j & 3) >= len) {
+    for (int j = 0; j < 8; ++j) {
+      if (T0 + 16 * (j >> 2) + 4 * kq + (j & 3) >= len) {
+        sc[j] = kNegInf;
+        if constexpr (F::kQuant) {
           const uint32_t keep = (j & 1) ? 0x0000ffffu : 0xffff0000u;
           sw[j >> 1] &= keep;
           zw[j >> 1] &= keep;
+        } else {
+#pragma unroll
+          for (int w = 0; w < F::kVWords; ++w) c.v[j >> 2][j & 3][w] = 0u;  // finite values under weight 0
         }
       }
     }
+  }
+  float vsf[8];
+  float ev = 0.0f;  // this lane's tokens have value scales below 2^ev
+  uint32_t vzp[4];  // 1024 + value zero of the lane's eight tokens, as f16 pairs
+  if constexpr (F::kQuant) {
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    const u16x2 m01 = __builtin_elementwise_max(__builtin_bit_cast(u16x2, sw[0]), __builtin_bit_cast(u16x2, sw[1]));
+    const u16x2 m23 = __builtin_elementwise_max(__builtin_bit_cast(u16x2, sw[2]), __builtin_bit_cast(u16x2, sw[3]));
+    const u16x2 mm = __builtin_elementwise_max(m01, m23);
+    const uint32_t top = mm.x > mm.y ? mm.x : mm.y;  // positive f16: bit order is value order
+    ev = (float)((int)((top >> 10) & 31u) - 14);
+    const h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const uint32_t bits = (j & 1) ? (sw[j >> 1] >> 16) : (sw[j >> 1] & 0xffffu);
       vsf[j] = (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
-      ev[j] = (float)((int)((bits >> 10) & 31u) - 14);  // vscale < 2^ev
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const h2 z = __builtin_bit_cast(h2, zw[j]) + k1024;
-      vzp[2 * j] = z.x;
-      vzp[2 * j + 1] = z.y;
-    }
+    for (int j = 0; j < 4; ++j) vzp[j] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, zw[j]) + k1024);
   } else {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      vsf[j] = 1.0f;
-      ev[j] = 0.0f;
-    }
+    for (int j = 0; j < 8; ++j) vsf[j] = 1.0f;
   }
   after_scores();
 
   // ---- online softmax of row n over this chunk (8 scores here, 24 on the row's other lanes) -------------
   float mx = kNegInf;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) mx = fmaxf(mx, sc[j] + ev[j]);
+  for (int j = 0; j < 8; ++j) mx = fmaxf(mx, sc[j]);
+  mx += ev;
   mx = fmaxf(mx, shfl_xor_f(mx, 16));
   mx = fmaxf(mx, shfl_xor_f(mx, 32));
   const bool move = mx > m + kSlack;
@@ -464,8 +508,8 @@ __device__ __forceinline__ void zero_empty_splits(const KiviParams& p, const int
 // (slots: the piece of workgroup gg is in slot 2 gg if it was that workgroup's first piece, else 2 gg + 1),
 // writes the split's out and lse (natural log) and resets the counter.
 template <int NT>
-__device__ __forceinline__ void arrive_and_combine(const KiviParams& p, int seg, int b, int h, int j, int64_t sc0,
-                                                   int64_t per, int64_t g_first, int n, int tid, int* s_flag) {
+__device__ __forceinline__ void arrive_and_combine(const KiviParams& p, int seg, int b, int h, int j, int sc0,
+                                                   int per, int g_first, int n, int tid, int* s_flag) {
   constexpr int D = kHeadDim;
   if (tid == 0) {
     const unsigned prev = __hip_atomic_fetch_add(p.counters + seg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -483,7 +527,7 @@ __device__ __forceinline__ void arrive_and_combine(const KiviParams& p, int seg,
       float lv[4], ov[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int64_t gg = g_first + i0 + i;
+        const int gg = g_first + i0 + i;
         const int64_t slot = (i0 + i == 0 && sc0 != gg * per) ? 2 * gg + 1 : 2 * gg;
         const bool in = i0 + i < n;
         lv[i] = in ? ws_load(p.ws_lse + slot * G + r) : kNegInf;
@@ -547,55 +591,57 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void kivi_decode_kernel(const
   zero_empty_splits<NT>(p, s_prefix);
 
   // ---- this workgroup's range of chunks on the line of (sequence, KV head) segments ---------------------
-  const int64_t C = (int64_t)HR * s_prefix[B];
+  const int C = HR * s_prefix[B];  // < 2^31, checked on the host
   if (C == 0) return;
-  const int64_t per = (C + gridDim.x - 1) / gridDim.x;
-  const int64_t g = blockIdx.x;
-  const int64_t c_begin = g * per;
+  const int per = (C + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int g = blockIdx.x;
+  const int c_begin = g * per;
   if (c_begin >= C) return;
-  const int64_t c_end = min(c_begin + per, C);
-  int64_t c = c_begin;
+  const int c_end = min(c_begin + per, C);
+  int c = c_begin;
 
   int b;
   {
     int lo = 0, hi = B - 1;  // largest b with HR * prefix[b] <= c
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
-      if ((int64_t)HR * s_prefix[mid] <= c) lo = mid; else hi = mid - 1;
+      if (HR * s_prefix[mid] <= c) lo = mid; else hi = mid - 1;
     }
     b = sread(lo);
   }
   int nb = sread(s_prefix[b + 1] - s_prefix[b]);
   int h, k;
   {
-    const int64_t r = c - (int64_t)HR * s_prefix[b];
-    h = sread((int)(r / nb));
-    k = sread((int)(r - (int64_t)h * nb));
+    const int r = c - HR * s_prefix[b];
+    h = sread(r / nb);
+    k = sread(r - h * nb);
   }
 
   // Chunks [k, k_end) of (b, h) form this piece: up to the split's end, the segment's end or the range's.
-  auto piece_end = [&](int k0, int64_t c0) {
+  auto piece_end = [&](int k0, int c0) {
     const int split_end = min((k0 / p.cps + 1) * p.cps, nb);
-    const int64_t seg_c0 = (int64_t)HR * s_prefix[b] + (int64_t)h * nb;
-    return k0 + (int)(min(c_end, seg_c0 + split_end) - c0);
+    const int seg_c0 = HR * s_prefix[b] + h * nb;
+    return k0 + (min(c_end, seg_c0 + split_end) - c0);
   };
 
   float qf[CPL];
   KChunk<FMT, CPL> cr;
+  const LaneOffsets lo = lane_offsets<FMT, RP, CPL>(p, lane);
+  Head hd = head_of(p, b, h);
   int len = sread(s_len[b]);
   load_q_fold<RP, CPL>(p, b, h, lane, qf);
   {
     const int k_end = piece_end(k, c);
     if (k + wave < k_end) {
-      issue_k<FMT, RP, CPL>(p, b, h, k + wave, len, lane, cr);
-      issue_v<FMT, CPL>(p, b, h, k + wave, len, lane, cr);
+      issue_k<FMT, CPL>(p, hd, lo, k + wave, cr);
+      issue_v<FMT, CPL>(p, hd, lo, k + wave, cr);
     }
   }
 
   for (;;) {
     const int j_cur = k / p.cps;
     const int k_end = piece_end(k, c);
-    const int64_t seg_c0 = (int64_t)HR * s_prefix[b] + (int64_t)h * nb;
+    const int seg_c0 = HR * s_prefix[b] + h * nb;
     const int split_end = min((j_cur + 1) * p.cps, nb);
 
     float m = kNegInf, l = 0.0f;
@@ -603,7 +649,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void kivi_decode_kernel(const
 #pragma unroll
     for (int mu = 0; mu < 8; ++mu) o[mu] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     T qh[4], ql[4];
-    f16x8 kzp[4];
+    uint32_t kzp[4][4];
     float inv = 0.0f;
     if constexpr (!F::kQuant) {  // unquantized: one fold serves the whole piece
       const uint32_t unit[CPL / 2] = {};
@@ -626,17 +672,17 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void kivi_decode_kernel(const
         read_fold<FMT, RP>(n, kq, G, s_qh[wave], s_ql[wave], s_kz[wave], s_inv[wave], qh, ql, kzp, inv);
       }
       compute<FMT, CPL>(cr, kk, len, lane, qh, ql, kzp, inv, m, l, o, [&]() {
-        if (kn < k_end) issue_k<FMT, RP, CPL>(p, b, h, kn, len, lane, cr);
+        if (kn < k_end) issue_k<FMT, CPL>(p, hd, lo, kn, cr);
       });
-      if (kn < k_end) issue_v<FMT, CPL>(p, b, h, kn, len, lane, cr);
+      if (kn < k_end) issue_v<FMT, CPL>(p, hd, lo, kn, cr);
       kk = kn;
       if constexpr (F::kQuant) __builtin_amdgcn_wave_barrier();  // the LDS fold buffers are rewritten next
     }
 
     // The next piece (if any): its first chunk (and q rows, for a new KV head) go in flight now.
     const int b_cur = b, h_cur = h;
-    const int64_t c_piece = c;
-    const int64_t c_next = c + (k_end - k);
+    const int c_piece = c;
+    const int c_next = c + (k_end - k);
     if (c_next < c_end) {
       if (k_end < nb) {
         k = k_end;  // the same (sequence, KV head): the next split
@@ -652,12 +698,13 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void kivi_decode_kernel(const
           nb = sread(s_prefix[b + 1] - s_prefix[b]);
         }
         len = sread(s_len[b]);
+        hd = head_of(p, b, h);
         load_q_fold<RP, CPL>(p, b, h, lane, qf);
       }
       const int k_next_end = piece_end(k, c_next);
       if (k + wave < k_next_end) {
-        issue_k<FMT, RP, CPL>(p, b, h, k + wave, len, lane, cr);
-        issue_v<FMT, CPL>(p, b, h, k + wave, len, lane, cr);
+        issue_k<FMT, CPL>(p, hd, lo, k + wave, cr);
+        issue_v<FMT, CPL>(p, hd, lo, k + wave, cr);
       }
     }
 
@@ -679,11 +726,11 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void kivi_decode_kernel(const
 
     // ---- merge the waves; write the split's result, or this piece's partial ---------------------------
     const int seg = (b_cur * HR + h_cur) * p.S + j_cur;
-    const int64_t sc0 = seg_c0 + (int64_t)j_cur * p.cps;
-    const int64_t g_first = sc0 / per;
-    const int64_t g_last = (seg_c0 + split_end - 1) / per;
+    const int sc0 = seg_c0 + j_cur * p.cps;
+    const int g_first = sc0 / per;
+    const int g_last = (seg_c0 + split_end - 1) / per;
     const bool whole = g_first == g_last;
-    const int64_t slot = c_piece == c_begin ? 2 * g : 2 * g + 1;
+    const int slot = c_piece == c_begin ? 2 * g : 2 * g + 1;
     for (int idx = tid; idx < RP * D; idx += NT) {
       const int r = idx / D;
       const int ch = idx - r * D;
@@ -714,7 +761,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void kivi_decode_kernel(const
     if (!whole) {
       ws_publish();
       __syncthreads();
-      arrive_and_combine<NT>(p, seg, b_cur, h_cur, j_cur, sc0, per, g_first, (int)(g_last - g_first + 1), tid, &s_last);
+      arrive_and_combine<NT>(p, seg, b_cur, h_cur, j_cur, sc0, per, g_first, g_last - g_first + 1, tid, &s_last);
     }
     if (c_next >= c_end) break;
     c = c_next;

@@ -179,8 +179,9 @@ typedef enum {
  *   lse          float32 [B, Hq, S] (strides lse_stride_{b,h,s}): log sum exp (natural log) of that split's
  *                scores sm_scale * q.k, -inf for an empty split
  *
- * D = 128; Hq a multiple of Hkv with at most 16 query heads per KV head; split a multiple of 32 (and of
- * group); for INT4 / INT8, group a multiple of 32, T a multiple of group and num_groups * group >= T.
+ * D = 128; Hq a multiple of Hkv with at most 16 query heads per KV head; T and split multiples of 32
+ * (split also of group); for INT4 / INT8, group a power of two of at least 32, T a multiple of group and
+ * num_groups * group >= T. One KV head's codes must span less than 2 GiB.
  * Every cached byte is read once for all query heads of its KV head. The tokens are shared out over the
  * launched workgroups regardless of the split; a split that several workgroups cover is combined exactly
  * in the same launch. Buffers: as for bpt_paged_decode (bpt_kivi_plan gives the sizes; counters zero
