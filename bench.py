@@ -8,8 +8,9 @@ the timed events). `value` = algorithmic KV bytes read per call / mean event-tim
 
 Also reported: the dominant kernel's roofline (HBM-bound; algorithmic bytes / its event-timed duration
 against 8 TB/s), the oracle timed on the host CPU over a bounded sample of the same workload, µs/call +
-GB/s for all five measured shapes, and the KIVI (contiguous 4/8/16-bit cache) decode at the shapes of
-fastserve's kernel-2 benchmark. Prints ONE JSON line.
+GB/s for all five measured shapes, the KIVI (contiguous 4/8/16-bit cache) decode at the shapes of
+fastserve's kernel-2 benchmark, and the fused RMSNorm + INT8 quantizer at the shapes of its kernel-1
+benchmark. Prints ONE JSON line.
 """
 
 from __future__ import annotations
@@ -206,6 +207,42 @@ def measure_kivi(flush, iters: int, warmup: int) -> dict:
     return table
 
 
+def measure_norm_quant(flush, iters: int, warmup: int) -> dict:
+    """RMSNorm + per-token INT8 at the shapes of fastserve's kernel-1 benchmark (bf16, d = 1024 / 2048,
+    1 .. 32768 rows): cold µs/call and GB/s of the bytes it must move (2d read + d + 4 written per row),
+    and µs/call replayed from a graph (the launch-bound decode sizes)."""
+    import torch
+
+    from bpt_amd import measure, rms_norm_int8
+
+    table = {}
+    for d in (1024, 2048):
+        gen = torch.Generator(device="cuda:0").manual_seed(d)
+        weight = (torch.randn(d, generator=gen, device="cuda:0").abs() + 0.5).to(torch.bfloat16)
+        for rows in (1, 16, 256, 4096, 32768):
+            x = (torch.randn((rows, d), generator=gen, device="cuda:0") * 3).to(torch.bfloat16)
+            out = (torch.empty((rows, d), dtype=torch.int8, device="cuda:0"),
+                   torch.empty(rows, dtype=torch.float32, device="cuda:0"))
+
+            def call():
+                rms_norm_int8(x, weight, 1e-6, out=out)
+
+            total, _ = timed_calls(call, flush, iters, warmup)
+            graph = measure.graph_time_ms(call, calls=20, warmup=2, iters=10)
+            ms = statistics.fmean(total)
+            moved = rows * (2 * d + d + 4)
+            name = f"norm-int8-{rows}x{d}"
+            table[name] = {
+                "us_per_call": round(ms * 1e3, 2),
+                "us_per_call_graph": round(statistics.median(graph) * 1e3, 2),
+                "gbps": round(moved / (ms * 1e-3) / 1e9, 1),
+                "bytes_moved": moved,
+            }
+            log(f"{name}: {table[name]['us_per_call']} us cold, {table[name]['us_per_call_graph']} us in a graph, "
+                f"{table[name]['gbps']} GB/s")
+    return table
+
+
 def cpu_baseline(name: str, budget_s: float) -> dict:
     """The oracle (numpy float32) on the host over the first sequences of the same workload."""
     import numpy as np
@@ -263,6 +300,7 @@ def main() -> int:
     ap.add_argument("--flush-bytes", type=int, default=1 << 30)
     ap.add_argument("--no-configs", action="store_true", help="skip the five-shape table")
     ap.add_argument("--no-kivi", action="store_true", help="skip the KIVI (contiguous 4/8/16-bit cache) table")
+    ap.add_argument("--no-norm", action="store_true", help="skip the RMSNorm + INT8 table")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--profile", action="store_true", help="short run for rocprofv3 (no JSON line)")
@@ -368,6 +406,8 @@ def main() -> int:
         result["configs"] = table
     if not args.no_kivi:
         result["kivi"] = measure_kivi(flush, iters=20, warmup=5)
+    if not args.no_norm:
+        result["norm_quant"] = measure_norm_quant(flush, iters=20, warmup=5)
     if not args.no_cpu_baseline:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(args.workload, args.cpu_seconds)

@@ -163,6 +163,23 @@ class KiviArgs(ctypes.Structure):
     ]
 
 
+class NormQuantArgs(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("x_dtype", _i32),
+        ("weight_dtype", _i32),
+        ("rows", _i32),
+        ("d", _i32),
+        ("eps", ctypes.c_float),
+        ("x", _vp),
+        ("x_stride_row", _i64),
+        ("weight", _vp),
+        ("codes", _vp),
+        ("codes_stride_row", _i64),
+        ("scale", _vp),
+    ]
+
+
 # Every symbol include/bpt_amd.h declares, with its ctypes signature.
 SIGNATURES = {
     "bpt_decode_plan": (
@@ -176,6 +193,7 @@ SIGNATURES = {
         [ctypes.POINTER(KiviArgs), ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)],
     ),
     "bpt_kivi_decode": (_i32, [ctypes.POINTER(KiviArgs), _vp]),
+    "bpt_rms_norm_int8": (_i32, [ctypes.POINTER(NormQuantArgs), _vp]),
     "bpt_last_error": (ctypes.c_char_p, []),
     "bpt_abi_version": (_i32, []),
     "bpt_fp8_decode_table": (_i32, [_vp, _vp]),
@@ -184,7 +202,7 @@ SIGNATURES = {
     "bpt_copy_probe": (_i32, [_vp, _vp, ctypes.c_uint64, _vp]),
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 class BptError(RuntimeError):

@@ -120,6 +120,19 @@ struct KiviParams {
   int q_dtype;
 };
 
+// Launch-ready form of bpt_norm_quant_args.
+struct NormQuantParams {
+  const void* x;
+  int64_t x_rs;  // elements between rows (channel stride 1)
+  const void* w;
+  int8_t* codes;
+  int64_t c_rs;
+  float* scale;
+  int rows, d;
+  float eps;
+  int x_dtype, w_dtype;
+};
+
 // KIVI storage formats of bpt_kivi_args.bits / kv_dtype.
 constexpr int kKivi4 = 0;
 constexpr int kKivi8 = 1;
@@ -131,6 +144,7 @@ int decode_chunk_tokens(int kv_dtype, int rows_per_group);
 hipError_t launch_decode(const DecodeParams& p, int kv_dtype, int scale_kind, int rows_per_group, hipStream_t stream);
 hipError_t launch_decode_mfma(const DecodeParams& p, int kv_dtype, int scale_kind, hipStream_t stream);
 hipError_t launch_kivi(const KiviParams& p, int fmt, hipStream_t stream);
+hipError_t launch_norm_quant(const NormQuantParams& p, bool vec8, hipStream_t stream);
 hipError_t launch_append(const AppendParams& p, int kv_dtype, int scale_kind, int head_dim, hipStream_t stream);
 hipError_t launch_fp8_table(float* out, hipStream_t stream);
 hipError_t launch_fp8_encode(const float* x, float scale, uint8_t* out, int64_t n, hipStream_t stream);

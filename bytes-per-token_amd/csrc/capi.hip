@@ -371,6 +371,43 @@ int bpt_kivi_decode(const bpt_kivi_args* a, void* stream) {
   return BPT_OK;
 }
 
+int bpt_rms_norm_int8(const bpt_norm_quant_args* a, void* stream) {
+  const char* fn = "bpt_rms_norm_int8";
+  if (!a) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: args is NULL", fn);
+  if (a->struct_size != sizeof(bpt_norm_quant_args))
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: struct_size %u != %zu (stale binding)", fn, a->struct_size,
+                sizeof(bpt_norm_quant_args));
+  if (a->x_dtype < BPT_F_BF16 || a->x_dtype > BPT_F_F32 || a->weight_dtype < BPT_F_BF16 || a->weight_dtype > BPT_F_F32)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: x and weight must be bf16, f16 or f32", fn);
+  if (a->rows < 0 || a->d < 1) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: rows >= 0 and d >= 1", fn);
+  if (!(a->eps >= 0.0f) || !std::isfinite(a->eps)) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: eps must be finite and >= 0", fn);
+  if (a->rows == 0) return BPT_OK;
+  if (!a->x || !a->weight || !a->codes || !a->scale)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: x, weight, codes and scale must be non-NULL", fn);
+  if (a->x_stride_row < a->d || a->codes_stride_row < a->d)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: row strides must be at least d", fn);
+  const int xb = float_bytes(a->x_dtype), wb = float_bytes(a->weight_dtype);
+  // 8 elements per lane per step when every row and the weight start on 16 bytes (codes on 8).
+  const bool vec8 = a->d % 8 == 0 && aligned16(a->x) && (a->x_stride_row * xb) % 16 == 0 && aligned16(a->weight) &&
+                    ((uintptr_t)a->codes % 8) == 0 && a->codes_stride_row % 8 == 0;
+  (void)wb;
+  bpt::NormQuantParams p;
+  p.x = a->x;
+  p.x_rs = a->x_stride_row;
+  p.w = a->weight;
+  p.codes = a->codes;
+  p.c_rs = a->codes_stride_row;
+  p.scale = a->scale;
+  p.rows = a->rows;
+  p.d = a->d;
+  p.eps = a->eps;
+  p.x_dtype = a->x_dtype;
+  p.w_dtype = a->weight_dtype;
+  hipError_t e = bpt::launch_norm_quant(p, vec8, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(fn, e);
+  return BPT_OK;
+}
+
 int bpt_quant_append(const bpt_append_args* a, void* stream) {
   const char* fn = "bpt_quant_append";
   if (!a) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: args is NULL", fn);

@@ -23,6 +23,8 @@
  *                        with float16 grids, or float16 / bfloat16 keys and values): one partial
  *                        (out, lse) per split, as that launcher returns them.
  *   bpt_kivi_plan        the workspace / counter sizing for bpt_kivi_decode (host only).
+ *   bpt_rms_norm_int8    kernels/norm_quant.py:43-109 rms_norm_int8 (kernel 1), defined by
+ *                        kernels/reference.py:44-55: RMSNorm fused with per-token INT8 quantization.
  */
 #ifndef BPT_AMD_H
 #define BPT_AMD_H
@@ -34,7 +36,7 @@
 extern "C" {
 #endif
 
-#define BPT_ABI_VERSION 3
+#define BPT_ABI_VERSION 4
 
 /* return codes */
 #define BPT_OK 0
@@ -224,6 +226,27 @@ typedef struct {
   size_t counters_bytes;
 } bpt_kivi_args;
 
+/*
+ * RMSNorm + per-token symmetric INT8, one pass over each row, float32 arithmetic:
+ *   y = x * rsqrt(mean(x^2) + eps) * weight;  scale = max(max|y| / 127, 1e-12);
+ *   codes = clamp(round_half_even(y / scale), -128, 127)
+ *   x       [rows, d] (row stride x_stride_row elements, channel stride 1), BF16 / F16 / F32
+ *   weight  [d], BF16 / F16 / F32
+ *   codes   int8 [rows, d] (row stride codes_stride_row), scale float32 [rows]
+ */
+typedef struct {
+  uint32_t struct_size; /* sizeof(bpt_norm_quant_args) */
+  int32_t x_dtype, weight_dtype; /* bpt_float_dtype */
+  int32_t rows, d;
+  float eps;
+  const void* x;
+  int64_t x_stride_row;
+  const void* weight;
+  int8_t* codes;
+  int64_t codes_stride_row;
+  float* scale;
+} bpt_norm_quant_args;
+
 /* ---- entry points ------------------------------------------------------------------------------- */
 
 /* Host-only: validate args, fill chunk_tokens / grid_groups, report the workspace and counter sizes in
@@ -241,6 +264,9 @@ int bpt_kivi_plan(bpt_kivi_args* args, size_t* workspace_bytes, size_t* counters
 
 /* Decode attention over a KIVI cache: one launch, every split's (out, lse) written. */
 int bpt_kivi_decode(const bpt_kivi_args* args, void* stream);
+
+/* RMSNorm fused with per-token INT8 quantization (one launch). */
+int bpt_rms_norm_int8(const bpt_norm_quant_args* args, void* stream);
 
 /* Thread-local message of the last failing call ("" when none). */
 const char* bpt_last_error(void);
