@@ -152,6 +152,21 @@ def measure_workload(name: str, flush, iters: int, warmup: int) -> dict:
         ub = w.kv_bytes(unique=True)
         row["unique_kv_bytes"] = ub
         row["unique_gbps"] = round(ub / (med * 1e-3) / 1e9, 1)
+        # The shared-prefix cascade over the same inputs: the prefix read once per 16 query rows of the
+        # group, each sequence's own pages once, the two merged (two launches).
+        from bpt_amd import cascade_decode_attention
+
+        def cascade():
+            cascade_decode_attention(*args, **kw, prefix_pages=w.shape.shared_prefix_pages, out=out)
+
+        ctot, _ = timed_calls(cascade, flush, iters, warmup)
+        cmed = statistics.median(ctot)
+        row["cascade"] = {
+            "us_per_call": round(cmed * 1e3, 2),
+            "graph_warm_us_per_call": round(statistics.median(measure.graph_time_ms(cascade, calls=10, warmup=2, iters=10)) * 1e3, 2),
+            "unique_gbps": round(ub / (cmed * 1e-3) / 1e9, 1),
+            "logical_gbps": round(nbytes / (cmed * 1e-3) / 1e9, 1),
+        }
     if name == "qwen3-1.7b-int8":
         # The step's quantize-on-write: one new row per sequence into slot 15 of its last page.
         b, hkv = w.shape.batch, w.shape.kv_heads

@@ -9,11 +9,13 @@ it has not been built.
 """
 
 from . import kivi
+from .cascade import cascade_decode_attention
 from .kv_cache import OutOfBlocksError, PagedMeta, PagedQuantKVCache
 from .norm_quant import rms_norm_int8
 from .paged_attention import decode_kernel_name, decode_plan, kv_read_bytes, paged_decode_attention, quantize_append
 
 __all__ = [
+    "cascade_decode_attention",
     "OutOfBlocksError",
     "PagedMeta",
     "PagedQuantKVCache",

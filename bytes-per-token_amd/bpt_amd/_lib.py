@@ -73,7 +73,15 @@ class DecodeArgs(ctypes.Structure):
         ("workspace_bytes", ctypes.c_size_t),
         ("counters", _vp),
         ("counters_bytes", ctypes.c_size_t),
+        ("flags", _i32),
+        ("len_offset", _i32),
+        ("lse_out", _vp),
+        ("merge_out", _vp),
+        ("merge_lse", _vp),
     ]
+
+
+DECODE_NONCAUSAL = 1
 
 
 class AppendArgs(ctypes.Structure):
@@ -202,7 +210,7 @@ SIGNATURES = {
     "bpt_copy_probe": (_i32, [_vp, _vp, ctypes.c_uint64, _vp]),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 
 class BptError(RuntimeError):

@@ -103,8 +103,9 @@ def _decode_args(
     _require(block_table.dim() == 2 and block_table.shape[0] == b, f"block_table must be [{b}, max_blocks]")
     _require(block_table.dtype in _INDEX_CODES, "block_table must be int32 or int64")
     _require(block_table.stride(1) == 1, "block_table rows must be contiguous")
-    _require(context_lens.dim() == 1 and context_lens.shape[0] == b, f"context_lens must be [{b}]")
-    _require(context_lens.dtype == torch.int32 and context_lens.is_contiguous(), "context_lens must be contiguous int32")
+    if context_lens is not None:
+        _require(context_lens.dim() == 1 and context_lens.shape[0] == b, f"context_lens must be [{b}]")
+        _require(context_lens.dtype == torch.int32 and context_lens.is_contiguous(), "context_lens must be contiguous int32")
     _require(out_dtype in _FLOAT_CODES, f"out dtype must be bf16, f16 or f32, got {out_dtype}")
     scale_kind, sc_strides = _scale_layout(k_scale, v_scale, kv_code, k_cache.shape)
 
@@ -129,7 +130,7 @@ def _decode_args(
     a.scale_stride_block, a.scale_stride_token, a.scale_stride_head = sc_strides
     a.block_table = block_table.data_ptr()
     a.table_stride_b = block_table.stride(0)
-    a.context_lens = context_lens.data_ptr()
+    a.context_lens = _ptr(context_lens)
     return a, (b, nq, hq, d)
 
 
@@ -195,6 +196,8 @@ def paged_decode_attention(
     out_dtype: torch.dtype = torch.bfloat16,
     workspace: torch.Tensor | None = None,
     counters: torch.Tensor | None = None,
+    lse: torch.Tensor | None = None,
+    _cascade: dict | None = None,
 ) -> torch.Tensor:
     """softmax(q kᵀ · scale) v over each sequence's paged cache, dequantized in registers.
 
@@ -209,6 +212,9 @@ def paged_decode_attention(
     workspace     optional device buffer of at least decode_plan(...)[2] bytes for the split-K partials
     counters      optional device buffer of at least decode_plan(...)[3] bytes, zero-filled before its first
                   use (every call leaves it zeroed); default for both: cached per (device, stream)
+    lse           optional contiguous float32 [B, Q, Hq] (or [B, Hq]) receiving each row's log-sum-exp of
+                  scale * q.k over the tokens it saw (natural log, -inf for none): with `out` in float32 it is
+                  the partial that kernels/reference.py:205-211 merges
 
     Returns out [B, Q, Hq, D] (or [B, Hq, D]) in `out_dtype` (bf16 by default). One kernel launch.
     """
@@ -231,6 +237,21 @@ def paged_decode_attention(
         _require(out4.stride(-1) == 1 and out4.device == dev, "out must be a cuda tensor with contiguous channels")
     a.out = out4.data_ptr()
     a.out_stride_b, a.out_stride_q, a.out_stride_h = out4.stride(0), out4.stride(1), out4.stride(2)
+    if lse is not None:
+        _require(lse.dtype == torch.float32 and lse.is_contiguous() and lse.numel() == b * nq * hq and lse.device == dev,
+                 f"lse must be a contiguous float32 tensor of {b} x {nq} x {hq} on q's device")
+        a.lse_out = lse.data_ptr()
+    if _cascade is not None:  # the cascade's two launches (cascade.py): flags, length offset, partial to merge
+        a.flags = _cascade.get("flags", 0)
+        a.len_offset = _cascade.get("len_offset", 0)
+        merge = _cascade.get("merge")
+        if merge is not None:
+            m_out, m_lse = merge
+            _require(m_out.dtype == torch.float32 and m_out.is_contiguous() and tuple(m_out.shape) == (b, nq, hq, d),
+                     "the merged partial must be contiguous float32 [B, Q, Hq, D]")
+            _require(m_lse.dtype == torch.float32 and m_lse.is_contiguous() and m_lse.numel() == b * nq * hq,
+                     "the merged partial's lse must be contiguous float32 [B, Q, Hq]")
+            a.merge_out, a.merge_lse = m_out.data_ptr(), m_lse.data_ptr()
     lib = _lib.lib()
     ws_bytes, cnt_bytes = ctypes.c_size_t(0), ctypes.c_size_t(0)
     _lib.check(lib.bpt_decode_plan(ctypes.byref(a), ctypes.byref(ws_bytes), ctypes.byref(cnt_bytes)))

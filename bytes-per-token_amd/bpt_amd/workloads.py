@@ -105,9 +105,9 @@ def quantize_per_token_int8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor
 
 
 def make(name: str = DEFAULT, device="cuda", seed: int = 0, batch: int | None = None,
-         length_cap: int | None = None) -> Workload:
-    """Build workload `name` on `device`. `batch` / `length_cap` shrink it (tests); defaults are full size."""
-    shape = SHAPES[name]
+         length_cap: int | None = None, shape: Shape | None = None) -> Workload:
+    """Build workload `name` (or the given `shape`) on `device`. `batch` / `length_cap` shrink it (tests)."""
+    shape = SHAPES[name] if shape is None else shape
     gen = torch.Generator().manual_seed(seed)
     b = batch if batch is not None else shape.batch
     lengths = _lengths(shape, gen, b)

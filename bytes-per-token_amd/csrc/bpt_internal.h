@@ -70,6 +70,11 @@ struct DecodeParams {
   int64_t per_forced;  // chunks per workgroup when the caller fixed the split count, else 0
   float qscale;      // sm_scale * log2(e)
   int q_dtype, out_dtype, table_i64;
+  int noncausal;        // every query sees all of its sequence's tokens
+  int len_offset;       // subtracted from every context length
+  float* lse_out;       // optional [B, Q, Hq]: each row's log-sum-exp (natural log)
+  const float* merge_out;  // optional [B, Q, Hq, D]: another token range's normalized partial, merged into out
+  const float* merge_lse;  // its log-sum-exp [B, Q, Hq] (natural log, -inf when empty)
 };
 
 struct AppendParams {
@@ -115,6 +120,7 @@ struct KiviParams {
   int cps;      // chunks per split
   int gshift;   // log2(chunks per key group)
   int len_cap;  // lengths are clamped to this (the laid-out tokens, and the splits' reach)
+  int len_offset;  // always 0 here (the paged decode's parameter of the same name)
   int grid;
   float qscale;  // sm_scale * log2(e)
   int q_dtype;

@@ -219,8 +219,12 @@ int bpt_paged_decode(const bpt_decode_args* a, void* stream) {
   int rc = make_plan(a, &pl);
   if (rc) return rc;
   if (a->batch == 0) return BPT_OK;
-  if (!a->q || !a->k_cache || !a->v_cache || !a->block_table || !a->context_lens || !a->out)
-    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: q, caches, block_table, context_lens and out must be non-NULL", fn);
+  if (!a->q || !a->k_cache || !a->v_cache || !a->block_table || !a->out)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: q, caches, block_table and out must be non-NULL", fn);
+  if ((a->merge_out == nullptr) != (a->merge_lse == nullptr))
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: merge_out and merge_lse go together", fn);
+  if (a->flags & ~BPT_DECODE_NONCAUSAL) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: unknown flags %d", fn, a->flags);
+  if (a->len_offset < 0) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: len_offset must be >= 0", fn);
   if (a->kv_dtype != BPT_KV_BF16 && (!a->k_scale || !a->v_scale))
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: k_scale and v_scale are required for a quantized cache", fn);
   const int eb = a->kv_dtype == BPT_KV_BF16 ? 2 : 1;
@@ -279,6 +283,11 @@ int bpt_paged_decode(const bpt_decode_args* a, void* stream) {
   p.q_dtype = a->q_dtype;
   p.out_dtype = a->out_dtype;
   p.table_i64 = a->table_dtype == BPT_IDX_I64;
+  p.noncausal = (a->flags & BPT_DECODE_NONCAUSAL) != 0;
+  p.len_offset = a->len_offset;
+  p.lse_out = a->lse_out;
+  p.merge_out = a->merge_out;
+  p.merge_lse = a->merge_lse;
   hipError_t e = pl.mfma ? bpt::launch_decode_mfma(p, a->kv_dtype, a->scale_kind, (hipStream_t)stream)
                          : bpt::launch_decode(p, a->kv_dtype, a->scale_kind, pl.rows_per_group, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(fn, e);
@@ -362,6 +371,7 @@ int bpt_kivi_decode(const bpt_kivi_args* a, void* stream) {
   p.S = a->num_splits;
   p.cps = a->split / bpt::kMfmaChunk;
   p.gshift = quant ? log2i(a->group / bpt::kMfmaChunk) : 0;
+  p.len_offset = 0;
   p.len_cap = pl.len_cap;
   p.grid = pl.grid;
   p.qscale = a->sm_scale * bpt::kLog2e;

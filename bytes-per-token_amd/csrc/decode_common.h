@@ -118,7 +118,7 @@ __device__ __forceinline__ void load_q(const DecodeParams& p, int64_t base, floa
 // Lengths (clamped to the launch's cap), chunks per sequence and their exclusive prefix sum over the batch
 // (the segment line: sequence b's segments start at chunk HR * prefix[b]), computed by the whole workgroup
 // into LDS: s_prefix[B + 1], s_len[B]; s_wsum holds one int per wave. Params: any parameter block with B,
-// lens and len_cap.
+// lens (NULL: every sequence is len_cap long), len_offset and len_cap.
 template <int NW, int CH, typename Params>
 __device__ __forceinline__ void build_segment_line(const Params& p, int* s_prefix, int* s_len, int* s_wsum) {
   constexpr int NT = NW * 64;
@@ -130,7 +130,7 @@ __device__ __forceinline__ void build_segment_line(const Params& p, int* s_prefi
   const int hi = min(lo + per_thread, B);
   int sum = 0;
   for (int b = lo; b < hi; ++b) {
-    int len = p.lens[b];
+    int len = (p.lens ? p.lens[b] : p.len_cap + p.len_offset) - p.len_offset;  // no lengths: all full
     len = len < 0 ? 0 : (len > p.len_cap ? p.len_cap : len);
     s_len[b] = len;
     sum += (len + CH - 1) / CH;
@@ -158,7 +158,28 @@ __device__ __forceinline__ void build_segment_line(const Params& p, int* s_prefi
   __syncthreads();
 }
 
-// Sequences with no tokens get zero output (workgroups take them round-robin).
+constexpr float kLn2 = 0.69314718055994531f;
+
+// Final value of output element (b, qi, hq, ch) from this launch's normalized result o, whose base-2
+// log-sum-exp is lse2 (-inf: the row saw no token): merged with the caller's partial of another token
+// range when one is given (kernels/reference.py:205-211 for two parts), then stored; the row's natural-log
+// log-sum-exp goes to lse_out (once per row) when asked for.
+__device__ __forceinline__ void write_out(const DecodeParams& p, int b, int qi, int hq, int ch, float o, float lse2) {
+  const int64_t row = ((int64_t)b * p.Q + qi) * p.Hq + hq;
+  if (p.merge_out) {
+    const float other = p.merge_lse[row] * kLog2e;
+    const float m = fmaxf(lse2, other);
+    if (m != kNegInf) {
+      const float a = fast_exp2(lse2 - m), c = fast_exp2(other - m);
+      o = (a * o + c * p.merge_out[row * kHeadDim + ch]) / (a + c);
+      lse2 = m + __log2f(a + c);
+    }
+  }
+  store_float(p.out, (int64_t)b * p.o_sb + (int64_t)qi * p.o_sq + (int64_t)hq * p.o_sh + ch, p.out_dtype, o);
+  if (p.lse_out && ch == 0) p.lse_out[row] = lse2 == kNegInf ? kNegInf : lse2 * kLn2;
+}
+
+// Sequences with no tokens get zero output, or the caller's partial (workgroups take them round-robin).
 template <int NT>
 __device__ __forceinline__ void zero_empty_sequences(const DecodeParams& p, const int* s_prefix) {
   constexpr int D = kHeadDim;
@@ -169,7 +190,7 @@ __device__ __forceinline__ void zero_empty_sequences(const DecodeParams& p, cons
       const int ch = i % D;
       const int hq = (i / D) % p.Hq;
       const int qi = i / (D * p.Hq);
-      store_float(p.out, (int64_t)b * p.o_sb + (int64_t)qi * p.o_sq + (int64_t)hq * p.o_sh + ch, p.out_dtype, 0.0f);
+      write_out(p, b, qi, hq, ch, 0.0f, kNegInf);
     }
   }
 }
@@ -224,8 +245,7 @@ __device__ __forceinline__ void arrive_and_combine(const DecodeParams& p, int se
     }
     const int qi = gr / p.G;
     const int hq = hh * p.G + (gr - qi * p.G);
-    store_float(p.out, (int64_t)b * p.o_sb + (int64_t)qi * p.o_sq + (int64_t)hq * p.o_sh + ch, p.out_dtype,
-                W > 0.0f ? O / W : 0.0f);
+    write_out(p, b, qi, hq, ch, W > 0.0f ? O / W : 0.0f, W > 0.0f ? M + __log2f(W) : kNegInf);
   }
   if (tid == 0) __hip_atomic_store(p.counters + seg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

@@ -483,8 +483,6 @@ __device__ __forceinline__ int64_t lse_index(const KiviParams& p, int b, int hq,
   return (int64_t)b * p.l_sb + (int64_t)hq * p.l_sh + (int64_t)j * p.l_ss;
 }
 
-constexpr float kLn2 = 0.69314718055994531f;
-
 // Splits past a row's length: out 0, lse -inf (workgroups take the rows round-robin).
 template <int NT>
 __device__ __forceinline__ void zero_empty_splits(const KiviParams& p, const int* s_prefix) {

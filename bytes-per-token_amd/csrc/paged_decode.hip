@@ -352,7 +352,7 @@ __device__ __forceinline__ void load_q_rows(const DecodeParams& p, QRows<KV, RG,
       const int hq = h * p.G + (gr - qi * p.G);
       const int64_t base = (int64_t)b * p.q_sb + (int64_t)qi * p.q_sq + (int64_t)hq * p.q_sh + part * VEC;
       load_q<VEC>(p, base, QRows<KV, RG, QS>::kDot ? 1.0f : p.qscale * kscale_head, qf);
-      rlen[r] = len - (p.Q - 1 - qi);
+      rlen[r] = len - (p.noncausal ? 0 : p.Q - 1 - qi);
     } else {
 #pragma unroll
       for (int v = 0; v < VEC; ++v) qf[v] = 0.0f;
@@ -532,8 +532,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
       if (whole) {
         const int qi = gr / p.G;
         const int hq = h * p.G + (gr - qi * p.G);
-        store_float(p.out, (int64_t)b_cur * p.o_sb + (int64_t)qi * p.o_sq + (int64_t)hq * p.o_sh + ch, p.out_dtype,
-                    o);
+        write_out(p, b_cur, qi, hq, ch, o, L > 0.0f ? M - kBias + __log2f(L) : kNegInf);
       } else {
         ws_store(p.ws_out + (wslot * RG + r) * D + ch, o);
         if (ch == 0) ws_store(p.ws_lse + wslot * RG + r, L > 0.0f ? M - kBias + __log2f(L) : kNegInf);

@@ -250,7 +250,7 @@ __device__ __forceinline__ void mfma_load_q(const DecodeParams& p, int b, int h,
   const bool in = n < rows;
   const int qi = in ? n / p.G : 0;
   const int hq = in ? h * p.G + (n - qi * p.G) : 0;
-  rlen = in ? len - (p.Q - 1 - qi) : 0;
+  rlen = in ? len - (p.noncausal ? 0 : p.Q - 1 - qi) : 0;
   const int64_t base = (int64_t)b * p.q_sb + (int64_t)qi * p.q_sq + (int64_t)hq * p.q_sh + 32 * kq;
   if constexpr (!QS && !MQ<KV, QS>::kF16) {
     // bf16 q on the bf16 path: the words already are the operands.
@@ -426,8 +426,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_mfma_kernel(const De
       if (whole) {
         const int qi = r / p.G;
         const int hq = h_cur * p.G + (r - qi * p.G);
-        store_float(p.out, (int64_t)b_cur * p.o_sb + (int64_t)qi * p.o_sq + (int64_t)hq * p.o_sh + ch, p.out_dtype,
-                    out);
+        write_out(p, b_cur, qi, hq, ch, out, L > 0.0f ? M - kBias + __log2f(L) : kNegInf);
       } else {
         ws_store(p.ws_out + (wslot * RG + r) * D + ch, out);
         if (ch == 0) ws_store(p.ws_lse + wslot * RG + r, L > 0.0f ? M - kBias + __log2f(L) : kNegInf);

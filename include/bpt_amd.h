@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define BPT_ABI_VERSION 4
+#define BPT_ABI_VERSION 5
 
 /* return codes */
 #define BPT_OK 0
@@ -75,6 +75,7 @@ typedef enum { BPT_IDX_I32 = 0, BPT_IDX_I64 = 1 } bpt_index_dtype;
  *   block_table  [B, max_blocks_per_seq] (row stride table_stride_b) physical page of each logical page
  *   context_lens [B] int32: tokens in the cache for each sequence, the Q new ones included. Query i of
  *                sequence b sits at position context_lens[b] - Q + i and sees slots 0 .. that position.
+ *                NULL: every sequence holds max_context tokens.
  *   out          [B, Q, Hq, D] (strides out_stride_{b,q,h}), BF16 or F32
  *
  * max_context bounds context_lens and sizes the launch (no device->host read); lengths above it, or
@@ -126,7 +127,17 @@ typedef struct {
   size_t workspace_bytes;
   void* counters;         /* uint32 arrival counters, zero before first use and after every call */
   size_t counters_bytes;
+
+  /* Cascade (a prefix shared by several sequences attended once, then each sequence's own tokens): */
+  int32_t flags;           /* BPT_DECODE_NONCAUSAL: every query sees all of its sequence's tokens */
+  int32_t len_offset;      /* tokens subtracted from every context length (and from every query position) */
+  float* lse_out;          /* optional contiguous float32 [B, Q, Hq]: each row's log-sum-exp (natural log) */
+  const float* merge_out;  /* optional contiguous float32 [B, Q, Hq, D]: a partial over other tokens ... */
+  const float* merge_lse;  /* ... and its log-sum-exp [B, Q, Hq] (natural log, -inf if empty), merged into
+                              out (and lse_out) exactly, as kernels/reference.py:205-211 merges parts */
 } bpt_decode_args;
+
+#define BPT_DECODE_NONCAUSAL 1
 
 /*
  * New K/V rows written into the paged pools, quantized on the way (store-before-attend).
