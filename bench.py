@@ -60,7 +60,20 @@ def profile_pass(args) -> int:
 
     torch.cuda.set_device(0)
     flush = measure.ReadProbe(args.flush_bytes)
-    if args.workload.startswith("kivi-"):  # kivi-<int4|int8|bf16>-<batch>x<context>
+    if args.workload.startswith("norm-int8-"):  # norm-int8-<rows>x<d>
+        from bpt_amd import rms_norm_int8
+
+        rows, d = (int(x) for x in args.workload.split("-")[2].split("x"))
+        gen = torch.Generator(device="cuda:0").manual_seed(d)
+        weight = (torch.randn(d, generator=gen, device="cuda:0").abs() + 0.5).to(torch.bfloat16)
+        x = (torch.randn((rows, d), generator=gen, device="cuda:0") * 3).to(torch.bfloat16)
+        out = (torch.empty((rows, d), dtype=torch.int8, device="cuda:0"),
+               torch.empty(rows, dtype=torch.float32, device="cuda:0"))
+        for _ in range(args.warmup + args.steps):
+            flush.run()
+            rms_norm_int8(x, weight, 1e-6, out=out)
+        nbytes = rows * (3 * d + 4)
+    elif args.workload.startswith("kivi-"):  # kivi-<int4|int8|bf16>-<batch>x<context>
         from bpt_amd import kivi
 
         fmt, shape = args.workload.split("-")[1:]
@@ -75,9 +88,16 @@ def profile_pass(args) -> int:
         w = workloads.make(args.workload, device="cuda:0", seed=0)
         out = torch.empty(tuple(w.q.shape), dtype=torch.bfloat16, device="cuda:0")
         pargs, kw = w.args(), w.kwargs()
+        if args.cascade:
+            from bpt_amd import cascade_decode_attention
+
+            kw = {**kw, "prefix_pages": w.shape.shared_prefix_pages}
         for _ in range(args.warmup + args.steps):
             flush.run()
-            paged_decode_attention(*pargs, **kw, out=out)
+            if args.cascade:
+                cascade_decode_attention(*pargs, **kw, out=out)
+            else:
+                paged_decode_attention(*pargs, **kw, out=out)
         nbytes = w.kv_bytes()
     torch.cuda.synchronize()
     src = torch.ones(64 << 20, dtype=torch.float32, device="cuda:0")
@@ -319,6 +339,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--profile", action="store_true", help="short run for rocprofv3 (no JSON line)")
+    ap.add_argument("--cascade", action="store_true", help="with --profile: the shared-prefix cascade call")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
