@@ -16,6 +16,9 @@
 #ifndef BPT_DECODE_WAVES
 #define BPT_DECODE_WAVES 4
 #endif
+#ifndef BPT_DECODE_MFMA_WAVES_PER_SIMD
+#define BPT_DECODE_MFMA_WAVES_PER_SIMD 2
+#endif
 #ifndef BPT_DECODE_MFMA_MIN_ROWS
 #define BPT_DECODE_MFMA_MIN_ROWS 2
 #endif
@@ -45,6 +48,8 @@ constexpr int kMfmaMinRows = BPT_DECODE_MFMA_MIN_ROWS;
 constexpr int kMfmaMinRowsInt8 = BPT_DECODE_MFMA_MIN_ROWS_INT8;
 constexpr int kMfmaRows = 16;
 constexpr int kMfmaChunk = 32;
+// Waves per SIMD the matrix-core decode kernel is compiled for (its register budget: 512 / this).
+constexpr int kMfmaWavesPerSimd = BPT_DECODE_MFMA_WAVES_PER_SIMD;
 
 // Launch-ready form of bpt_decode_args (cache strides in bytes).
 struct DecodeParams {
@@ -71,6 +76,8 @@ struct DecodeParams {
   float qscale;      // sm_scale * log2(e)
   int q_dtype, out_dtype, table_i64;
   int noncausal;        // every query sees all of its sequence's tokens
+  int xcd_major;        // number the stream-K line XCD-major (per-token scales: the KV heads of a sequence
+                        // share scale cache lines); else round-robin over the XCDs
   int len_offset;       // subtracted from every context length
   float* lse_out;       // optional [B, Q, Hq]: each row's log-sum-exp (natural log)
   const float* merge_out;  // optional [B, Q, Hq, D]: another token range's normalized partial, merged into out

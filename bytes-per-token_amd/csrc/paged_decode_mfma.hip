@@ -278,7 +278,7 @@ __device__ __forceinline__ void mfma_load_q(const DecodeParams& p, int b, int h,
 }
 
 template <int KV, int SK, bool PU, bool QS>
-__global__ __launch_bounds__(kDecodeWaves * 64) void decode_mfma_kernel(const DecodeParams p) {
+__global__ __launch_bounds__(kDecodeWaves * 64, kMfmaWavesPerSimd) void decode_mfma_kernel(const DecodeParams p) {
   constexpr int NW = kDecodeWaves;
   constexpr int NT = NW * 64;
   constexpr int D = kHeadDim;
@@ -307,7 +307,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_mfma_kernel(const De
   const int64_t C = (int64_t)HR * s_prefix[B];
   if (C == 0) return;
   const int64_t per = p.per_forced > 0 ? p.per_forced : (C + gridDim.x - 1) / gridDim.x;
-  const int64_t g = blockIdx.x;
+  const int64_t g = line_index(p);
   const int64_t c_begin = g * per;
   if (c_begin >= C) return;
   const int64_t c_end = min(c_begin + per, C);
