@@ -40,7 +40,7 @@ constexpr int kMChunk = 32;  // tokens per chunk: two 16-token tiles
 
 // This lane's share of one chunk: K for its token of each tile, V for its eight score tokens.
 struct MChunk {
-  U4 k[2][2];          // tile t: token 16 t + n, channels 32 kq .. 32 kq + 31
+  U4 k[2][2];          // tile t, load j: token 16 t + 8 j + l / 8, bytes 16 (l % 8) .. 16 (l % 8) + 15
   u32x2 v[2][4];       // tile t, token 4 kq + i: channels 8 n .. 8 n + 7
   float ks[8], vs[8];  // per-token scales of tokens 16 t + 4 kq + i (index 4 t + i)
 };
@@ -62,18 +62,42 @@ __device__ __forceinline__ int mfma_page(const DecodeParams& p, int b, int tile_
   return clamp_page(p, table[table_word(p, b, tok >> p.logP)]);
 }
 
+// K rows are loaded whole: each load instruction covers eight tokens' 128-byte rows (lane l: token
+// l / 8, 16 bytes at 16 (l % 8)), which the memory pipeline serves faster than the operand layout's half
+// rows of sixteen tokens; mfma_k_operand then rearranges them through LDS.
 template <bool PU>
 __device__ __forceinline__ void mfma_issue_k(const DecodeParams& p, int b, int h, int kk, int len, int lane, MChunk& c) {
   const int T0 = kk * kMChunk;
-  const int kq = lane >> 4, n = lane & 15;
-  const int64_t head_off = (int64_t)h * p.kv_shead;
+  const int r = lane >> 3, sg = lane & 7;
+  const int64_t head_off = (int64_t)h * p.kv_shead + 16 * sg;
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    const int tok = min(T0 + 16 * t + n, len - 1);
-    const int e = mfma_page<PU>(p, b, T0 + 16 * t, tok, len);
-    const int64_t off = (int64_t)e * p.kv_sblk + (int64_t)(tok & (p.P - 1)) * p.kv_stok + head_off + 32 * kq;
-    c.k[t][0] = load16(p.k + off);
-    c.k[t][1] = load16(p.k + off + 16);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int tok = min(T0 + 16 * t + 8 * j + r, len - 1);
+      const int e = mfma_page<PU>(p, b, T0 + 16 * t, tok, len);
+      c.k[t][j] = load16(p.k + (int64_t)e * p.kv_sblk + (int64_t)(tok & (p.P - 1)) * p.kv_stok + head_off);
+    }
+  }
+}
+
+// The score MFMAs' K operand from the loaded rows: lane l gets token 16 t + n, bytes 32 kq .. 32 kq + 31
+// (n = l % 16, kq = l / 16), through this wave's LDS tile sk. The 16-byte segments of row x sit at
+// segment ^ (x % 8) ^ (x / 8): every 8 lanes of a store (one row) or of a load (rows n .. n + 7) and every
+// 16 (two rows; rows n .. n + 15) touch distinct banks.
+__device__ __forceinline__ void mfma_k_operand(const MChunk& c, U4 (&sk)[2][16][8], int lane, U4 (&kr)[2][2]) {
+  const int r = lane >> 3, sg = lane & 7;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) sk[t][8 * j + r][sg ^ r ^ j] = c.k[t][j];
+  }
+  const int n = lane & 15, kq = lane >> 4;
+  const int sw = (n & 7) ^ (n >> 3);
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) kr[t][j] = sk[t][n][(2 * kq + j) ^ sw];
   }
 }
 
@@ -166,17 +190,19 @@ struct MQ {
 // `after_scores` runs once the chunk's K registers are consumed (the caller issues the next chunk's K loads
 // there, so they fly during this chunk's softmax and value products).
 template <int KV, int SK, bool QS, typename AfterScores>
-__device__ __forceinline__ void mfma_compute(MChunk& c, int kk, int lane, const typename MQ<KV, QS>::T (&qb)[MQ<KV, QS>::kOps],
-                                             float qscale, int rlen, float& m, float& l, f32x4 (&o)[8],
-                                             AfterScores after_scores) {
+__device__ __forceinline__ void mfma_compute(MChunk& c, U4 (&sk)[2][16][8], int kk, int lane,
+                                             const typename MQ<KV, QS>::T (&qb)[MQ<KV, QS>::kOps], float qscale,
+                                             int rlen, float& m, float& l, f32x4 (&o)[8], AfterScores after_scores) {
   const int T0 = kk * kMChunk;
   const int kq = lane >> 4;
+  U4 kr[2][2];
+  mfma_k_operand(c, sk, lane, kr);
   float sc[8];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     f32x4 st = {0.0f, 0.0f, 0.0f, 0.0f};
-    const uint32_t w[8] = {c.k[t][0].x, c.k[t][0].y, c.k[t][0].z, c.k[t][0].w,
-                           c.k[t][1].x, c.k[t][1].y, c.k[t][1].z, c.k[t][1].w};
+    const uint32_t w[8] = {kr[t][0].x, kr[t][0].y, kr[t][0].z, kr[t][0].w,
+                           kr[t][1].x, kr[t][1].y, kr[t][1].z, kr[t][1].w};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       if constexpr (MQ<KV, QS>::kF16) {
@@ -292,6 +318,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, kMfmaWavesPerSimd) void decode_m
   __shared__ float s_m[NW][RG];
   __shared__ float s_l[NW][RG];
   __shared__ float s_o[NW][RG][D];
+  __shared__ U4 s_k[NW][2][16][8];  // each wave's K rows of one chunk, on their way to the operand layout
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -358,7 +385,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, kMfmaWavesPerSimd) void decode_m
     // the next chunk's K loads are issued as soon as kk's scores are done, its V loads after kk's values.
     for (int kk = k + wave; kk < k_end;) {
       const int kn = kk + NW;
-      mfma_compute<KV, SK, QS>(cr, kk, lane, qb, qscale, rlen, m, l, o, [&]() {
+      mfma_compute<KV, SK, QS>(cr, s_k[wave], kk, lane, qb, qscale, rlen, m, l, o, [&]() {
         if (kn < k_end) mfma_issue_k<PU>(p, b, h, kn, len, lane, cr);
       });
       if (kn < k_end) mfma_issue_v<SK, PU>(p, b, h, kn, len, lane, cr);
