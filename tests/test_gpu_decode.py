@@ -132,11 +132,14 @@ def test_formats_and_ragged_lengths(fmt, scales, lengths):
             assert got[i].float().abs().sum().item() == 0
 
 
+@pytest.mark.parametrize("fmt,scales", [("fp8", "head"), ("int8", "token"), ("bf16", None)])
 @pytest.mark.parametrize("num_splits", [1, 2, 7, 64, 1000])
-def test_forced_split_counts(num_splits):
-    c = make_case("fp8", [4096, 1000, 33, 1])
+def test_forced_split_counts(num_splits, fmt, scales):
+    # 64 and 1000 splits give more partitions than workgroups: each workgroup then runs several partitions,
+    # one piece (and one partial) each, some of them inside one segment.
+    c = make_case(fmt, [4096, 1000, 33, 1], scales=scales)
     got, want = run_case(c, num_splits=num_splits)
-    check(got, want, f"num_splits={num_splits}")
+    check(got, want, f"{fmt} num_splits={num_splits}")
 
 
 @pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 8), (32, 8), (64, 8), (12, 4), (40, 8)])
