@@ -72,8 +72,7 @@ struct DecodeParams {
   int B, Q, Hq, Hkv, G, P, logP, num_blocks, max_blocks, len_cap;
   int n_rg, HR;      // row groups per KV head; segments per sequence (Hkv * n_rg)
   int grid;          // workgroups launched
-  int64_t per_forced;  // chunks per partition when the caller fixed the split count, else 0
-  int multi_part;      // more partitions than workgroups: a workgroup runs several
+  int64_t per_forced;  // chunks per workgroup when the caller fixed the split count, else 0
   float qscale;      // sm_scale * log2(e)
   int q_dtype, out_dtype, table_i64;
   int noncausal;        // every query sees all of its sequence's tokens

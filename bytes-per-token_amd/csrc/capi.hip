@@ -46,7 +46,6 @@ struct Plan {
   bool mfma;  // the matrix-core kernel (all rows of a KV head in one 16-row group)
   int rows, rows_per_group, n_rg, HR, chunk, grid, len_cap;
   int64_t per_forced;
-  int64_t parts;  // stream-K partitions (workspace slots beyond one per segment)
   size_t ws_out_floats, ws_lse_floats, workspace, counters;
 };
 
@@ -104,24 +103,26 @@ int make_plan(const bpt_decode_args* a, Plan* pl) {
   if (seq_chunks > 0x7fffffffLL / (hr > 0 ? hr : 1))
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: batch x context x heads too large", fn);
   const int64_t bound_c = seq_chunks * hr;
-  // Partitions of the stream-K line: num_splits fixes their size (a max_context sequence gets num_splits of
-  // them); otherwise there is one per workgroup. A workgroup takes ceil(partitions / grid) of them.
-  const int64_t max_grid = (int64_t)bpt::kComputeUnits * bpt::kDecodeGroupsPerCu;
-  int64_t& parts = pl->parts;
   if (a->num_splits > 0) {
+    // num_splits partitions for a max_context sequence. When that gives more partitions than resident
+    // workgroups, each workgroup takes several consecutive ones whole: inside a workgroup the online
+    // softmax simply continues across their boundary (the log-sum-exp merge of the two partials, done in
+    // registers), so the partials that go through memory are those of the resident workgroups.
+    const int64_t max_grid = (int64_t)bpt::kComputeUnits * bpt::kDecodeGroupsPerCu;
     int64_t per = (max_nb + a->num_splits - 1) / a->num_splits;
-    pl->per_forced = per < 1 ? 1 : per;
-    parts = (bound_c + pl->per_forced - 1) / pl->per_forced;
-    if (parts < 1) parts = 1;
-    pl->grid = (int)(parts < max_grid ? parts : max_grid);
+    if (per < 1) per = 1;
+    const int64_t parts = (bound_c + per - 1) / per;
+    if (parts > max_grid) per *= (parts + max_grid - 1) / max_grid;
+    pl->per_forced = per;
+    int64_t grid = (bound_c + pl->per_forced - 1) / pl->per_forced;
+    pl->grid = (int)(grid < 1 ? 1 : grid);
   } else {
     pl->per_forced = 0;
-    int64_t grid = max_grid;
+    int64_t grid = (int64_t)bpt::kComputeUnits * bpt::kDecodeGroupsPerCu;
     if (bound_c < grid) grid = bound_c;
     pl->grid = (int)(grid < 1 ? 1 : grid);
-    parts = pl->grid;
   }
-  const size_t slots = (size_t)a->batch * pl->HR + (size_t)parts;
+  const size_t slots = (size_t)a->batch * pl->HR + pl->grid;
   pl->ws_out_floats = slots * pl->rows_per_group * a->head_dim;
   pl->ws_lse_floats = slots * pl->rows_per_group;
   pl->workspace = align256((pl->ws_out_floats + pl->ws_lse_floats) * sizeof(float));
@@ -285,7 +286,6 @@ int bpt_paged_decode(const bpt_decode_args* a, void* stream) {
   p.HR = pl.HR;
   p.grid = pl.grid;
   p.per_forced = pl.per_forced;
-  p.multi_part = pl.parts > pl.grid;
   p.len_cap = pl.len_cap;
   p.qscale = a->sm_scale * bpt::kLog2e;
   p.q_dtype = a->q_dtype;

@@ -191,13 +191,6 @@ __device__ __forceinline__ int64_t line_index(const DecodeParams& p) {
   return (int64_t)k * q + min(k, r) + (x >> 3);
 }
 
-// The stream-K line of C chunks is cut into partitions of `per` chunks (each one split-K partial per segment
-// it touches). Without a forced split count there is one partition per workgroup; with one, a workgroup
-// takes ceil(partitions / workgroups) consecutive partitions.
-__device__ __forceinline__ int64_t partitions_per_group(const DecodeParams& p, int64_t C, int64_t per) {
-  return p.per_forced > 0 ? ((C + per - 1) / per + gridDim.x - 1) / gridDim.x : 1;
-}
-
 // Sequences with no tokens get zero output, or the caller's partial (workgroups take them round-robin).
 template <int NT>
 __device__ __forceinline__ void zero_empty_sequences(const DecodeParams& p, const int* s_prefix) {

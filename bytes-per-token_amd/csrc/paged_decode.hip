@@ -404,12 +404,10 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
   const int64_t C = (int64_t)HR * s_prefix[B];
   if (C == 0) return;
   const int64_t per = p.per_forced > 0 ? p.per_forced : (C + gridDim.x - 1) / gridDim.x;
-  const int64_t upw = partitions_per_group(p, C, per);
-  int64_t partition = line_index(p) * upw;  // the partition of the current piece, and where it ends
-  const int64_t c_begin = partition * per;
+  const int64_t g = line_index(p);
+  const int64_t c_begin = g * per;
   if (c_begin >= C) return;
-  const int64_t c_end = min(c_begin + upw * per, C);
-  int64_t partition_end = c_begin + per;
+  const int64_t c_end = min(c_begin + per, C);
   int64_t c = c_begin;
 
   int b;
@@ -444,7 +442,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
     const int h = hr / p.n_rg;
     load_q_rows<KV, RG, QS>(p, q, rlen, b, h, hr - h * p.n_rg, rows, part, len,
                             SK == kScaleHead ? load_uniform(p.ks + h) : 1.0f);
-    const int k_end = k + (int)(min(min(c_end, partition_end), (int64_t)HR * s_prefix[b] + (int64_t)hr * nb + nb) - c);
+    const int k_end = k + (int)(min(c_end, (int64_t)HR * s_prefix[b] + (int64_t)hr * nb + nb) - c);
     if (k + wave < k_end) {
       fetch_pages<KV, CL, PU>(p, b, k + wave, len, slot, gp);
       issue_chunk<KV, SK, CL, PU>(p, gp, h, k + wave, len, slot, part, cr);
@@ -454,7 +452,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
   // ---- pieces: the parts of segments inside [c_begin, c_end) -------------------------------------------
   for (;;) {
     const int64_t seg_c0 = (int64_t)HR * s_prefix[b] + (int64_t)hr * nb;
-    const int64_t pe = min(min(c_end, partition_end), seg_c0 + nb);  // a piece ends with its range, partition or segment
+    const int64_t pe = min(c_end, seg_c0 + nb);
     const int k_end = k + (int)(pe - c);
     const int h = hr / p.n_rg;
     const int rg = hr - h * p.n_rg;
@@ -478,39 +476,28 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
       kk = kn;
     }
 
-    // The next piece (if any): its q rows (for a new segment) and this wave's first chunk go in flight now.
+    // The next piece (if any): its q rows and this wave's first chunk go in flight now.
     const int b_cur = b, hr_cur = hr, nb_cur = nb;
     const int64_t c_next = pe;
-    int64_t partition_next = partition;
-    if (c_next == partition_end) {
-      ++partition_next;
-      partition_end += per;
-    }
     if (c_next < c_end) {
-      if (c_next < seg_c0 + nb) {
-        k = k_end;  // the segment goes on past a partition boundary
-      } else {
-        ++hr;
-        k = 0;
-        if (hr == HR) {
-          hr = 0;
-          do {
-            ++b;
-          } while (s_prefix[b + 1] == s_prefix[b]);
-          b = sread(b);
-          nb = sread(s_prefix[b + 1] - s_prefix[b]);
-        }
-        len = sread(s_len[b]);
-        const int hn = hr / p.n_rg;
-        load_q_rows<KV, RG, QS>(p, q, rlen, b, hn, hr - hn * p.n_rg, rows, part, len,
-                                SK == kScaleHead ? load_uniform(p.ks + hn) : 1.0f);
+      ++hr;
+      k = 0;
+      if (hr == HR) {
+        hr = 0;
+        do {
+          ++b;
+        } while (s_prefix[b + 1] == s_prefix[b]);
+        b = sread(b);
+        nb = sread(s_prefix[b + 1] - s_prefix[b]);
       }
+      len = sread(s_len[b]);
       const int hn = hr / p.n_rg;
-      const int64_t seg_next = (int64_t)HR * s_prefix[b] + (int64_t)hr * nb;
-      const int kn_end = k + (int)(min(min(c_end, partition_end), seg_next + nb) - c_next);
-      if (k + wave < kn_end) {
-        fetch_pages<KV, CL, PU>(p, b, k + wave, len, slot, gp);
-        issue_chunk<KV, SK, CL, PU>(p, gp, hn, k + wave, len, slot, part, cr);
+      load_q_rows<KV, RG, QS>(p, q, rlen, b, hn, hr - hn * p.n_rg, rows, part, len,
+                              SK == kScaleHead ? load_uniform(p.ks + hn) : 1.0f);
+      const int kn_end = (int)min((int64_t)nb, c_end - c_next);
+      if (wave < kn_end) {
+        fetch_pages<KV, CL, PU>(p, b, wave, len, slot, gp);
+        issue_chunk<KV, SK, CL, PU>(p, gp, hn, wave, len, slot, part, cr);
       }
     }
 
@@ -522,7 +509,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
     const int64_t g_first = seg_c0 / per;
     const int64_t g_last = (seg_c0 + nb_cur - 1) / per;
     const bool whole = g_first == g_last;
-    const int64_t wslot = (int64_t)seg + partition;  // (segment, partition) pairs map to distinct slots
+    const int64_t wslot = (int64_t)seg + g;
     const float vscale_head = SK == kScaleHead ? load_uniform(p.vs + h) : 1.0f;
     for (int idx = tid; idx < RG * D; idx += NT) {
       const int r = idx / D;
@@ -560,7 +547,6 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
     }
     if (c_next >= c_end) break;
     c = c_next;
-    partition = partition_next;
     __syncthreads();  // the LDS merge buffers are rewritten by the next piece
   }
 }

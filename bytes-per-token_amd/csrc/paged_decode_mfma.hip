@@ -303,8 +303,7 @@ __device__ __forceinline__ void mfma_load_q(const DecodeParams& p, int b, int h,
   }
 }
 
-// MP: a workgroup may run several partitions (a forced split count with more partitions than workgroups).
-template <int KV, int SK, bool PU, bool QS, bool MP>
+template <int KV, int SK, bool PU, bool QS>
 __global__ __launch_bounds__(kDecodeWaves * 64, kMfmaWavesPerSimd) void decode_mfma_kernel(const DecodeParams p) {
   constexpr int NW = kDecodeWaves;
   constexpr int NT = NW * 64;
@@ -335,12 +334,10 @@ __global__ __launch_bounds__(kDecodeWaves * 64, kMfmaWavesPerSimd) void decode_m
   const int64_t C = (int64_t)HR * s_prefix[B];
   if (C == 0) return;
   const int64_t per = p.per_forced > 0 ? p.per_forced : (C + gridDim.x - 1) / gridDim.x;
-  const int64_t upw = MP ? partitions_per_group(p, C, per) : 1;
-  int64_t partition = line_index(p) * upw;  // the partition of the current piece, and where it ends
-  const int64_t c_begin = partition * per;
+  const int64_t g = line_index(p);
+  const int64_t c_begin = g * per;
   if (c_begin >= C) return;
-  const int64_t c_end = min(c_begin + upw * per, C);
-  int64_t partition_end = MP ? c_begin + per : c_end;
+  const int64_t c_end = min(c_begin + per, C);
   int64_t c = c_begin;
 
   int b;
@@ -370,13 +367,13 @@ __global__ __launch_bounds__(kDecodeWaves * 64, kMfmaWavesPerSimd) void decode_m
   float qscale = p.qscale * (SK == kScaleHead ? load_uniform(p.ks + h) : 1.0f);
   mfma_load_q<KV, QS>(p, b, h, rows, len, lane, qb, rlen);
   {
-    const int k_end = k + (int)(min(min(c_end, partition_end), (int64_t)HR * s_prefix[b] + (int64_t)h * nb + nb) - c);
+    const int k_end = k + (int)(min(c_end, (int64_t)HR * s_prefix[b] + (int64_t)h * nb + nb) - c);
     if (k + wave < k_end) mfma_issue<SK, PU>(p, b, h, k + wave, len, lane, cr);
   }
 
   for (;;) {
     const int64_t seg_c0 = (int64_t)HR * s_prefix[b] + (int64_t)h * nb;
-    const int64_t pe = min(min(c_end, partition_end), seg_c0 + nb);  // a piece ends with its range, partition or segment
+    const int64_t pe = min(c_end, seg_c0 + nb);
     const int k_end = k + (int)(pe - c);
 
     float m = kNegInf, l = 0.0f;
@@ -395,35 +392,24 @@ __global__ __launch_bounds__(kDecodeWaves * 64, kMfmaWavesPerSimd) void decode_m
       kk = kn;
     }
 
-    // The next piece (if any): its q rows (for a new segment) and this wave's first chunk go in flight now.
+    // The next piece (if any): its q rows and this wave's first chunk go in flight now.
     const int b_cur = b, h_cur = h, nb_cur = nb;
     const int64_t c_next = pe;
-    int64_t partition_next = partition;
-    if (MP && c_next == partition_end) {
-      ++partition_next;
-      partition_end += per;
-    }
     if (c_next < c_end) {
-      if (MP && c_next < seg_c0 + nb) {
-        k = k_end;  // the segment goes on past a partition boundary
-      } else {
-        ++h;
-        k = 0;
-        if (h == HR) {
-          h = 0;
-          do {
-            ++b;
-          } while (s_prefix[b + 1] == s_prefix[b]);
-          b = sread(b);
-          nb = sread(s_prefix[b + 1] - s_prefix[b]);
-        }
-        len = sread(s_len[b]);
-        qscale = p.qscale * (SK == kScaleHead ? load_uniform(p.ks + h) : 1.0f);
-        mfma_load_q<KV, QS>(p, b, h, rows, len, lane, qb, rlen);
+      ++h;
+      k = 0;
+      if (h == HR) {
+        h = 0;
+        do {
+          ++b;
+        } while (s_prefix[b + 1] == s_prefix[b]);
+        b = sread(b);
+        nb = sread(s_prefix[b + 1] - s_prefix[b]);
       }
-      const int64_t seg_next = (int64_t)HR * s_prefix[b] + (int64_t)h * nb;
-      const int kn_end = k + (int)(min(min(c_end, partition_end), seg_next + nb) - c_next);
-      if (k + wave < kn_end) mfma_issue<SK, PU>(p, b, h, k + wave, len, lane, cr);
+      len = sread(s_len[b]);
+      qscale = p.qscale * (SK == kScaleHead ? load_uniform(p.ks + h) : 1.0f);
+      mfma_load_q<KV, QS>(p, b, h, rows, len, lane, qb, rlen);
+      if (wave < (int)min((int64_t)nb, c_end - c_next)) mfma_issue<SK, PU>(p, b, h, wave, len, lane, cr);
     }
 
     // This wave's state of row n: the four lanes' weight sums added, stored for the workgroup merge.
@@ -445,7 +431,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, kMfmaWavesPerSimd) void decode_m
     const int64_t g_first = seg_c0 / per;
     const int64_t g_last = (seg_c0 + nb_cur - 1) / per;
     const bool whole = g_first == g_last;
-    const int64_t wslot = (int64_t)seg + partition;  // (segment, partition) pairs map to distinct slots
+    const int64_t wslot = (int64_t)seg + g;
     const float vscale_head = SK == kScaleHead ? load_uniform(p.vs + h_cur) : 1.0f;
     for (int idx = tid; idx < RG * D; idx += NT) {
       const int r = idx / D;
@@ -480,25 +466,18 @@ __global__ __launch_bounds__(kDecodeWaves * 64, kMfmaWavesPerSimd) void decode_m
     }
     if (c_next >= c_end) break;
     c = c_next;
-    partition = partition_next;
     __syncthreads();  // the LDS merge buffers are rewritten by the next piece
   }
 }
 
-template <int KV, int SK, bool PU, bool QS>
-static void launch_mp(const DecodeParams& p, hipStream_t stream) {
-  dim3 grid(p.grid), block(kDecodeWaves * 64);
-  const size_t lds = (size_t)(2 * p.B + 1) * sizeof(int);
-  if (p.multi_part) hipLaunchKernelGGL((decode_mfma_kernel<KV, SK, PU, QS, true>), grid, block, lds, stream, p);
-  else hipLaunchKernelGGL((decode_mfma_kernel<KV, SK, PU, QS, false>), grid, block, lds, stream, p);
-}
-
 template <int KV, int SK>
 static hipError_t launch_mfma_sk(const DecodeParams& p, bool pu, bool qs, hipStream_t stream) {
-  if (pu && !qs) launch_mp<KV, SK, true, false>(p, stream);
-  else if (pu) launch_mp<KV, SK, true, true>(p, stream);
-  else if (!qs) launch_mp<KV, SK, false, false>(p, stream);
-  else launch_mp<KV, SK, false, true>(p, stream);
+  dim3 grid(p.grid), block(kDecodeWaves * 64);
+  const size_t lds = (size_t)(2 * p.B + 1) * sizeof(int);
+  if (pu && !qs) hipLaunchKernelGGL((decode_mfma_kernel<KV, SK, true, false>), grid, block, lds, stream, p);
+  else if (pu) hipLaunchKernelGGL((decode_mfma_kernel<KV, SK, true, true>), grid, block, lds, stream, p);
+  else if (!qs) hipLaunchKernelGGL((decode_mfma_kernel<KV, SK, false, false>), grid, block, lds, stream, p);
+  else hipLaunchKernelGGL((decode_mfma_kernel<KV, SK, false, true>), grid, block, lds, stream, p);
   return hipGetLastError();
 }
 

@@ -58,13 +58,13 @@ def expected_counters(batch, segments_per_seq):
 
 def test_plan_honours_requested_splits(built_lib):
     # 32/8 heads: 4 rows per KV head (one 16-row matrix-core group), 32-token chunks; 32768 tokens in 32
-    # partitions of 32 chunks each: 1024 partitions, two per workgroup on 512 workgroups (two per CU), and
-    # a workspace slot for every (segment, partition) pair.
+    # partitions of 32 chunks each: 1024 partitions, more than the 512 resident workgroups (two per CU), so
+    # each workgroup takes two consecutive partitions whole.
     q, k, v, table, lens, ks, vs = cpu_case(b=4, hq=32, max_blocks=2048, nb=8192)
     grid, chunk, ws, cnt = decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=32768, num_splits=32)
     assert chunk == 32 and grid == 512
-    assert ws == expected_workspace(4, 8, 16, 4 * 8 * 32) and cnt == expected_counters(4, 8)
-    # Fewer partitions than workgroup slots: one workgroup each.
+    assert ws == expected_workspace(4, 8, 16, grid) and cnt == expected_counters(4, 8)
+    # Fewer partitions than resident workgroups: one workgroup each.
     grid, _, ws, _ = decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=32768, num_splits=8)
     assert grid == 4 * 8 * 8 and ws == expected_workspace(4, 8, 16, grid)
 

@@ -135,8 +135,8 @@ def test_formats_and_ragged_lengths(fmt, scales, lengths):
 @pytest.mark.parametrize("fmt,scales", [("fp8", "head"), ("int8", "token"), ("bf16", None)])
 @pytest.mark.parametrize("num_splits", [1, 2, 7, 64, 1000])
 def test_forced_split_counts(num_splits, fmt, scales):
-    # 64 and 1000 splits give more partitions than workgroups: each workgroup then runs several partitions,
-    # one piece (and one partial) each, some of them inside one segment.
+    # 64 and 1000 splits give more partitions than resident workgroups: each workgroup then takes several
+    # consecutive partitions whole.
     c = make_case(fmt, [4096, 1000, 33, 1], scales=scales)
     got, want = run_case(c, num_splits=num_splits)
     check(got, want, f"{fmt} num_splits={num_splits}")
