@@ -19,6 +19,9 @@
 #ifndef BPT_DECODE_MFMA_WAVES_PER_SIMD
 #define BPT_DECODE_MFMA_WAVES_PER_SIMD 2
 #endif
+#ifndef BPT_DECODE_PIECE_COST
+#define BPT_DECODE_PIECE_COST 8
+#endif
 #ifndef BPT_DECODE_MFMA_MIN_ROWS
 #define BPT_DECODE_MFMA_MIN_ROWS 2
 #endif
@@ -36,6 +39,10 @@ constexpr int kDecodeWaves = BPT_DECODE_WAVES;
 // Compute units of an MI355X; the auto plan launches kDecodeGroupsPerCu workgroups per CU.
 constexpr int kComputeUnits = 256;
 constexpr int kDecodeGroupsPerCu = BPT_DECODE_GROUPS_PER_CU;
+// Stream-K line units charged for each segment start, in chunks: the cost of merging one more piece (the
+// wave merge, the partial's round trip and, for one workgroup, the combine), so that a workgroup whose
+// range starts a segment gets correspondingly fewer chunks.
+constexpr int kDecodePieceCost = BPT_DECODE_PIECE_COST;
 
 // 16-byte K loads (and V loads) per lane per chunk: fewer for 4-row groups, whose q and accumulators take
 // twice the registers.
@@ -73,6 +80,7 @@ struct DecodeParams {
   int n_rg, HR;      // row groups per KV head; segments per sequence (Hkv * n_rg)
   int grid;          // workgroups launched
   int64_t per_forced;  // chunks per workgroup when the caller fixed the split count, else 0
+  int piece_cost;      // line units charged per segment start (0 with a fixed split count)
   float qscale;      // sm_scale * log2(e)
   int q_dtype, out_dtype, table_i64;
   int noncausal;        // every query sees all of its sequence's tokens

@@ -115,12 +115,15 @@ __device__ __forceinline__ void load_q(const DecodeParams& p, int64_t base, floa
   }
 }
 
-// Lengths (clamped to the launch's cap), chunks per sequence and their exclusive prefix sum over the batch
-// (the segment line: sequence b's segments start at chunk HR * prefix[b]), computed by the whole workgroup
-// into LDS: s_prefix[B + 1], s_len[B]; s_wsum holds one int per wave. Params: any parameter block with B,
-// lens (NULL: every sequence is len_cap long), len_offset and len_cap.
+// Lengths (clamped to the launch's cap), the cost of each sequence's segments and its exclusive prefix sum
+// over the batch (the segment line: sequence b's segments start at HR * prefix[b]), computed by the whole
+// workgroup into LDS: s_prefix[B + 1], s_len[B]; s_wsum holds one int per wave. A segment of a non-empty
+// sequence costs its chunks plus piece_cost units, which stand for the merge of one more piece and sit
+// at the segment's start, ahead of its chunks. Params: any parameter block with B, lens (NULL: every
+// sequence is len_cap long), len_offset and len_cap.
 template <int NW, int CH, typename Params>
-__device__ __forceinline__ void build_segment_line(const Params& p, int* s_prefix, int* s_len, int* s_wsum) {
+__device__ __forceinline__ void build_segment_line(const Params& p, int* s_prefix, int* s_len, int* s_wsum,
+                                                   int piece_cost = 0) {
   constexpr int NT = NW * 64;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -133,7 +136,7 @@ __device__ __forceinline__ void build_segment_line(const Params& p, int* s_prefi
     int len = (p.lens ? p.lens[b] : p.len_cap + p.len_offset) - p.len_offset;  // no lengths: all full
     len = len < 0 ? 0 : (len > p.len_cap ? p.len_cap : len);
     s_len[b] = len;
-    sum += (len + CH - 1) / CH;
+    sum += len > 0 ? (len + CH - 1) / CH + piece_cost : 0;
   }
   int x = sum;
 #pragma unroll
@@ -148,7 +151,7 @@ __device__ __forceinline__ void build_segment_line(const Params& p, int* s_prefi
   run += x - sum;
   for (int b = lo; b < hi; ++b) {
     s_prefix[b] = run;
-    run += (s_len[b] + CH - 1) / CH;
+    run += s_len[b] > 0 ? (s_len[b] + CH - 1) / CH + piece_cost : 0;
   }
   if (tid == 0) {
     int total = 0;

@@ -396,7 +396,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
   const int wave = sread(tid >> 6);
   const int B = p.B;
 
-  build_segment_line<NW, CH>(p, s_prefix, s_len, s_wsum);
+  build_segment_line<NW, CH>(p, s_prefix, s_len, s_wsum, p.piece_cost);
   zero_empty_sequences<NT>(p, s_prefix);
 
   // ---- this workgroup's range of chunks -----------------------------------------------------------
@@ -419,12 +419,21 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
     }
     b = sread(lo);
   }
-  int nb = sread(s_prefix[b + 1] - s_prefix[b]);
+  // A segment spans X line units, then its nb chunks; a range that starts among the X units starts with
+  // the segment's first chunk.
+  const int X = p.piece_cost;
+  int span = sread(s_prefix[b + 1] - s_prefix[b]);
+  int nb = span - X;
   int hr, k;
   {
     const int64_t r = c - (int64_t)HR * s_prefix[b];
-    hr = sread((int)(r / nb));
-    k = sread((int)(r - (int64_t)hr * nb));
+    hr = sread((int)(r / span));
+    k = sread(max((int)(r - (int64_t)hr * span) - X, 0));
+  }
+  {
+    // A range that holds no chunk (it lies within one segment's X units) has nothing to do.
+    const int64_t seg_c0 = (int64_t)HR * s_prefix[b] + (int64_t)hr * span;
+    if (min(c_end, seg_c0 + span) - seg_c0 - X <= k) return;
   }
 
   const int slot = lane / LPR;
@@ -442,7 +451,8 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
     const int h = hr / p.n_rg;
     load_q_rows<KV, RG, QS>(p, q, rlen, b, h, hr - h * p.n_rg, rows, part, len,
                             SK == kScaleHead ? load_uniform(p.ks + h) : 1.0f);
-    const int k_end = k + (int)(min(c_end, (int64_t)HR * s_prefix[b] + (int64_t)hr * nb + nb) - c);
+    const int64_t seg_c0 = (int64_t)HR * s_prefix[b] + (int64_t)hr * span;
+    const int k_end = (int)(min(c_end, seg_c0 + span) - seg_c0 - X);
     if (k + wave < k_end) {
       fetch_pages<KV, CL, PU>(p, b, k + wave, len, slot, gp);
       issue_chunk<KV, SK, CL, PU>(p, gp, h, k + wave, len, slot, part, cr);
@@ -451,9 +461,9 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
 
   // ---- pieces: the parts of segments inside [c_begin, c_end) -------------------------------------------
   for (;;) {
-    const int64_t seg_c0 = (int64_t)HR * s_prefix[b] + (int64_t)hr * nb;
-    const int64_t pe = min(c_end, seg_c0 + nb);
-    const int k_end = k + (int)(pe - c);
+    const int64_t seg_c0 = (int64_t)HR * s_prefix[b] + (int64_t)hr * span;
+    const int64_t pe = min(c_end, seg_c0 + span);
+    const int k_end = (int)(pe - seg_c0 - X);  // this piece's chunks: [k, k_end)
     const int h = hr / p.n_rg;
     const int rg = hr - h * p.n_rg;
 
@@ -476,9 +486,11 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
       kk = kn;
     }
 
-    // The next piece (if any): its q rows and this wave's first chunk go in flight now.
+    // The next piece (if the range holds chunks of the next segment): its q rows and this wave's first
+    // chunk go in flight now.
     const int b_cur = b, hr_cur = hr, nb_cur = nb;
     const int64_t c_next = pe;
+    bool more = false;
     if (c_next < c_end) {
       ++hr;
       k = 0;
@@ -488,16 +500,20 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
           ++b;
         } while (s_prefix[b + 1] == s_prefix[b]);
         b = sread(b);
-        nb = sread(s_prefix[b + 1] - s_prefix[b]);
+        span = sread(s_prefix[b + 1] - s_prefix[b]);
+        nb = span - X;
       }
-      len = sread(s_len[b]);
-      const int hn = hr / p.n_rg;
-      load_q_rows<KV, RG, QS>(p, q, rlen, b, hn, hr - hn * p.n_rg, rows, part, len,
-                              SK == kScaleHead ? load_uniform(p.ks + hn) : 1.0f);
-      const int kn_end = (int)min((int64_t)nb, c_end - c_next);
-      if (wave < kn_end) {
-        fetch_pages<KV, CL, PU>(p, b, wave, len, slot, gp);
-        issue_chunk<KV, SK, CL, PU>(p, gp, hn, wave, len, slot, part, cr);
+      const int kn_end = (int)min((int64_t)nb, c_end - c_next - X);
+      more = kn_end > 0;
+      if (more) {
+        len = sread(s_len[b]);
+        const int hn = hr / p.n_rg;
+        load_q_rows<KV, RG, QS>(p, q, rlen, b, hn, hr - hn * p.n_rg, rows, part, len,
+                                SK == kScaleHead ? load_uniform(p.ks + hn) : 1.0f);
+        if (wave < kn_end) {
+          fetch_pages<KV, CL, PU>(p, b, wave, len, slot, gp);
+          issue_chunk<KV, SK, CL, PU>(p, gp, hn, wave, len, slot, part, cr);
+        }
       }
     }
 
@@ -506,8 +522,8 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
 
     // ---- merge the waves; write the segment's output, or this piece's partial ---------------------
     const int seg = b_cur * HR + hr_cur;
-    const int64_t g_first = seg_c0 / per;
-    const int64_t g_last = (seg_c0 + nb_cur - 1) / per;
+    const int64_t g_first = (seg_c0 + X) / per;  // the workgroups holding the segment's first and last chunks
+    const int64_t g_last = (seg_c0 + X + nb_cur - 1) / per;
     const bool whole = g_first == g_last;
     const int64_t wslot = (int64_t)seg + g;
     const float vscale_head = SK == kScaleHead ? load_uniform(p.vs + h) : 1.0f;
@@ -545,7 +561,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
       __syncthreads();
       arrive_and_combine<RG, NT>(p, seg, b_cur, hr_cur, g_first, (int)(g_last - g_first + 1), rows, tid, &s_last);
     }
-    if (c_next >= c_end) break;
+    if (!more) break;
     c = c_next;
     __syncthreads();  // the LDS merge buffers are rewritten by the next piece
   }

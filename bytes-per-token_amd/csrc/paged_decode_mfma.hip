@@ -326,7 +326,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, kMfmaWavesPerSimd) void decode_m
   const int kq = lane >> 4, n = lane & 15;
   const int B = p.B;
 
-  build_segment_line<NW, kMChunk>(p, s_prefix, s_len, s_wsum);
+  build_segment_line<NW, kMChunk>(p, s_prefix, s_len, s_wsum, p.piece_cost);
   zero_empty_sequences<NT>(p, s_prefix);
 
   // ---- this workgroup's range of chunks (segments are (sequence, KV head): HR = Hkv) ---------------------
@@ -349,14 +349,23 @@ __global__ __launch_bounds__(kDecodeWaves * 64, kMfmaWavesPerSimd) void decode_m
     }
     b = sread(lo);
   }
-  int nb = sread(s_prefix[b + 1] - s_prefix[b]);
+  // A segment spans X line units, then its nb chunks; a range that starts among the X units starts with
+  // the segment's first chunk.
+  const int X = p.piece_cost;
+  int span = sread(s_prefix[b + 1] - s_prefix[b]);
+  int nb = span - X;
   int h, k;
   {
     const int64_t r = c - (int64_t)HR * s_prefix[b];
-    h = sread((int)(r / nb));
-    k = sread((int)(r - (int64_t)h * nb));
+    h = sread((int)(r / span));
+    k = sread(max((int)(r - (int64_t)h * span) - X, 0));
   }
   const int rows = p.Q * p.G;
+  {
+    // A range that holds no chunk (it lies within one segment's X units) has nothing to do.
+    const int64_t seg_c0 = (int64_t)HR * s_prefix[b] + (int64_t)h * span;
+    if (min(c_end, seg_c0 + span) - seg_c0 - X <= k) return;
+  }
 
   // The first piece's q rows and first chunk are requested before the loop; every later piece's while the
   // previous piece's waves are merged.
@@ -367,14 +376,15 @@ __global__ __launch_bounds__(kDecodeWaves * 64, kMfmaWavesPerSimd) void decode_m
   float qscale = p.qscale * (SK == kScaleHead ? load_uniform(p.ks + h) : 1.0f);
   mfma_load_q<KV, QS>(p, b, h, rows, len, lane, qb, rlen);
   {
-    const int k_end = k + (int)(min(c_end, (int64_t)HR * s_prefix[b] + (int64_t)h * nb + nb) - c);
+    const int64_t seg_c0 = (int64_t)HR * s_prefix[b] + (int64_t)h * span;
+    const int k_end = (int)(min(c_end, seg_c0 + span) - seg_c0 - X);
     if (k + wave < k_end) mfma_issue<SK, PU>(p, b, h, k + wave, len, lane, cr);
   }
 
   for (;;) {
-    const int64_t seg_c0 = (int64_t)HR * s_prefix[b] + (int64_t)h * nb;
-    const int64_t pe = min(c_end, seg_c0 + nb);
-    const int k_end = k + (int)(pe - c);
+    const int64_t seg_c0 = (int64_t)HR * s_prefix[b] + (int64_t)h * span;
+    const int64_t pe = min(c_end, seg_c0 + span);
+    const int k_end = (int)(pe - seg_c0 - X);  // this piece's chunks: [k, k_end)
 
     float m = kNegInf, l = 0.0f;
     f32x4 o[8];
@@ -392,9 +402,11 @@ __global__ __launch_bounds__(kDecodeWaves * 64, kMfmaWavesPerSimd) void decode_m
       kk = kn;
     }
 
-    // The next piece (if any): its q rows and this wave's first chunk go in flight now.
+    // The next piece (if the range holds chunks of the next segment): its q rows and this wave's first
+    // chunk go in flight now.
     const int b_cur = b, h_cur = h, nb_cur = nb;
     const int64_t c_next = pe;
+    bool more = false;
     if (c_next < c_end) {
       ++h;
       k = 0;
@@ -404,12 +416,17 @@ __global__ __launch_bounds__(kDecodeWaves * 64, kMfmaWavesPerSimd) void decode_m
           ++b;
         } while (s_prefix[b + 1] == s_prefix[b]);
         b = sread(b);
-        nb = sread(s_prefix[b + 1] - s_prefix[b]);
+        span = sread(s_prefix[b + 1] - s_prefix[b]);
+        nb = span - X;
       }
-      len = sread(s_len[b]);
-      qscale = p.qscale * (SK == kScaleHead ? load_uniform(p.ks + h) : 1.0f);
-      mfma_load_q<KV, QS>(p, b, h, rows, len, lane, qb, rlen);
-      if (wave < (int)min((int64_t)nb, c_end - c_next)) mfma_issue<SK, PU>(p, b, h, wave, len, lane, cr);
+      const int kn_end = (int)min((int64_t)nb, c_end - c_next - X);
+      more = kn_end > 0;
+      if (more) {
+        len = sread(s_len[b]);
+        qscale = p.qscale * (SK == kScaleHead ? load_uniform(p.ks + h) : 1.0f);
+        mfma_load_q<KV, QS>(p, b, h, rows, len, lane, qb, rlen);
+        if (wave < kn_end) mfma_issue<SK, PU>(p, b, h, wave, len, lane, cr);
+      }
     }
 
     // This wave's state of row n: the four lanes' weight sums added, stored for the workgroup merge.
@@ -428,8 +445,8 @@ __global__ __launch_bounds__(kDecodeWaves * 64, kMfmaWavesPerSimd) void decode_m
 
     // ---- merge the waves; write the segment's output, or this piece's partial ---------------------
     const int seg = b_cur * HR + h_cur;
-    const int64_t g_first = seg_c0 / per;
-    const int64_t g_last = (seg_c0 + nb_cur - 1) / per;
+    const int64_t g_first = (seg_c0 + X) / per;  // the workgroups holding the segment's first and last chunks
+    const int64_t g_last = (seg_c0 + X + nb_cur - 1) / per;
     const bool whole = g_first == g_last;
     const int64_t wslot = (int64_t)seg + g;
     const float vscale_head = SK == kScaleHead ? load_uniform(p.vs + h_cur) : 1.0f;
@@ -464,7 +481,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, kMfmaWavesPerSimd) void decode_m
       __syncthreads();
       arrive_and_combine<RG, NT>(p, seg, b_cur, h_cur, g_first, (int)(g_last - g_first + 1), rows, tid, &s_last);
     }
-    if (c_next >= c_end) break;
+    if (!more) break;
     c = c_next;
     __syncthreads();  // the LDS merge buffers are rewritten by the next piece
   }
