@@ -84,8 +84,6 @@ struct DecodeParams {
   float qscale;      // sm_scale * log2(e)
   int q_dtype, out_dtype, table_i64;
   int noncausal;        // every query sees all of its sequence's tokens
-  int xcd_major;        // number the stream-K line XCD-major (per-token scales: the KV heads of a sequence
-                        // share scale cache lines); else round-robin over the XCDs
   int len_offset;       // subtracted from every context length
   float* lse_out;       // optional [B, Q, Hq]: each row's log-sum-exp (natural log)
   const float* merge_out;  // optional [B, Q, Hq, D]: another token range's normalized partial, merged into out

@@ -294,7 +294,6 @@ int bpt_paged_decode(const bpt_decode_args* a, void* stream) {
   p.out_dtype = a->out_dtype;
   p.table_i64 = a->table_dtype == BPT_IDX_I64;
   p.noncausal = (a->flags & BPT_DECODE_NONCAUSAL) != 0;
-  p.xcd_major = a->scale_kind == BPT_SCALE_PER_TOKEN_HEAD;
   p.len_offset = a->len_offset;
   p.lse_out = a->lse_out;
   p.merge_out = a->merge_out;

@@ -183,13 +183,11 @@ __device__ __forceinline__ void write_out(const DecodeParams& p, int b, int qi, 
 }
 
 // This workgroup's place on the stream-K line. Workgroups are dispatched to the 8 XCDs round-robin (block x
-// runs on XCD x % 8, each XCD with its own L2). XCD-major numbering gives XCD k one contiguous stretch of
-// the line, so neighbouring ranges meet in one L2: the KV heads of one sequence, whose per-token scales
-// share cache lines. Round-robin numbering (the default) instead puts the same KV head of different
-// sequences, which share prefix pages, in one L2 when every range is one segment.
-__device__ __forceinline__ int64_t line_index(const DecodeParams& p) {
+// runs on XCD x % 8, each XCD with its own L2), and the line is numbered XCD-major: XCD k takes one
+// contiguous stretch of it. Neighbouring ranges then meet in one L2: the KV heads of a sequence (one page
+// holds all of them, and per-token scales share cache lines across them) and the ranges of one segment.
+__device__ __forceinline__ int64_t line_index() {
   const int x = blockIdx.x, n = gridDim.x;
-  if (!p.xcd_major) return x;
   const int q = n >> 3, r = n & 7, k = x & 7;
   return (int64_t)k * q + min(k, r) + (x >> 3);
 }
