@@ -42,7 +42,7 @@ constexpr int kMChunk = 32;  // tokens per chunk: two 16-token tiles
 struct MChunk {
   U4 k[2][2];          // tile t, load j: token 16 t + 8 j + l / 8, bytes 16 (l % 8) .. 16 (l % 8) + 15
   u32x2 v[2][4];       // tile t, token 4 kq + i: channels 8 n .. 8 n + 7
-  float ks[8], vs[8];  // per-token scales of tokens 16 t + 4 kq + i (index 4 t + i)
+  float sc1;           // per-token scales: lane l holds tile l / 32's token l % 16, K (l / 16 even) or V
 };
 
 __device__ __forceinline__ u32x2 load8(const uint8_t* p) { return __builtin_nontemporal_load((const u32x2*)p); }
@@ -114,15 +114,15 @@ __device__ __forceinline__ void mfma_issue_v(const DecodeParams& p, int b, int h
       const int e = mfma_page<PU>(p, b, T0 + 16 * t, tok, len);
       const int64_t row = (int64_t)e * p.kv_sblk + (int64_t)(tok & (p.P - 1)) * p.kv_stok;
       c.v[t][i] = load8(p.v + row + head_off + 8 * n);
-      if constexpr (SK == kScaleTokenHead) {
-        const int64_t so = (int64_t)e * p.sc_sblk + (int64_t)(tok & (p.P - 1)) * p.sc_stok + (int64_t)h * p.sc_shead;
-        c.ks[4 * t + i] = p.ks[so];
-        c.vs[4 * t + i] = p.vs[so];
-      } else {
-        c.ks[4 * t + i] = 1.0f;
-        c.vs[4 * t + i] = 1.0f;
-      }
     }
+  }
+  if constexpr (SK == kScaleTokenHead) {
+    // One scale per lane (32 tokens x K and V); mfma_compute spreads them through LDS.
+    const int t = lane >> 5;
+    const int tok = min(T0 + 16 * t + (lane & 15), len - 1);
+    const int e = mfma_page<PU>(p, b, T0 + 16 * t, tok, len);
+    const int64_t so = (int64_t)e * p.sc_sblk + (int64_t)(tok & (p.P - 1)) * p.sc_stok + (int64_t)h * p.sc_shead;
+    c.sc1 = ((lane >> 4) & 1 ? p.vs : p.ks)[so];
   }
 }
 
@@ -190,13 +190,23 @@ struct MQ {
 // `after_scores` runs once the chunk's K registers are consumed (the caller issues the next chunk's K loads
 // there, so they fly during this chunk's softmax and value products).
 template <int KV, int SK, bool QS, typename AfterScores>
-__device__ __forceinline__ void mfma_compute(MChunk& c, U4 (&sk)[2][16][8], int kk, int lane,
+__device__ __forceinline__ void mfma_compute(MChunk& c, U4 (&sk)[2][16][8], float (&ssc)[64], int kk, int lane,
                                              const typename MQ<KV, QS>::T (&qb)[MQ<KV, QS>::kOps], float qscale,
                                              int rlen, float& m, float& l, f32x4 (&o)[8], AfterScores after_scores) {
   const int T0 = kk * kMChunk;
   const int kq = lane >> 4;
   U4 kr[2][2];
   mfma_k_operand(c, sk, lane, kr);
+  // Per-token scales of this lane's score tokens 16 t + 4 kq + i: ks4[t][i] (K), vs4[t][i] (V).
+  f32x4 ks4[2], vs4[2];
+  if constexpr (SK == kScaleTokenHead) {
+    ssc[lane] = c.sc1;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      ks4[t] = *(const f32x4*)&ssc[32 * t + 4 * kq];
+      vs4[t] = *(const f32x4*)&ssc[32 * t + 16 + 4 * kq];
+    }
+  }
   float sc[8];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
@@ -219,7 +229,7 @@ __device__ __forceinline__ void mfma_compute(MChunk& c, U4 (&sk)[2][16][8], int 
     for (int i = 0; i < 4; ++i) {
       const int tok = T0 + 16 * t + 4 * kq + i;
       float x = st[i] * qscale;
-      if constexpr (SK == kScaleTokenHead) x *= c.ks[4 * t + i];
+      if constexpr (SK == kScaleTokenHead) x *= ks4[t][i];
       sc[4 * t + i] = tok < rlen ? x : kNegInf;
     }
   }
@@ -246,7 +256,7 @@ __device__ __forceinline__ void mfma_compute(MChunk& c, U4 (&sk)[2][16][8], int 
   for (int j = 0; j < 8; ++j) {
     const float e = fast_exp2(sc[j] - base);
     l += e;
-    pb[j] = (_Float16)(e * c.vs[j]);
+    pb[j] = (_Float16)(SK == kScaleTokenHead ? e * vs4[j >> 2][j & 3] : e);
   }
 
   // ---- O^T += V^T P^T: eight M-tiles of 16 channels (tile mu: channels 8 n' + mu) -------------------------
@@ -319,6 +329,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, kMfmaWavesPerSimd) void decode_m
   __shared__ float s_l[NW][RG];
   __shared__ float s_o[NW][RG][D];
   __shared__ U4 s_k[NW][2][16][8];  // each wave's K rows of one chunk, on their way to the operand layout
+  __shared__ float s_sc[NW][64];    // each wave's per-token scales of one chunk
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -395,7 +406,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, kMfmaWavesPerSimd) void decode_m
     // the next chunk's K loads are issued as soon as kk's scores are done, its V loads after kk's values.
     for (int kk = k + wave; kk < k_end;) {
       const int kn = kk + NW;
-      mfma_compute<KV, SK, QS>(cr, s_k[wave], kk, lane, qb, qscale, rlen, m, l, o, [&]() {
+      mfma_compute<KV, SK, QS>(cr, s_k[wave], s_sc[wave], kk, lane, qb, qscale, rlen, m, l, o, [&]() {
         if (kn < k_end) mfma_issue_k<PU>(p, b, h, kn, len, lane, cr);
       });
       if (kn < k_end) mfma_issue_v<SK, PU>(p, b, h, kn, len, lane, cr);
