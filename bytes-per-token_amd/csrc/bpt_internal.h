@@ -32,7 +32,7 @@
 namespace bpt {
 
 constexpr int kHeadDim = 128;
-// Largest batch the decode kernel takes: its chunk-count prefix sum lives in LDS.
+// Largest batch the decode kernel takes: its per-sequence prefix sum lives in LDS.
 constexpr int kMaxBatch = 4096;
 // Waves per decode workgroup.
 constexpr int kDecodeWaves = BPT_DECODE_WAVES;

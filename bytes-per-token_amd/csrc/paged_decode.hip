@@ -7,8 +7,9 @@
 // the log-sum-exp algebra of reference.merge_partials.
 //
 // Work decomposition (stream-K): a segment is one (sequence, KV head, row group) and owns ceil(len / CHUNK)
-// chunks; segments are laid end to end (sequence-major) and the launched workgroups split that line into
-// equal contiguous ranges, so ragged batches and long contexts balance to within one chunk. Each
+// chunks, preceded on the line by a few units that stand for the cost of one more piece merge; segments are
+// laid end to end (sequence-major) and the launched workgroups split that line into equal contiguous
+// ranges (numbered XCD-major), so ragged batches and long contexts balance to within one chunk. Each
 // workgroup computes the chunk counts' prefix sum itself and keeps it, with the lengths, in LDS (lengths
 // stay on the device), then walks its range segment by segment ("pieces"). The waves of a workgroup take
 // a piece's chunks round-robin; each chunk's block-table entries are read while the previous chunk is
@@ -382,7 +383,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
   constexpr int CL = decode_loads(RG);
   constexpr int CH = CL * KvTraits<KV>::kRowsPerLoad;
 
-  extern __shared__ int s_dyn[];  // [B + 1] chunks per sequence (exclusive prefix sum), then [B] lengths
+  extern __shared__ int s_dyn[];  // [B + 1] line cost per sequence (exclusive prefix sum), then [B] lengths
   int* s_prefix = s_dyn;
   int* s_len = s_dyn + p.B + 1;
   __shared__ int s_wsum[NW];
@@ -570,7 +571,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
 template <int KV, int SK, int RG>
 static hipError_t launch_t(const DecodeParams& p, bool page_uniform, hipStream_t stream) {
   dim3 grid(p.grid), block(kDecodeWaves * 64);
-  const size_t lds = (size_t)(2 * p.B + 1) * sizeof(int);  // the chunk-count prefix sum and the lengths
+  const size_t lds = (size_t)(2 * p.B + 1) * sizeof(int);  // the line's cost prefix sum and the lengths
   // A non-bf16 q needs the hi + lo split on the dot-product paths; the INT8 path reads q as floats.
   const bool qs = KV != kKvInt8 && p.q_dtype != kFBf16;
   if (page_uniform && !qs)

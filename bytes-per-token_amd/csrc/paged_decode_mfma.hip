@@ -11,8 +11,9 @@
 // l = lane, n = l % 16 (this lane's row), kq = l / 16:
 //  * scores S^T = K Q^T with v_mfma_f32_16x16x32_bf16, four K-steps of 32 channels per tile. A = K rows
 //    (lane: token 16 t + n, channels 32 kq + 8 s .. + 7 at step s: 32 contiguous bytes per lane, FP8
-//    decoded to bf16 exactly); B = Q^T (lane: row n, the same channels, from registers). The result
-//    gives lane l the scores of row n for tokens 16 t + 4 kq + i (i < 4), t = 0, 1: eight per lane.
+//    decoded to bf16 exactly; loaded as whole 128-byte rows and rearranged through LDS); B = Q^T (lane:
+//    row n, the same channels, from registers). The result gives lane l the scores of row n for tokens
+//    16 t + 4 kq + i (i < 4), t = 0, 1: eight per lane.
 //  * online softmax per row over those eight values; the row's four lanes agree on the maximum through
 //    two shuffles and keep partial weight sums that are added at the end.
 //  * output O^T += V^T P^T with v_mfma_f32_16x16x32_f16: the contraction index k = 8 kq + j is mapped to
@@ -320,7 +321,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, kMfmaWavesPerSimd) void decode_m
   constexpr int D = kHeadDim;
   constexpr int RG = kMRows;
 
-  extern __shared__ int s_dyn[];  // [B + 1] chunks per sequence (exclusive prefix sum), then [B] lengths
+  extern __shared__ int s_dyn[];  // [B + 1] line cost per sequence (exclusive prefix sum), then [B] lengths
   int* s_prefix = s_dyn;
   int* s_len = s_dyn + p.B + 1;
   __shared__ int s_wsum[NW];
