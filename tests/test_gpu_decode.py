@@ -245,6 +245,17 @@ def test_many_short_sequences_share_workgroups():
             assert got[i].float().abs().sum().item() == 0
 
 
+@pytest.mark.parametrize("fmt,scales", [("fp8", "head"), ("int8", "token"), ("bf16", None)])
+def test_segments_of_one_chunk_mostly_overhead_units(fmt, scales):
+    """1500 sequences of 1..40 tokens: each segment is one or two chunks behind its piece-cost units, so
+    many workgroup ranges hold no chunk at all (they return at once) and many start among a segment's
+    units (they start at its first chunk)."""
+    lengths = [int(x) for x in np.random.default_rng(5).integers(1, 41, 1500)]
+    c = make_case(fmt, lengths, scales=scales, pool_extra=3)
+    got, want = run_case(c)
+    check(got, want, f"{fmt}: 1500 sequences of one or two chunks")
+
+
 def test_workspace_counters_reset_between_calls_of_different_shapes():
     """One cached workspace serves calls of different shapes in a row; an explicit zeroed one works too."""
     from bpt_amd import decode_plan, paged_decode_attention
