@@ -211,6 +211,57 @@ __device__ __forceinline__ void zero_empty_sequences(const DecodeParams& p, cons
 // Count this workgroup's arrival at segment `seg` (its partial is stored and complete); the last of its n
 // pieces (workspace slots seg + first ...) to arrive combines them, as reference.merge_partials does (base
 // 2), writes the rows and resets the counter. Called by the whole workgroup; s_flag is one LDS int.
+// The combine of one segment's n pieces (workspace slots seg + first ..), CPC channels per thread.
+template <int RG, int NT, int CPC>
+__device__ __forceinline__ void combine_rows(const DecodeParams& p, int seg, int b, int hh, int rg, int64_t first,
+                                             int n, int live, int tid) {
+  constexpr int D = kHeadDim;
+  for (int idx = tid; idx < live * (D / CPC); idx += NT) {
+    const int r = idx / (D / CPC);
+    const int ch = CPC * (idx - r * (D / CPC));
+    const int gr = rg * RG + r;
+    const float* lse = p.ws_lse + ((int64_t)seg + first) * RG + r;
+    const float* prt = p.ws_out + (((int64_t)seg + first) * RG + r) * D + ch;
+    float M = kNegInf, W = 0.0f;  // running maximum and weight
+    float O[CPC];                 // weighted outputs
+#pragma unroll
+    for (int c = 0; c < CPC; ++c) O[c] = 0.0f;
+    for (int j0 = 0; j0 < n; j0 += 8) {
+      float lv[8], ov[8][CPC];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const bool in = j0 + j < n;
+        lv[j] = in ? ws_load(lse + (int64_t)(j0 + j) * RG) : kNegInf;
+#pragma unroll
+        for (int c = 0; c < CPC; ++c) ov[j][c] = in ? ws_load(prt + (int64_t)(j0 + j) * RG * D + c) : 0.0f;
+      }
+      float bm = lv[0];
+#pragma unroll
+      for (int j = 1; j < 8; ++j) bm = fmaxf(bm, lv[j]);
+      const float nm = fmaxf(M, bm);
+      const float mu = nm == kNegInf ? 0.0f : nm;
+      const float alpha = W > 0.0f ? fast_exp2(M - mu) : 0.0f;
+      W *= alpha;
+#pragma unroll
+      for (int c = 0; c < CPC; ++c) O[c] *= alpha;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float e = fast_exp2(lv[j] - mu);  // 0 for empty pieces (lse -inf)
+        W += e;
+#pragma unroll
+        for (int c = 0; c < CPC; ++c) O[c] = fmaf(e, ov[j][c], O[c]);
+      }
+      M = nm;
+    }
+    const int qi = gr / p.G;
+    const int hq = hh * p.G + (gr - qi * p.G);
+    const float inv = W > 0.0f ? 1.0f / W : 0.0f;
+    const float lse2 = W > 0.0f ? M + __log2f(W) : kNegInf;
+#pragma unroll
+    for (int c = 0; c < CPC; ++c) write_out(p, b, qi, hq, ch + c, O[c] * inv, lse2);
+  }
+}
+
 template <int RG, int NT>
 __device__ __forceinline__ void arrive_and_combine(const DecodeParams& p, int seg, int b, int hr, int64_t first, int n,
                                                    int rows, int tid, int* s_flag) {
@@ -224,42 +275,12 @@ __device__ __forceinline__ void arrive_and_combine(const DecodeParams& p, int se
   ws_acquire();
   const int hh = hr / p.n_rg;
   const int rg = hr - hh * p.n_rg;
-  for (int idx = tid; idx < RG * D; idx += NT) {
-    const int r = idx / D;
-    const int ch = idx - r * D;
-    const int gr = rg * RG + r;
-    if (gr >= rows) continue;
-    const float* lse = p.ws_lse + ((int64_t)seg + first) * RG + r;
-    const float* prt = p.ws_out + (((int64_t)seg + first) * RG + r) * D + ch;
-    float M = kNegInf, W = 0.0f, O = 0.0f;  // running maximum, weight and weighted output
-    for (int j0 = 0; j0 < n; j0 += 8) {
-      float lv[8], ov[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const bool in = j0 + j < n;
-        lv[j] = in ? ws_load(lse + (int64_t)(j0 + j) * RG) : kNegInf;
-        ov[j] = in ? ws_load(prt + (int64_t)(j0 + j) * RG * D) : 0.0f;
-      }
-      float bm = lv[0];
-#pragma unroll
-      for (int j = 1; j < 8; ++j) bm = fmaxf(bm, lv[j]);
-      const float nm = fmaxf(M, bm);
-      const float mu = nm == kNegInf ? 0.0f : nm;
-      const float alpha = W > 0.0f ? fast_exp2(M - mu) : 0.0f;
-      W *= alpha;
-      O *= alpha;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float e = fast_exp2(lv[j] - mu);  // 0 for empty pieces (lse -inf)
-        W += e;
-        O = fmaf(e, ov[j], O);
-      }
-      M = nm;
-    }
-    const int qi = gr / p.G;
-    const int hq = hh * p.G + (gr - qi * p.G);
-    write_out(p, b, qi, hq, ch, W > 0.0f ? O / W : 0.0f, W > 0.0f ? M + __log2f(W) : kNegInf);
-  }
+  const int live = min(RG, rows - rg * RG);  // this row group's real rows
+  // CPC channels of one row per thread, every piece's loads issued before they are combined: four when that
+  // still keeps the whole workgroup busy, fewer for few rows.
+  if (live * (D / 4) >= NT) combine_rows<RG, NT, 4>(p, seg, b, hh, rg, first, n, live, tid);
+  else if (live * (D / 2) >= NT) combine_rows<RG, NT, 2>(p, seg, b, hh, rg, first, n, live, tid);
+  else combine_rows<RG, NT, 1>(p, seg, b, hh, rg, first, n, live, tid);
   if (tid == 0) __hip_atomic_store(p.counters + seg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 

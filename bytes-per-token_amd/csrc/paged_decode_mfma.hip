@@ -328,7 +328,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, kMfmaWavesPerSimd) void decode_m
   __shared__ int s_last;
   __shared__ float s_m[NW][RG];
   __shared__ float s_l[NW][RG];
-  __shared__ float s_o[NW][RG][D];
+  __shared__ __attribute__((aligned(16))) float s_o[NW][RG][D];
   __shared__ U4 s_k[NW][2][16][8];  // each wave's K rows of one chunk, on their way to the operand layout
   __shared__ float s_sc[NW][64];    // each wave's per-token scales of one chunk
 
@@ -462,30 +462,34 @@ __global__ __launch_bounds__(kDecodeWaves * 64, kMfmaWavesPerSimd) void decode_m
     const bool whole = g_first == g_last;
     const int64_t wslot = (int64_t)seg + g;
     const float vscale_head = SK == kScaleHead ? load_uniform(p.vs + h_cur) : 1.0f;
-    for (int idx = tid; idx < RG * D; idx += NT) {
-      const int r = idx / D;
-      const int ch = idx - r * D;
-      if (r >= rows) continue;
+    // Four channels of one row per thread, rows < `rows` only.
+    for (int idx = tid; idx < rows * (D / 4); idx += NT) {
+      const int r = idx / (D / 4);
+      const int ch = 4 * (idx - r * (D / 4));
       float M = kNegInf;
 #pragma unroll
       for (int w = 0; w < NW; ++w) M = fmaxf(M, s_m[w][r]);
       const float mu = M == kNegInf ? 0.0f : M;
-      float L = 0.0f, A = 0.0f;
+      float L = 0.0f;
+      f32x4 A = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int w = 0; w < NW; ++w) {
         const float lw = s_l[w][r];
         const float e = lw > 0.0f ? fast_exp2(s_m[w][r] - mu) : 0.0f;
         L += lw * e;
-        A += lw > 0.0f ? s_o[w][r][ch] * e : 0.0f;
+        if (lw > 0.0f) A += *(const f32x4*)&s_o[w][r][ch] * e;
       }
-      const float out = L > 0.0f ? A / L * vscale_head : 0.0f;
+      const float f = L > 0.0f ? vscale_head / L : 0.0f;
+      const float lse2 = L > 0.0f ? M - kBias + __log2f(L) : kNegInf;
       if (whole) {
         const int qi = r / p.G;
         const int hq = h_cur * p.G + (r - qi * p.G);
-        write_out(p, b_cur, qi, hq, ch, out, L > 0.0f ? M - kBias + __log2f(L) : kNegInf);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) write_out(p, b_cur, qi, hq, ch + j, A[j] * f, lse2);
       } else {
-        ws_store(p.ws_out + (wslot * RG + r) * D + ch, out);
-        if (ch == 0) ws_store(p.ws_lse + wslot * RG + r, L > 0.0f ? M - kBias + __log2f(L) : kNegInf);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ws_store(p.ws_out + (wslot * RG + r) * D + ch + j, A[j] * f);
+        if (ch == 0) ws_store(p.ws_lse + wslot * RG + r, lse2);
       }
     }
     if (!whole) {
