@@ -1,0 +1,51 @@
+"""GPU: a seeded sweep of paged decode configurations against the oracle, at the decode tolerance
+(|got - want| <= 2e-3 + 1e-2 * |want|).
+
+Each case draws the batch size, ragged lengths (zeros and one-token rows included), query and KV head
+counts, queries per sequence, page size, cache format and scale granularity, q dtype and split count from
+one seed, so both kernels, the stream-K line walk (pieces, split segments, ranges that hold no chunk) and
+the split-K combine meet many combinations that the targeted tests in test_gpu_decode.py do not spell out.
+Sizes stay small enough for the oracle to finish in well under a second per case.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from test_gpu_decode import check, make_case, run_case
+
+pytestmark = pytest.mark.gpu
+
+FORMATS = [("fp8", "head"), ("fp8", "token"), ("int8", "token"), ("int8", "head"), ("bf16", None)]
+HEADS = [(8, 8), (16, 8), (32, 8), (12, 4), (40, 8), (64, 4)]
+
+
+def draw(seed: int) -> dict:
+    g = np.random.default_rng(1000 + seed)
+    fmt, scales = FORMATS[g.integers(len(FORMATS))]
+    hq, hkv = HEADS[g.integers(len(HEADS))]
+    nq = int(g.choice([1, 1, 2, 3, 5]))
+    while nq * hq // hkv > 16 and nq > 1:  # keep Q * G within one 16-row group now and then
+        nq -= 1
+    b = int(g.integers(1, 24))
+    cap = int(g.choice([40, 300, 1200, 2500]))
+    lengths = [int(x) for x in g.integers(0, cap + 1, b)]
+    lengths[int(g.integers(b))] = int(g.choice([0, 1, cap]))
+    return dict(
+        fmt=fmt, scales=scales, hq=hq, hkv=hkv, nq=nq, lengths=lengths,
+        page=int(g.choice([8, 16, 16, 32, 64])),
+        q_dtype=[torch.bfloat16, torch.float16, torch.float32][int(g.integers(3))],
+        num_splits=[None, None, 1, 3, 17][int(g.integers(5))],
+    )
+
+
+@pytest.mark.parametrize("seed", range(64))
+def test_random_configuration(seed):
+    cfg = draw(seed)
+    c = make_case(cfg["fmt"], cfg["lengths"], hq=cfg["hq"], hkv=cfg["hkv"], nq=cfg["nq"], page=cfg["page"],
+                  scales=cfg["scales"] or "head", seed=seed)
+    got, want = run_case(c, q=c["q"].to(cfg["q_dtype"]), num_splits=cfg["num_splits"])
+    check(got, want, f"seed {seed}: {cfg}")
+    for i, t in enumerate(cfg["lengths"]):
+        if t == 0:
+            assert got[i].float().abs().sum().item() == 0, f"seed {seed}: row {i} has no tokens"
