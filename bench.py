@@ -114,10 +114,13 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def timed_calls(call, flush, steps: int, warmup: int):
+def timed_calls(call, flush, steps: int, warmup: int, call_ev=None):
     """Warmup, then `steps` cold calls: (ms per call from HIP events, wall seconds of the timed region).
 
-    Each call is one kernel launch, so the events bracket exactly the decode kernel.
+    Each call is one kernel launch. With `call_ev` (a decode call taking two raw hipEvent_t handles), the
+    launch itself records the events around its kernel (bpt_paged_decode_timed), which is the kernel's
+    duration as rocprofv3 reports it; otherwise events recorded on the stream bracket the call and add a few
+    microseconds of their own.
     """
     import torch
 
@@ -126,13 +129,21 @@ def timed_calls(call, flush, steps: int, warmup: int):
     torch.cuda.synchronize()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    if call_ev is not None:
+        for e in starts + ends:  # torch creates an event on its first record
+            e.record()
+        if not all(e.cuda_event for e in starts + ends):
+            call_ev = None
     torch.cuda.synchronize()  # barrier: one rank, so the synchronize is the barrier
     t0 = time.perf_counter()
     for i in range(steps):
         flush.run()
-        starts[i].record()
-        call()
-        ends[i].record()
+        if call_ev is not None:
+            call_ev(starts[i].cuda_event, ends[i].cuda_event)
+        else:
+            starts[i].record()
+            call()
+            ends[i].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     return [s.elapsed_time(e) for s, e in zip(starts, ends)], wall
@@ -150,7 +161,10 @@ def measure_workload(name: str, flush, iters: int, warmup: int) -> dict:
     def call():
         paged_decode_attention(*args, **kw, out=out)
 
-    total, _ = timed_calls(call, flush, iters, warmup)
+    def call_ev(start, stop):
+        paged_decode_attention(*args, **kw, out=out, _events=(start, stop))
+
+    total, _ = timed_calls(call, flush, iters, warmup, call_ev)
     graph = measure.graph_time_ms(call, calls=10, warmup=2, iters=10)
     nbytes = w.kv_bytes()
     med = statistics.median(total)
@@ -368,8 +382,11 @@ def main() -> int:
     def call():
         paged_decode_attention(*pargs, **kw, out=out)
 
+    def call_ev(start, stop):
+        paged_decode_attention(*pargs, **kw, out=out, _events=(start, stop))
+
     log(f"timing {args.steps} cold steps after {args.warmup} warmup")
-    total, wall = timed_calls(call, flush, args.steps, args.warmup)
+    total, wall = timed_calls(call, flush, args.steps, args.warmup, call_ev)
     nbytes = w.kv_bytes()
     ms_per_step = statistics.fmean(total)
     value = nbytes / (ms_per_step * 1e-3) / 1e9
@@ -411,7 +428,8 @@ def main() -> int:
             "kv_bytes_per_call": nbytes,
             "workgroups": groups,
             "chunk_tokens": chunk_tokens,
-            "timing": f"HIP events around each call, {args.flush_bytes >> 20} MiB read flush before each (untimed)",
+            "timing": f"HIP events recorded by each call's kernel launch (hipExtLaunchKernel), {args.flush_bytes >> 20} "
+                      "MiB read flush before each (untimed)",
         },
         "us_per_call": round(ms_per_step * 1e3, 2),
         "us_per_call_median": round(statistics.median(total) * 1e3, 2),

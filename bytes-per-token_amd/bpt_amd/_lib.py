@@ -195,6 +195,7 @@ SIGNATURES = {
         [ctypes.POINTER(DecodeArgs), ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)],
     ),
     "bpt_paged_decode": (_i32, [ctypes.POINTER(DecodeArgs), _vp]),
+    "bpt_paged_decode_timed": (_i32, [ctypes.POINTER(DecodeArgs), _vp, _vp, _vp]),
     "bpt_quant_append": (_i32, [ctypes.POINTER(AppendArgs), _vp]),
     "bpt_kivi_plan": (
         _i32,
@@ -210,7 +211,7 @@ SIGNATURES = {
     "bpt_copy_probe": (_i32, [_vp, _vp, ctypes.c_uint64, _vp]),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 
 class BptError(RuntimeError):

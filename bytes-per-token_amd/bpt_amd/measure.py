@@ -83,6 +83,28 @@ def event_times_ms(fn: Callable[[], object], *, warmup: int, iters: int, flush: 
     return [s.elapsed_time(e) for s, e in zip(starts, ends)]
 
 
+def kernel_event_times_ms(fn: Callable[[int, int], object], *, warmup: int, iters: int,
+                          flush: ReadProbe | None = None) -> list[float]:
+    """Milliseconds of the kernel itself per call: `fn(start, stop)` launches with the two raw hipEvent_t
+    handles recorded around its kernel (bpt_paged_decode_timed), so the separate event records of
+    event_times_ms, which add their own microseconds to a single launch, stay out of the interval. With
+    `flush`, the probe reads its buffer before every timed call (not timed)."""
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
+    for e in starts + ends:  # creates the events (torch does so on first record)
+        e.record()
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        fn(starts[0].cuda_event, ends[0].cuda_event)
+    torch.cuda.synchronize()
+    for i in range(iters):
+        if flush is not None:
+            flush.run()
+        fn(starts[i].cuda_event, ends[i].cuda_event)
+    torch.cuda.synchronize()
+    return [s.elapsed_time(e) for s, e in zip(starts, ends)]
+
+
 def graph_time_ms(fn: Callable[[], object], *, calls: int = 20, warmup: int = 3, iters: int = 20) -> list[float]:
     """Per-call milliseconds of `fn` replayed from a HIP graph holding `calls` copies (timing.py:102-123)."""
     side = torch.cuda.Stream()

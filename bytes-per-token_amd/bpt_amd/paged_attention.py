@@ -198,6 +198,7 @@ def paged_decode_attention(
     counters: torch.Tensor | None = None,
     lse: torch.Tensor | None = None,
     _cascade: dict | None = None,
+    _events: tuple | None = None,
 ) -> torch.Tensor:
     """softmax(q kᵀ · scale) v over each sequence's paged cache, dequantized in registers.
 
@@ -264,7 +265,11 @@ def paged_decode_attention(
         _require(t.device == dev and t.is_contiguous(), f"{name} must be a contiguous tensor on q's device")
     a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     a.counters, a.counters_bytes = counters.data_ptr(), counters.numel() * counters.element_size()
-    _lib.check(lib.bpt_paged_decode(ctypes.byref(a), ctypes.c_void_p(stream)))
+    if _events is None:
+        _lib.check(lib.bpt_paged_decode(ctypes.byref(a), ctypes.c_void_p(stream)))
+    else:  # measurement: two raw hipEvent_t handles recorded around the kernel itself
+        _lib.check(lib.bpt_paged_decode_timed(ctypes.byref(a), ctypes.c_void_p(stream), ctypes.c_void_p(_events[0]),
+                                              ctypes.c_void_p(_events[1])))
     result = out if out is not None else out4
     return result[:, 0] if (squeeze and result.dim() == 4) else result
 

@@ -1,6 +1,7 @@
 // Kernel parameter blocks and launchers shared between the kernel files and the C-ABI layer.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -160,8 +161,22 @@ constexpr int kKiviBf16 = 3;
 
 int decode_rows_per_load(int kv_dtype);
 int decode_chunk_tokens(int kv_dtype, int rows_per_group);
-hipError_t launch_decode(const DecodeParams& p, int kv_dtype, int scale_kind, int rows_per_group, hipStream_t stream);
-hipError_t launch_decode_mfma(const DecodeParams& p, int kv_dtype, int scale_kind, hipStream_t stream);
+// Optional events recorded around a kernel's own execution (hipExtLaunchKernel) when `start` is set.
+struct LaunchEvents {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+
+template <typename K, typename P>
+inline void launch_kernel(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t stream, const LaunchEvents& ev,
+                          const P& p) {
+  if (ev.start) hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, stream, ev.start, ev.stop, 0u, p);
+  else hipLaunchKernelGGL(kernel, grid, block, lds, stream, p);
+}
+
+hipError_t launch_decode(const DecodeParams& p, int kv_dtype, int scale_kind, int rows_per_group, hipStream_t stream,
+                         const LaunchEvents& ev = {});
+hipError_t launch_decode_mfma(const DecodeParams& p, int kv_dtype, int scale_kind, hipStream_t stream,
+                              const LaunchEvents& ev = {});
 hipError_t launch_kivi(const KiviParams& p, int fmt, hipStream_t stream);
 hipError_t launch_norm_quant(const NormQuantParams& p, bool vec8, hipStream_t stream);
 hipError_t launch_append(const AppendParams& p, int kv_dtype, int scale_kind, int head_dim, hipStream_t stream);

@@ -222,12 +222,20 @@ int bpt_decode_plan(bpt_decode_args* args, size_t* workspace_bytes, size_t* coun
   return BPT_OK;
 }
 
-int bpt_paged_decode(const bpt_decode_args* a, void* stream) {
-  const char* fn = "bpt_paged_decode";
+namespace {
+
+int paged_decode(const bpt_decode_args* a, void* stream, const bpt::LaunchEvents& ev, const char* fn) {
   Plan pl;
   int rc = make_plan(a, &pl);
   if (rc) return rc;
-  if (a->batch == 0) return BPT_OK;
+  if (a->batch == 0) {
+    if (ev.start) {  // nothing to launch: the interval is empty
+      hipError_t e = hipEventRecord(ev.start, (hipStream_t)stream);
+      if (e == hipSuccess) e = hipEventRecord(ev.stop, (hipStream_t)stream);
+      if (e != hipSuccess) return hip_fail(fn, e);
+    }
+    return BPT_OK;
+  }
   if (!a->q || !a->k_cache || !a->v_cache || !a->block_table || !a->out)
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: q, caches, block_table and out must be non-NULL", fn);
   if ((a->merge_out == nullptr) != (a->merge_lse == nullptr))
@@ -298,10 +306,23 @@ int bpt_paged_decode(const bpt_decode_args* a, void* stream) {
   p.lse_out = a->lse_out;
   p.merge_out = a->merge_out;
   p.merge_lse = a->merge_lse;
-  hipError_t e = pl.mfma ? bpt::launch_decode_mfma(p, a->kv_dtype, a->scale_kind, (hipStream_t)stream)
-                         : bpt::launch_decode(p, a->kv_dtype, a->scale_kind, pl.rows_per_group, (hipStream_t)stream);
+  hipError_t e = pl.mfma ? bpt::launch_decode_mfma(p, a->kv_dtype, a->scale_kind, (hipStream_t)stream, ev)
+                         : bpt::launch_decode(p, a->kv_dtype, a->scale_kind, pl.rows_per_group, (hipStream_t)stream, ev);
   if (e != hipSuccess) return hip_fail(fn, e);
   return BPT_OK;
+}
+
+}  // namespace
+
+int bpt_paged_decode(const bpt_decode_args* a, void* stream) { return paged_decode(a, stream, {}, "bpt_paged_decode"); }
+
+int bpt_paged_decode_timed(const bpt_decode_args* a, void* stream, void* start_event, void* stop_event) {
+  const char* fn = "bpt_paged_decode_timed";
+  if (!start_event || !stop_event) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: both events are required", fn);
+  bpt::LaunchEvents ev;
+  ev.start = (hipEvent_t)start_event;
+  ev.stop = (hipEvent_t)stop_event;
+  return paged_decode(a, stream, ev, fn);
 }
 
 int bpt_kivi_plan(bpt_kivi_args* args, size_t* workspace_bytes, size_t* counters_bytes) {

@@ -569,28 +569,28 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
 }
 
 template <int KV, int SK, int RG>
-static hipError_t launch_t(const DecodeParams& p, bool page_uniform, hipStream_t stream) {
+static hipError_t launch_t(const DecodeParams& p, bool page_uniform, hipStream_t stream, const LaunchEvents& ev) {
   dim3 grid(p.grid), block(kDecodeWaves * 64);
   const size_t lds = (size_t)(2 * p.B + 1) * sizeof(int);  // the line's cost prefix sum and the lengths
   // A non-bf16 q needs the hi + lo split on the dot-product paths; the INT8 path reads q as floats.
   const bool qs = KV != kKvInt8 && p.q_dtype != kFBf16;
   if (page_uniform && !qs)
-    hipLaunchKernelGGL((decode_kernel<KV, SK, RG, true, false>), grid, block, lds, stream, p);
+    launch_kernel(decode_kernel<KV, SK, RG, true, false>, grid, block, lds, stream, ev, p);
   else if (page_uniform)
-    hipLaunchKernelGGL((decode_kernel<KV, SK, RG, true, KV != kKvInt8>), grid, block, lds, stream, p);
+    launch_kernel(decode_kernel<KV, SK, RG, true, KV != kKvInt8>, grid, block, lds, stream, ev, p);
   else if (!qs)
-    hipLaunchKernelGGL((decode_kernel<KV, SK, RG, false, false>), grid, block, lds, stream, p);
+    launch_kernel(decode_kernel<KV, SK, RG, false, false>, grid, block, lds, stream, ev, p);
   else
-    hipLaunchKernelGGL((decode_kernel<KV, SK, RG, false, KV != kKvInt8>), grid, block, lds, stream, p);
+    launch_kernel(decode_kernel<KV, SK, RG, false, KV != kKvInt8>, grid, block, lds, stream, ev, p);
   return hipGetLastError();
 }
 
 template <int KV, int SK>
-static hipError_t launch_rg(const DecodeParams& p, int rg, bool pu, hipStream_t stream) {
+static hipError_t launch_rg(const DecodeParams& p, int rg, bool pu, hipStream_t stream, const LaunchEvents& ev) {
   switch (rg) {
-    case 1: return launch_t<KV, SK, 1>(p, pu, stream);
-    case 2: return launch_t<KV, SK, 2>(p, pu, stream);
-    case 4: return launch_t<KV, SK, 4>(p, pu, stream);
+    case 1: return launch_t<KV, SK, 1>(p, pu, stream, ev);
+    case 2: return launch_t<KV, SK, 2>(p, pu, stream, ev);
+    case 4: return launch_t<KV, SK, 4>(p, pu, stream, ev);
     default: return hipErrorInvalidValue;
   }
 }
@@ -603,15 +603,16 @@ int decode_rows_per_load(int kv_dtype) {
   return kv_dtype == kKvBf16 ? KvTraits<kKvBf16>::kRowsPerLoad : KvTraits<kKvFp8>::kRowsPerLoad;
 }
 
-hipError_t launch_decode(const DecodeParams& p, int kv_dtype, int scale_kind, int rows_per_group, hipStream_t stream) {
+hipError_t launch_decode(const DecodeParams& p, int kv_dtype, int scale_kind, int rows_per_group, hipStream_t stream,
+                         const LaunchEvents& ev) {
   const bool pu = p.P >= decode_rows_per_load(kv_dtype);
-  if (kv_dtype == kKvBf16) return launch_rg<kKvBf16, kScaleNone>(p, rows_per_group, pu, stream);
-  if (kv_dtype == kKvFp8 && scale_kind == kScaleHead) return launch_rg<kKvFp8, kScaleHead>(p, rows_per_group, pu, stream);
+  if (kv_dtype == kKvBf16) return launch_rg<kKvBf16, kScaleNone>(p, rows_per_group, pu, stream, ev);
+  if (kv_dtype == kKvFp8 && scale_kind == kScaleHead) return launch_rg<kKvFp8, kScaleHead>(p, rows_per_group, pu, stream, ev);
   if (kv_dtype == kKvFp8 && scale_kind == kScaleTokenHead)
-    return launch_rg<kKvFp8, kScaleTokenHead>(p, rows_per_group, pu, stream);
-  if (kv_dtype == kKvInt8 && scale_kind == kScaleHead) return launch_rg<kKvInt8, kScaleHead>(p, rows_per_group, pu, stream);
+    return launch_rg<kKvFp8, kScaleTokenHead>(p, rows_per_group, pu, stream, ev);
+  if (kv_dtype == kKvInt8 && scale_kind == kScaleHead) return launch_rg<kKvInt8, kScaleHead>(p, rows_per_group, pu, stream, ev);
   if (kv_dtype == kKvInt8 && scale_kind == kScaleTokenHead)
-    return launch_rg<kKvInt8, kScaleTokenHead>(p, rows_per_group, pu, stream);
+    return launch_rg<kKvInt8, kScaleTokenHead>(p, rows_per_group, pu, stream, ev);
   return hipErrorInvalidValue;
 }
 

@@ -504,26 +504,27 @@ __global__ __launch_bounds__(kDecodeWaves * 64, kMfmaWavesPerSimd) void decode_m
 }
 
 template <int KV, int SK>
-static hipError_t launch_mfma_sk(const DecodeParams& p, bool pu, bool qs, hipStream_t stream) {
+static hipError_t launch_mfma_sk(const DecodeParams& p, bool pu, bool qs, hipStream_t stream, const LaunchEvents& ev) {
   dim3 grid(p.grid), block(kDecodeWaves * 64);
   const size_t lds = (size_t)(2 * p.B + 1) * sizeof(int);
-  if (pu && !qs) hipLaunchKernelGGL((decode_mfma_kernel<KV, SK, true, false>), grid, block, lds, stream, p);
-  else if (pu) hipLaunchKernelGGL((decode_mfma_kernel<KV, SK, true, true>), grid, block, lds, stream, p);
-  else if (!qs) hipLaunchKernelGGL((decode_mfma_kernel<KV, SK, false, false>), grid, block, lds, stream, p);
-  else hipLaunchKernelGGL((decode_mfma_kernel<KV, SK, false, true>), grid, block, lds, stream, p);
+  if (pu && !qs) launch_kernel(decode_mfma_kernel<KV, SK, true, false>, grid, block, lds, stream, ev, p);
+  else if (pu) launch_kernel(decode_mfma_kernel<KV, SK, true, true>, grid, block, lds, stream, ev, p);
+  else if (!qs) launch_kernel(decode_mfma_kernel<KV, SK, false, false>, grid, block, lds, stream, ev, p);
+  else launch_kernel(decode_mfma_kernel<KV, SK, false, true>, grid, block, lds, stream, ev, p);
   return hipGetLastError();
 }
 
-hipError_t launch_decode_mfma(const DecodeParams& p, int kv_dtype, int scale_kind, hipStream_t stream) {
+hipError_t launch_decode_mfma(const DecodeParams& p, int kv_dtype, int scale_kind, hipStream_t stream,
+                              const LaunchEvents& ev) {
   const bool pu = p.P >= 16;
   // q needs the hi + lo split when it carries more bits than the score MFMA's type.
   const bool qs = kv_dtype == kKvInt8 ? p.q_dtype == kFF32 : p.q_dtype != kFBf16;
-  if (kv_dtype == kKvFp8 && scale_kind == kScaleHead) return launch_mfma_sk<kKvFp8, kScaleHead>(p, pu, qs, stream);
+  if (kv_dtype == kKvFp8 && scale_kind == kScaleHead) return launch_mfma_sk<kKvFp8, kScaleHead>(p, pu, qs, stream, ev);
   if (kv_dtype == kKvFp8 && scale_kind == kScaleTokenHead)
-    return launch_mfma_sk<kKvFp8, kScaleTokenHead>(p, pu, qs, stream);
-  if (kv_dtype == kKvInt8 && scale_kind == kScaleHead) return launch_mfma_sk<kKvInt8, kScaleHead>(p, pu, qs, stream);
+    return launch_mfma_sk<kKvFp8, kScaleTokenHead>(p, pu, qs, stream, ev);
+  if (kv_dtype == kKvInt8 && scale_kind == kScaleHead) return launch_mfma_sk<kKvInt8, kScaleHead>(p, pu, qs, stream, ev);
   if (kv_dtype == kKvInt8 && scale_kind == kScaleTokenHead)
-    return launch_mfma_sk<kKvInt8, kScaleTokenHead>(p, pu, qs, stream);
+    return launch_mfma_sk<kKvInt8, kScaleTokenHead>(p, pu, qs, stream, ev);
   return hipErrorInvalidValue;
 }
 

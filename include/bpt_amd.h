@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define BPT_ABI_VERSION 5
+#define BPT_ABI_VERSION 6
 
 /* return codes */
 #define BPT_OK 0
@@ -292,6 +292,12 @@ int bpt_fp8_decode_table(float* out256, void* stream);
 
 /* out[i] = e4m3fn(clamp(x[i] / scale, -448, 448)), the FP8 write-path encoder, for n floats. */
 int bpt_fp8_encode(const float* x, float scale, uint8_t* out, int64_t n, void* stream);
+
+/* bpt_paged_decode whose kernel launch also records two HIP events (hipEvent_t, created with timing) around
+ * the kernel's own execution, through hipExtLaunchKernel: the benchmark's per-call kernel time, free of the
+ * cost of separate event records. No reference counterpart. With nothing to launch (batch 0) both events
+ * are recorded on the stream at once. */
+int bpt_paged_decode_timed(const bpt_decode_args* args, void* stream, void* start_event, void* stop_event);
 
 /* Streaming read of `bytes` (multiple of 16) from buf; one float per workgroup into partial_sums. The
  * measured-peak probe, and the cache flush run before cold timings. Returns the workgroup count used

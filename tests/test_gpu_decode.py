@@ -256,6 +256,29 @@ def test_segments_of_one_chunk_mostly_overhead_units(fmt, scales):
     check(got, want, f"{fmt}: 1500 sequences of one or two chunks")
 
 
+def test_timed_entry_records_the_kernel_and_matches_the_plain_call():
+    """bpt_paged_decode_timed: the same output as bpt_paged_decode, and two events around the kernel whose
+    interval is positive (and empty for a batch with nothing to launch)."""
+    from bpt_amd import paged_decode_attention
+
+    c = make_case("fp8", [300, 77, 1024])
+    kw = dict(scale=0.0883883, max_context=1024)
+    args = (c["q"], c["k"], c["v"], c["table"], c["lens"], c["ks"], c["vs"])
+    want = paged_decode_attention(*args, **kw)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    stop.record()
+    torch.cuda.synchronize()
+    got = paged_decode_attention(*args, **kw, _events=(start.cuda_event, stop.cuda_event))
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert start.elapsed_time(stop) > 0.0
+    empty = (c["q"][:0], c["k"], c["v"], c["table"][:0], c["lens"][:0], c["ks"], c["vs"])
+    paged_decode_attention(*empty, **kw, _events=(start.cuda_event, stop.cuda_event))
+    torch.cuda.synchronize()
+    assert start.elapsed_time(stop) >= 0.0
+
+
 def test_workspace_counters_reset_between_calls_of_different_shapes():
     """One cached workspace serves calls of different shapes in a row; an explicit zeroed one works too."""
     from bpt_amd import decode_plan, paged_decode_attention
