@@ -1,7 +1,7 @@
 """The oracle: a CPU restatement (numpy) of fastserve's arithmetic for the paged decode-attention path.
 
 TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg may import
-this package, and only as the checker (or the timed CPU baseline), never as part of the product path. The
+this package, and only to check results (or as the timed CPU baseline), never as part of the product path. The
 HIP library has no CPU fallback and never calls into this package.
 
 Each function cites the fastserve file:line (relative to src/fastserve/) whose arithmetic it restates:
