@@ -49,6 +49,27 @@ def profiled_traffic(kernel: str, workload: str) -> dict | None:
     return {"bytes": int(m.group(1)), "source": f"profiles/{path.name}"} if m else None
 
 
+def append_call(w):
+    """The decode step's quantize-on-write on workload `w`: one new bf16 K/V row per sequence and KV head,
+    written into slot 15 of the sequence's last page. Returns (call, {"read": bytes, "written": bytes})."""
+    import torch
+
+    from bpt_amd import quantize_append
+
+    b, hkv = w.shape.batch, w.shape.kv_heads
+    g = torch.Generator(device="cuda:0").manual_seed(5)
+    k_new = torch.randn((b, 1, hkv, 128), generator=g, device="cuda:0").to(torch.bfloat16)
+    v_new = torch.randn((b, 1, hkv, 128), generator=g, device="cuda:0").to(torch.bfloat16)
+    last = torch.tensor([row[-1] for row in w.extra["tables"]], dtype=torch.int32, device="cuda:0").view(b, 1)
+    offs = torch.full((b, 1), 15, dtype=torch.int32, device="cuda:0")
+
+    def write():
+        quantize_append(k_new, v_new, w.k_cache, w.v_cache, w.k_scale, w.v_scale, last, offs)
+
+    scale_bytes = 4 if w.k_scale is not None and w.k_scale.dim() == 3 else 0
+    return write, {"read": b * hkv * 128 * 2 * 2, "written": b * hkv * (128 + scale_bytes) * 2}
+
+
 def profile_pass(args) -> int:
     """A short run for rocprofv3: cold decode calls on the workload, then three 256 MiB copies.
 
@@ -92,9 +113,12 @@ def profile_pass(args) -> int:
             from bpt_amd import cascade_decode_attention
 
             kw = {**kw, "prefix_pages": w.shape.shared_prefix_pages}
+        write = append_call(w)[0] if args.append else None
         for _ in range(args.warmup + args.steps):
             flush.run()
-            if args.cascade:
+            if write is not None:
+                write()
+            elif args.cascade:
                 cascade_decode_attention(*pargs, **kw, out=out)
             else:
                 paged_decode_attention(*pargs, **kw, out=out)
@@ -152,7 +176,7 @@ def timed_calls(call, flush, steps: int, warmup: int, call_ev=None):
 def measure_workload(name: str, flush, iters: int, warmup: int) -> dict:
     import torch
 
-    from bpt_amd import measure, paged_decode_attention, quantize_append, workloads
+    from bpt_amd import measure, paged_decode_attention, workloads
 
     w = workloads.make(name, device="cuda:0", seed=0)
     out = torch.empty(tuple(w.q.shape), dtype=torch.bfloat16, device="cuda:0")
@@ -202,22 +226,11 @@ def measure_workload(name: str, flush, iters: int, warmup: int) -> dict:
             "logical_gbps": round(nbytes / (cmed * 1e-3) / 1e9, 1),
         }
     if name == "qwen3-1.7b-int8":
-        # The step's quantize-on-write: one new row per sequence into slot 15 of its last page.
-        b, hkv = w.shape.batch, w.shape.kv_heads
-        g = torch.Generator(device="cuda:0").manual_seed(5)
-        k_new = torch.randn((b, 1, hkv, 128), generator=g, device="cuda:0").to(torch.bfloat16)
-        v_new = torch.randn((b, 1, hkv, 128), generator=g, device="cuda:0").to(torch.bfloat16)
-        last = torch.tensor([row_[-1] for row_ in w.extra["tables"]], dtype=torch.int32, device="cuda:0").view(b, 1)
-        offs = torch.full((b, 1), 15, dtype=torch.int32, device="cuda:0")
-
-        def write():
-            quantize_append(k_new, v_new, w.k_cache, w.v_cache, w.k_scale, w.v_scale, last, offs)
-
+        write, row["append_bytes"] = append_call(w)
         wt, _ = timed_calls(write, flush, iters, warmup)
         wg = measure.graph_time_ms(write, calls=20, warmup=2, iters=10)
         row["append_us_per_call"] = round(statistics.median(wt) * 1e3, 2)
         row["append_graph_us_per_call"] = round(statistics.median(wg) * 1e3, 2)
-        row["append_bytes"] = {"read": b * hkv * 128 * 2 * 2, "written": b * hkv * (128 + 4) * 2}
     del w, out
     torch.cuda.empty_cache()
     return row
@@ -354,6 +367,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--profile", action="store_true", help="short run for rocprofv3 (no JSON line)")
     ap.add_argument("--cascade", action="store_true", help="with --profile: the shared-prefix cascade call")
+    ap.add_argument("--append", action="store_true", help="with --profile: the step's quantize-on-write call")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
