@@ -14,6 +14,9 @@
 #ifndef BPT_DECODE_GROUPS_PER_CU
 #define BPT_DECODE_GROUPS_PER_CU 2
 #endif
+#ifndef BPT_DECODE_MIN_CHUNKS_MANY_ROWS
+#define BPT_DECODE_MIN_CHUNKS_MANY_ROWS 8
+#endif
 #ifndef BPT_DECODE_WAVES
 #define BPT_DECODE_WAVES 4
 #endif
@@ -40,6 +43,11 @@ constexpr int kDecodeWaves = BPT_DECODE_WAVES;
 // Compute units of an MI355X; the auto plan launches kDecodeGroupsPerCu workgroups per CU.
 constexpr int kComputeUnits = 256;
 constexpr int kDecodeGroupsPerCu = BPT_DECODE_GROUPS_PER_CU;
+// Matrix-core segments of kManyRows rows or more: the auto plan launches no more workgroups than a
+// max_context batch fills with kDecodeMinChunksManyRows chunks each. Their pieces are dear (the merge,
+// partial and combine of up to 16 rows), so a small batch runs faster on fewer, fuller workgroups.
+constexpr int kManyRows = 8;
+constexpr int kDecodeMinChunksManyRows = BPT_DECODE_MIN_CHUNKS_MANY_ROWS;
 // Stream-K line units charged for each segment start, in chunks: the cost of merging one more piece (the
 // wave merge, the partial's round trip and, for one workgroup, the combine), so that a workgroup whose
 // range starts a segment gets correspondingly fewer chunks.

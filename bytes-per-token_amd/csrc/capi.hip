@@ -120,7 +120,9 @@ int make_plan(const bpt_decode_args* a, Plan* pl) {
   } else {
     pl->per_forced = 0;
     int64_t grid = (int64_t)bpt::kComputeUnits * bpt::kDecodeGroupsPerCu;
-    if (bound_c < grid) grid = bound_c;
+    const int64_t min_chunks = pl->mfma && pl->rows >= bpt::kManyRows ? bpt::kDecodeMinChunksManyRows : 1;
+    const int64_t fill = (bound_c + min_chunks - 1) / min_chunks;
+    if (fill < grid) grid = fill;
     pl->grid = (int)(grid < 1 ? 1 : grid);
   }
   const size_t slots = (size_t)a->batch * pl->HR + pl->grid;

@@ -103,6 +103,21 @@ def test_plan_puts_2_to_16_quantized_rows_in_one_matrix_core_group(built_lib, fm
     assert ws == expected_workspace(16, 8, 16 if fmt == "fp8" else 2, grid)
 
 
+def test_plan_gives_many_row_segments_fuller_workgroups(built_lib):
+    # 10 rows per KV head (5 queries x 2 heads) on the matrix cores: a small batch gets no more workgroups
+    # than 8 chunks each would fill (2 sequences x 8 KV heads x 96 chunks of 32 tokens -> 192)...
+    q, k, v, table, lens, ks, vs = cpu_case("fp8", b=2, nq=5, max_blocks=256, nb=8192)
+    grid, chunk, ws, _ = decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=3072)
+    assert chunk == 32 and grid == 2 * 8 * 96 // 8 and ws == expected_workspace(2, 8, 16, grid)
+    # ... a full batch still fills the chip, and 2 rows per KV head keep one chunk per workgroup as the floor.
+    q, k, v, table, lens, ks, vs = cpu_case("fp8", b=16, nq=5, max_blocks=256, nb=8192)
+    assert decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=3072)[0] == 512
+    q, k, v, table, lens, ks, vs = cpu_case("fp8", b=1, max_blocks=64, nb=64)
+    assert decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=1024)[0] == 8 * 32
+    q, k, v, table, lens, ks, vs = cpu_case("fp8", b=1, nq=5, max_blocks=64, nb=64)
+    assert decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=1024)[0] == 8 * 32 // 8
+
+
 def test_plan_keeps_bf16_on_the_vector_kernel(built_lib):
     # BF16: 3 groups of 4 rows per KV head for 10 rows.
     q, k, v, table, lens, _, _ = cpu_case("bf16", b=16, nq=5, max_blocks=256, nb=8192)
