@@ -256,6 +256,23 @@ def test_segments_of_one_chunk_mostly_overhead_units(fmt, scales):
     check(got, want, f"{fmt}: 1500 sequences of one or two chunks")
 
 
+@pytest.mark.parametrize("fmt,scales", [("fp8", "head"), ("int8", "token")])
+def test_largest_batch(fmt, scales):
+    """The largest batch a call takes (4096 sequences: the per-sequence prefix sum fills the most LDS),
+    with lengths of 0..40 tokens."""
+    from bpt_amd import paged_decode_attention
+
+    lengths = [int(x) for x in np.random.default_rng(9).integers(0, 41, 4096)]
+    c = make_case(fmt, lengths, scales=scales, pool_extra=3)
+    got, want = run_case(c)
+    check(got, want, f"{fmt}: 4096 sequences")
+    with pytest.raises(ValueError, match="batch"):
+        q = torch.zeros((4097, 1, 16, 128), dtype=torch.bfloat16, device=DEV)
+        table = torch.zeros((4097, c["table"].shape[1]), dtype=torch.int32, device=DEV)
+        lens = torch.zeros(4097, dtype=torch.int32, device=DEV)
+        paged_decode_attention(q, c["k"], c["v"], table, lens, c["ks"], c["vs"], scale=0.1, max_context=40)
+
+
 def test_timed_entry_records_the_kernel_and_matches_the_plain_call():
     """bpt_paged_decode_timed: the same output as bpt_paged_decode, and two events around the kernel whose
     interval is positive (and empty for a batch with nothing to launch)."""
