@@ -18,6 +18,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import platform
 import statistics
 import sys
 import time
@@ -337,6 +338,12 @@ def cpu_baseline(name: str, budget_s: float) -> dict:
     while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 10):
         times.append(run(n))
     med = statistics.median(times)
+    cpu_model = platform.processor() or "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu_model = next(line.split(":", 1)[1].strip() for line in f if line.startswith("model name"))
+    except (OSError, StopIteration):
+        pass
     hkv = w.shape.kv_heads
     elem = 2 if w.shape.kv_format == "bf16" else 1
     nbytes = sum(lengths[:n]) * hkv * 128 * 2 * elem
@@ -350,6 +357,7 @@ def cpu_baseline(name: str, budget_s: float) -> dict:
         f"{len(lengths)} sequences ({sum(lengths[:n])} tokens), median of {len(times)} runs: "
         f"{med * 1e3:.1f} ms per run",
         "us_per_call_full_workload_est": round(med / sum(lengths[:n]) * sum(lengths) * 1e6, 1),
+        "cpu": f"{cpu_model}, {os.cpu_count()} logical CPUs visible",
     }
 
 
