@@ -208,9 +208,6 @@ __device__ __forceinline__ void zero_empty_sequences(const DecodeParams& p, cons
   }
 }
 
-// Count this workgroup's arrival at segment `seg` (its partial is stored and complete); the last of its n
-// pieces (workspace slots seg + first ...) to arrive combines them, as reference.merge_partials does (base
-// 2), writes the rows and resets the counter. Called by the whole workgroup; s_flag is one LDS int.
 // The combine of one segment's n pieces (workspace slots seg + first ..), CPC channels per thread.
 template <int RG, int NT, int CPC>
 __device__ __forceinline__ void combine_rows(const DecodeParams& p, int seg, int b, int hh, int rg, int64_t first,
@@ -262,16 +259,12 @@ __device__ __forceinline__ void combine_rows(const DecodeParams& p, int seg, int
   }
 }
 
+// The combine of segment `seg` by the last of its n pieces to arrive (the whole workgroup), which then
+// resets the segment's counter.
 template <int RG, int NT>
-__device__ __forceinline__ void arrive_and_combine(const DecodeParams& p, int seg, int b, int hr, int64_t first, int n,
-                                                   int rows, int tid, int* s_flag) {
+__device__ __forceinline__ void combine_segment(const DecodeParams& p, int seg, int b, int hr, int64_t first, int n,
+                                                int rows, int tid) {
   constexpr int D = kHeadDim;
-  if (tid == 0) {
-    const unsigned prev = __hip_atomic_fetch_add(p.counters + seg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *s_flag = prev == (unsigned)n - 1u;
-  }
-  __syncthreads();
-  if (!*s_flag) return;
   ws_acquire();
   const int hh = hr / p.n_rg;
   const int rg = hr - hh * p.n_rg;
@@ -282,6 +275,20 @@ __device__ __forceinline__ void arrive_and_combine(const DecodeParams& p, int se
   else if (live * (D / 2) >= NT) combine_rows<RG, NT, 2>(p, seg, b, hh, rg, first, n, live, tid);
   else combine_rows<RG, NT, 1>(p, seg, b, hh, rg, first, n, live, tid);
   if (tid == 0) __hip_atomic_store(p.counters + seg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Count this workgroup's arrival at segment `seg` (its partial is stored and complete); the last of its n
+// pieces (workspace slots seg + first ...) to arrive combines them, as reference.merge_partials does (base
+// 2), writes the rows and resets the counter. Called by the whole workgroup; s_flag is one LDS int.
+template <int RG, int NT>
+__device__ __forceinline__ void arrive_and_combine(const DecodeParams& p, int seg, int b, int hr, int64_t first, int n,
+                                                   int rows, int tid, int* s_flag) {
+  if (tid == 0) {
+    const unsigned prev = __hip_atomic_fetch_add(p.counters + seg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *s_flag = prev == (unsigned)n - 1u;
+  }
+  __syncthreads();
+  if (*s_flag) combine_segment<RG, NT>(p, seg, b, hr, first, n, rows, tid);
 }
 
 }  // namespace bpt
