@@ -521,24 +521,28 @@ __device__ __forceinline__ void arrive_and_combine(const KiviParams& p, int seg,
     const int r = idx / D;
     const int ch = idx - r * D;
     float M = kNegInf, W = 0.0f, O = 0.0f;
-    for (int i0 = 0; i0 < n; i0 += 4) {
-      float lv[4], ov[4];
+    // kJ pieces' loads in flight per round: a split over many workgroups is combined in few round trips.
+    constexpr int kJ = 16;
+    for (int i0 = 0; i0 < n; i0 += kJ) {
+      float lv[kJ], ov[kJ];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < kJ; ++i) {
         const int gg = g_first + i0 + i;
         const int64_t slot = (i0 + i == 0 && sc0 != gg * per) ? 2 * gg + 1 : 2 * gg;
         const bool in = i0 + i < n;
         lv[i] = in ? ws_load(p.ws_lse + slot * G + r) : kNegInf;
         ov[i] = in ? ws_load(p.ws_out + (slot * G + r) * D + ch) : 0.0f;
       }
-      float bm = fmaxf(fmaxf(lv[0], lv[1]), fmaxf(lv[2], lv[3]));
+      float bm = lv[0];
+#pragma unroll
+      for (int i = 1; i < kJ; ++i) bm = fmaxf(bm, lv[i]);
       const float nm = fmaxf(M, bm);
       const float mu = nm == kNegInf ? 0.0f : nm;
       const float alpha = W > 0.0f ? fast_exp2(M - mu) : 0.0f;
       W *= alpha;
       O *= alpha;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < kJ; ++i) {
         const float e = fast_exp2(lv[i] - mu);
         W += e;
         O = fmaf(e, ov[i], O);
