@@ -39,7 +39,7 @@ def draw(seed: int) -> dict:
     )
 
 
-@pytest.mark.parametrize("seed", range(64))
+@pytest.mark.parametrize("seed", range(256))
 def test_random_configuration(seed):
     cfg = draw(seed)
     c = make_case(cfg["fmt"], cfg["lengths"], hq=cfg["hq"], hkv=cfg["hkv"], nq=cfg["nq"], page=cfg["page"],
