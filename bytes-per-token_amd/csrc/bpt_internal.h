@@ -43,11 +43,16 @@ constexpr int kDecodeWaves = BPT_DECODE_WAVES;
 // Compute units of an MI355X; the auto plan launches kDecodeGroupsPerCu workgroups per CU.
 constexpr int kComputeUnits = 256;
 constexpr int kDecodeGroupsPerCu = BPT_DECODE_GROUPS_PER_CU;
-// Matrix-core segments of kManyRows rows or more: the auto plan launches no more workgroups than a
-// max_context batch fills with kDecodeMinChunksManyRows chunks each. Their pieces are dear (the merge,
-// partial and combine of up to 16 rows), so a small batch runs faster on fewer, fuller workgroups.
+// Matrix-core segments of kManyRows rows or more run in workgroups of kMfmaManyRowWaves waves, one per CU,
+// and the auto plan launches no more of them than a max_context batch fills with kDecodeMinChunksManyRows
+// chunks each. Their pieces are dear (the merge, partial and combine of up to 16 rows), so fewer, fuller
+// workgroups win.
 constexpr int kManyRows = 8;
+constexpr int kMfmaManyRowWaves = 8;
 constexpr int kDecodeMinChunksManyRows = BPT_DECODE_MIN_CHUNKS_MANY_ROWS;
+// Waves per matrix-core workgroup for segments of `rows` rows, and workgroups per CU.
+constexpr int mfma_waves(int rows) { return rows >= kManyRows ? kMfmaManyRowWaves : kDecodeWaves; }
+constexpr int mfma_groups_per_cu(int rows) { return rows >= kManyRows ? 1 : kDecodeGroupsPerCu; }
 // Stream-K line units charged for each segment start, in chunks: the cost of merging one more piece (the
 // wave merge, the partial's round trip and, for one workgroup, the combine), so that a workgroup whose
 // range starts a segment gets correspondingly fewer chunks.

@@ -109,7 +109,8 @@ int make_plan(const bpt_decode_args* a, Plan* pl) {
     // workgroups, each workgroup takes several consecutive ones whole: inside a workgroup the online
     // softmax simply continues across their boundary (the log-sum-exp merge of the two partials, done in
     // registers), so the partials that go through memory are those of the resident workgroups.
-    const int64_t max_grid = (int64_t)bpt::kComputeUnits * bpt::kDecodeGroupsPerCu;
+    const int64_t max_grid =
+        (int64_t)bpt::kComputeUnits * (pl->mfma ? bpt::mfma_groups_per_cu(pl->rows) : bpt::kDecodeGroupsPerCu);
     int64_t per = (max_nb + a->num_splits - 1) / a->num_splits;
     if (per < 1) per = 1;
     const int64_t parts = (bound_c + per - 1) / per;
@@ -119,7 +120,8 @@ int make_plan(const bpt_decode_args* a, Plan* pl) {
     pl->grid = (int)(grid < 1 ? 1 : grid);
   } else {
     pl->per_forced = 0;
-    int64_t grid = (int64_t)bpt::kComputeUnits * bpt::kDecodeGroupsPerCu;
+    int64_t grid =
+        (int64_t)bpt::kComputeUnits * (pl->mfma ? bpt::mfma_groups_per_cu(pl->rows) : bpt::kDecodeGroupsPerCu);
     const int64_t min_chunks = pl->mfma && pl->rows >= bpt::kManyRows ? bpt::kDecodeMinChunksManyRows : 1;
     const int64_t fill = (bound_c + min_chunks - 1) / min_chunks;
     if (fill < grid) grid = fill;

@@ -314,9 +314,8 @@ __device__ __forceinline__ void mfma_load_q(const DecodeParams& p, int b, int h,
   }
 }
 
-template <int KV, int SK, bool PU, bool QS>
-__global__ __launch_bounds__(kDecodeWaves * 64, kMfmaWavesPerSimd) void decode_mfma_kernel(const DecodeParams p) {
-  constexpr int NW = kDecodeWaves;
+template <int KV, int SK, bool PU, bool QS, int NW>
+__global__ __launch_bounds__(NW * 64, kMfmaWavesPerSimd) void decode_mfma_kernel(const DecodeParams p) {
   constexpr int NT = NW * 64;
   constexpr int D = kHeadDim;
   constexpr int RG = kMRows;
@@ -503,15 +502,21 @@ __global__ __launch_bounds__(kDecodeWaves * 64, kMfmaWavesPerSimd) void decode_m
   }
 }
 
+template <int KV, int SK, int NW>
+static hipError_t launch_mfma_nw(const DecodeParams& p, bool pu, bool qs, hipStream_t stream, const LaunchEvents& ev) {
+  dim3 grid(p.grid), block(NW * 64);
+  const size_t lds = (size_t)(2 * p.B + 1) * sizeof(int);
+  if (pu && !qs) launch_kernel(decode_mfma_kernel<KV, SK, true, false, NW>, grid, block, lds, stream, ev, p);
+  else if (pu) launch_kernel(decode_mfma_kernel<KV, SK, true, true, NW>, grid, block, lds, stream, ev, p);
+  else if (!qs) launch_kernel(decode_mfma_kernel<KV, SK, false, false, NW>, grid, block, lds, stream, ev, p);
+  else launch_kernel(decode_mfma_kernel<KV, SK, false, true, NW>, grid, block, lds, stream, ev, p);
+  return hipGetLastError();
+}
+
 template <int KV, int SK>
 static hipError_t launch_mfma_sk(const DecodeParams& p, bool pu, bool qs, hipStream_t stream, const LaunchEvents& ev) {
-  dim3 grid(p.grid), block(kDecodeWaves * 64);
-  const size_t lds = (size_t)(2 * p.B + 1) * sizeof(int);
-  if (pu && !qs) launch_kernel(decode_mfma_kernel<KV, SK, true, false>, grid, block, lds, stream, ev, p);
-  else if (pu) launch_kernel(decode_mfma_kernel<KV, SK, true, true>, grid, block, lds, stream, ev, p);
-  else if (!qs) launch_kernel(decode_mfma_kernel<KV, SK, false, false>, grid, block, lds, stream, ev, p);
-  else launch_kernel(decode_mfma_kernel<KV, SK, false, true>, grid, block, lds, stream, ev, p);
-  return hipGetLastError();
+  if (mfma_waves(p.Q * p.G) == kMfmaManyRowWaves) return launch_mfma_nw<KV, SK, kMfmaManyRowWaves>(p, pu, qs, stream, ev);
+  return launch_mfma_nw<KV, SK, kDecodeWaves>(p, pu, qs, stream, ev);
 }
 
 hipError_t launch_decode_mfma(const DecodeParams& p, int kv_dtype, int scale_kind, hipStream_t stream,

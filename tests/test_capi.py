@@ -109,8 +109,11 @@ def test_plan_gives_many_row_segments_fuller_workgroups(built_lib):
     q, k, v, table, lens, ks, vs = cpu_case("fp8", b=2, nq=5, max_blocks=256, nb=8192)
     grid, chunk, ws, _ = decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=3072)
     assert chunk == 32 and grid == 2 * 8 * 96 // 8 and ws == expected_workspace(2, 8, 16, grid)
-    # ... a full batch still fills the chip, and 2 rows per KV head keep one chunk per workgroup as the floor.
+    # ... a full batch fills every CU with one 8-wave workgroup, and 2 rows per KV head keep two 4-wave
+    # workgroups per CU and one chunk per workgroup as the floor.
     q, k, v, table, lens, ks, vs = cpu_case("fp8", b=16, nq=5, max_blocks=256, nb=8192)
+    assert decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=3072)[0] == 256
+    q, k, v, table, lens, ks, vs = cpu_case("fp8", b=16, max_blocks=256, nb=8192)
     assert decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=3072)[0] == 512
     q, k, v, table, lens, ks, vs = cpu_case("fp8", b=1, max_blocks=64, nb=64)
     assert decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=1024)[0] == 8 * 32
