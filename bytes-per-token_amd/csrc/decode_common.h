@@ -25,6 +25,17 @@ __device__ __forceinline__ void ws_store(float* ptr, float v) {
 #endif
 }
 
+// Two adjacent floats (8-byte aligned) in one coherent 8-byte store.
+__device__ __forceinline__ void ws_store2(float* ptr, float a, float b) {
+#if BPT_WS_COHERENT
+  const uint64_t bits = (uint64_t)__float_as_uint(a) | ((uint64_t)__float_as_uint(b) << 32);
+  __hip_atomic_store((uint64_t*)ptr, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#else
+  ptr[0] = a;
+  ptr[1] = b;
+#endif
+}
+
 __device__ __forceinline__ float ws_load(const float* ptr) {
 #if BPT_WS_COHERENT
   return __hip_atomic_load(ptr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

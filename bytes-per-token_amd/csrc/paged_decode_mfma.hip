@@ -487,7 +487,7 @@ __global__ __launch_bounds__(NW * 64, kMfmaWavesPerSimd) void decode_mfma_kernel
         for (int j = 0; j < 4; ++j) write_out(p, b_cur, qi, hq, ch + j, A[j] * f, lse2);
       } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) ws_store(p.ws_out + (wslot * RG + r) * D + ch + j, A[j] * f);
+        for (int j = 0; j < 4; j += 2) ws_store2(p.ws_out + (wslot * RG + r) * D + ch + j, A[j] * f, A[j + 1] * f);
         if (ch == 0) ws_store(p.ws_lse + wslot * RG + r, lse2);
       }
     }
