@@ -25,6 +25,17 @@ __device__ __forceinline__ void ws_store(float* ptr, float v) {
 #endif
 }
 
+// Two adjacent floats (8-byte aligned) in one coherent 8-byte load.
+__device__ __forceinline__ void ws_load2(const float* ptr, float& a, float& b) {
+#if BPT_WS_COHERENT
+  const uint64_t bits = __hip_atomic_load((const uint64_t*)ptr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#else
+  const uint64_t bits = *(const uint64_t*)ptr;
+#endif
+  a = __uint_as_float((uint32_t)bits);
+  b = __uint_as_float((uint32_t)(bits >> 32));
+}
+
 // Two adjacent floats (8-byte aligned) in one coherent 8-byte store.
 __device__ __forceinline__ void ws_store2(float* ptr, float a, float b) {
 #if BPT_WS_COHERENT
@@ -240,8 +251,16 @@ __device__ __forceinline__ void combine_rows(const DecodeParams& p, int seg, int
       for (int j = 0; j < 8; ++j) {
         const bool in = j0 + j < n;
         lv[j] = in ? ws_load(lse + (int64_t)(j0 + j) * RG) : kNegInf;
+        if constexpr (CPC % 2 == 0) {
 #pragma unroll
-        for (int c = 0; c < CPC; ++c) ov[j][c] = in ? ws_load(prt + (int64_t)(j0 + j) * RG * D + c) : 0.0f;
+          for (int c = 0; c < CPC; c += 2) {
+            ov[j][c] = ov[j][c + 1] = 0.0f;
+            if (in) ws_load2(prt + (int64_t)(j0 + j) * RG * D + c, ov[j][c], ov[j][c + 1]);
+          }
+        } else {
+#pragma unroll
+          for (int c = 0; c < CPC; ++c) ov[j][c] = in ? ws_load(prt + (int64_t)(j0 + j) * RG * D + c) : 0.0f;
+        }
       }
       float bm = lv[0];
 #pragma unroll
