@@ -18,10 +18,11 @@
 //    two shuffles and keep partial weight sums that are added at the end.
 //  * output O^T += V^T P^T with v_mfma_f32_16x16x32_f16: the contraction index k = 8 kq + j is mapped to
 //    the lane's own score tokens (j < 4: 4 kq + j, j >= 4: 16 + 4 kq + j - 4), so P^T comes straight
-//    from this lane's weights (f16). V^T needs tokens contiguous per lane: the lane loads channels
-//    8 n' .. 8 n' + 7 (n' = l % 16) of its eight tokens (8 bytes each), transposes 4 x 4 byte blocks with
-//    v_perm and decodes FP8 -> f16 exactly; M-tile mu holds channels 8 n' + mu. The accumulator then
-//    gives lane l row n, channels 32 kq + 8 i + mu (i < 4, mu < 8): 32 contiguous channels.
+//    from this lane's weights (f16). V^T needs tokens contiguous per lane: V rows are loaded whole like K
+//    and passed through the same LDS tile, from which the lane reads channels 8 n' .. 8 n' + 7
+//    (n' = l % 16) of its eight tokens (8 bytes each); it transposes 4 x 4 byte blocks with v_perm and
+//    decodes FP8 -> f16 exactly; M-tile mu holds channels 8 n' + mu. The accumulator then gives lane l
+//    row n, channels 32 kq + 8 i + mu (i < 4, mu < 8): 32 contiguous channels.
 // Scales: sm_scale * log2(e) and a per-head K scale multiply the scores, per-token K / V scales the scores
 // and weights, a per-head V scale the output. Softmax is in base 2 with the same lazy reference point as
 // the vector kernel.
@@ -42,11 +43,9 @@ constexpr int kMChunk = 32;  // tokens per chunk: two 16-token tiles
 // This lane's share of one chunk: K for its token of each tile, V for its eight score tokens.
 struct MChunk {
   U4 k[2][2];          // tile t, load j: token 16 t + 8 j + l / 8, bytes 16 (l % 8) .. 16 (l % 8) + 15
-  u32x2 v[2][4];       // tile t, token 4 kq + i: channels 8 n .. 8 n + 7
+  U4 v[2][2];          // tile t, load j: V of token 16 t + 8 j + l / 8, bytes 16 (l % 8) .. + 15 (as k)
   float sc1;           // per-token scales: lane l holds tile l / 32's token l % 16, K (l / 16 even) or V
 };
-
-__device__ __forceinline__ u32x2 load8(const uint8_t* p) { return __builtin_nontemporal_load((const u32x2*)p); }
 
 __device__ __forceinline__ int clamp_page(const DecodeParams& p, int e) {
   return e < 0 ? 0 : (e >= p.num_blocks ? p.num_blocks - 1 : e);
@@ -105,16 +104,17 @@ __device__ __forceinline__ void mfma_k_operand(const MChunk& c, U4 (&sk)[2][16][
 template <int SK, bool PU>
 __device__ __forceinline__ void mfma_issue_v(const DecodeParams& p, int b, int h, int kk, int len, int lane, MChunk& c) {
   const int T0 = kk * kMChunk;
-  const int kq = lane >> 4, n = lane & 15;
-  const int64_t head_off = (int64_t)h * p.kv_shead;
+  {
+    const int r = lane >> 3, sg = lane & 7;
+    const int64_t head_off = (int64_t)h * p.kv_shead + 16 * sg;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
+    for (int t = 0; t < 2; ++t) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int tok = min(T0 + 16 * t + 4 * kq + i, len - 1);
-      const int e = mfma_page<PU>(p, b, T0 + 16 * t, tok, len);
-      const int64_t row = (int64_t)e * p.kv_sblk + (int64_t)(tok & (p.P - 1)) * p.kv_stok;
-      c.v[t][i] = load8(p.v + row + head_off + 8 * n);
+      for (int j = 0; j < 2; ++j) {
+        const int tok = min(T0 + 16 * t + 8 * j + r, len - 1);
+        const int e = mfma_page<PU>(p, b, T0 + 16 * t, tok, len);
+        c.v[t][j] = load16(p.v + (int64_t)e * p.kv_sblk + (int64_t)(tok & (p.P - 1)) * p.kv_stok + head_off);
+      }
     }
   }
   if constexpr (SK == kScaleTokenHead) {
@@ -262,10 +262,30 @@ __device__ __forceinline__ void mfma_compute(MChunk& c, U4 (&sk)[2][16][8], floa
 
   // ---- O^T += V^T P^T: eight M-tiles of 16 channels (tile mu: channels 8 n' + mu) -------------------------
   uint32_t lo[2][4], hi[2][4];  // [tile][j]: channel 8 n' + j (lo) or 8 n' + 4 + j (hi), bytes = tokens i
+  // V rows through the wave's LDS tile (the K operand's reads are done): lane (n', kq) reads channels
+  // 8 n' .. 8 n' + 7 of its score tokens 16 t + 4 kq + i, with the K tile's segment swizzle.
+  u32x2 vw[2][4];
+  {
+    const int r = lane >> 3, sg = lane & 7;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) sk[t][8 * j + r][sg ^ r ^ j] = c.v[t][j];
+    }
+    const int np = lane & 15;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = 4 * kq + i;
+        vw[t][i] = ((const u32x2*)&sk[t][row][(np >> 1) ^ (row & 7) ^ (row >> 3)])[np & 1];
+      }
+    }
+  }
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    transpose4(c.v[t][0].x, c.v[t][1].x, c.v[t][2].x, c.v[t][3].x, lo[t]);
-    transpose4(c.v[t][0].y, c.v[t][1].y, c.v[t][2].y, c.v[t][3].y, hi[t]);
+    transpose4(vw[t][0].x, vw[t][1].x, vw[t][2].x, vw[t][3].x, lo[t]);
+    transpose4(vw[t][0].y, vw[t][1].y, vw[t][2].y, vw[t][3].y, hi[t]);
   }
 #pragma unroll
   for (int mu = 0; mu < 8; ++mu) {
