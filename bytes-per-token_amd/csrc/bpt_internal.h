@@ -26,6 +26,9 @@
 #ifndef BPT_DECODE_PIECE_COST
 #define BPT_DECODE_PIECE_COST 8
 #endif
+#ifndef BPT_DECODE_MANY_ROW_PIECE_COST
+#define BPT_DECODE_MANY_ROW_PIECE_COST 10
+#endif
 #ifndef BPT_DECODE_MFMA_MIN_ROWS
 #define BPT_DECODE_MFMA_MIN_ROWS 2
 #endif
@@ -57,6 +60,9 @@ constexpr int mfma_groups_per_cu(int rows) { return rows >= kManyRows ? 1 : kDec
 // wave merge, the partial's round trip and, for one workgroup, the combine), so that a workgroup whose
 // range starts a segment gets correspondingly fewer chunks.
 constexpr int kDecodePieceCost = BPT_DECODE_PIECE_COST;
+// The same for matrix-core segments of kManyRows rows or more (8-wave workgroups; dearer merges).
+constexpr int kManyRowPieceCost = BPT_DECODE_MANY_ROW_PIECE_COST;
+constexpr int kMaxPieceCost = kDecodePieceCost > kManyRowPieceCost ? kDecodePieceCost : kManyRowPieceCost;
 
 // 16-byte K loads (and V loads) per lane per chunk: fewer for 4-row groups, whose q and accumulators take
 // twice the registers.

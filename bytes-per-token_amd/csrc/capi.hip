@@ -100,7 +100,7 @@ int make_plan(const bpt_decode_args* a, Plan* pl) {
   pl->len_cap = (int)(a->max_context < table_cap ? a->max_context : table_cap);
   const int64_t max_nb = (pl->len_cap + pl->chunk - 1) / pl->chunk;
   const int64_t seq_chunks = (int64_t)a->batch * max_nb;  // bound on the chunk prefix sum
-  const int64_t seq_cost = (int64_t)a->batch * (max_nb + bpt::kDecodePieceCost);  // and on the line's
+  const int64_t seq_cost = (int64_t)a->batch * (max_nb + bpt::kMaxPieceCost);  // and on the line's
   if (seq_cost > 0x7fffffffLL / (hr > 0 ? hr : 1))
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: batch x context x heads too large", fn);
   const int64_t bound_c = seq_chunks * hr;
@@ -299,7 +299,9 @@ int paged_decode(const bpt_decode_args* a, void* stream, const bpt::LaunchEvents
   p.HR = pl.HR;
   p.grid = pl.grid;
   p.per_forced = pl.per_forced;
-  p.piece_cost = pl.per_forced > 0 ? 0 : bpt::kDecodePieceCost;
+  p.piece_cost = pl.per_forced > 0                         ? 0
+                 : pl.mfma && pl.rows >= bpt::kManyRows ? bpt::kManyRowPieceCost
+                                                        : bpt::kDecodePieceCost;
   p.len_cap = pl.len_cap;
   p.qscale = a->sm_scale * bpt::kLog2e;
   p.q_dtype = a->q_dtype;
