@@ -13,6 +13,11 @@ import subprocess
 from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
+try:
+    from . import _lib
+except ImportError:  # run as a script: this directory is on sys.path
+    import _lib
+
 PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR.parent / "csrc"
 INCLUDE = PKG_DIR.parent.parent / "include"
@@ -44,6 +49,8 @@ def hipcc() -> str:
 
 def _compile(src: Path, obj: Path, defines: tuple[str, ...] = ()) -> None:
     cmd = [hipcc(), *HIPCC_FLAGS, *(f"-D{d}" for d in defines), f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
+    if src.name == "capi.hip":  # the sources' hash, which the loader compares with the tree's
+        cmd.insert(1, f'-DBPT_SOURCE_HASH="{_lib.source_hash()}"')
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{proc.stderr}")

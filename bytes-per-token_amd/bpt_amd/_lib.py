@@ -8,9 +8,26 @@ from __future__ import annotations
 
 import ctypes
 import functools
+import hashlib
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libbpt_amd.so"
+CSRC = Path(__file__).resolve().parent.parent / "csrc"
+INCLUDE = Path(__file__).resolve().parent.parent.parent / "include"
+
+
+def source_files() -> list[Path]:
+    """Every file the library is compiled from: csrc/*.hip, csrc/*.h and include/*.h."""
+    return sorted([*CSRC.glob("*.hip"), *CSRC.glob("*.h"), *INCLUDE.glob("*.h")])
+
+
+def source_hash() -> str:
+    """SHA-256 (first 16 hex digits) over the names and contents of the library's sources. The build embeds it
+    in the library (bpt_source_hash), so a library built from other sources is refused at load time."""
+    h = hashlib.sha256()
+    for f in source_files():
+        h.update(f.name.encode() + b"\0" + f.read_bytes() + b"\0")
+    return h.hexdigest()[:16]
 
 BPT_OK = 0
 BPT_ERR_INVALID_ARGUMENT = 1
@@ -205,22 +222,28 @@ SIGNATURES = {
     "bpt_rms_norm_int8": (_i32, [ctypes.POINTER(NormQuantArgs), _vp]),
     "bpt_last_error": (ctypes.c_char_p, []),
     "bpt_abi_version": (_i32, []),
+    "bpt_source_hash": (ctypes.c_char_p, []),
     "bpt_fp8_decode_table": (_i32, [_vp, _vp]),
     "bpt_fp8_encode": (_i32, [_vp, ctypes.c_float, _vp, _i64, _vp]),
     "bpt_read_probe": (_i32, [_vp, ctypes.c_uint64, _vp, ctypes.POINTER(_i64), _vp]),
     "bpt_copy_probe": (_i32, [_vp, _vp, ctypes.c_uint64, _vp]),
 }
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 
 class BptError(RuntimeError):
     """A HIP runtime error reported by the library."""
 
 
+class StaleLibraryError(RuntimeError):
+    """The built library was compiled from other sources than the ones in the tree."""
+
+
 @functools.cache
 def lib() -> ctypes.CDLL:
-    """The loaded library. Raises if it was never built: the kernels have no fallback."""
+    """The loaded library. Raises if it was never built (the kernels have no fallback), or if it was built
+    from sources other than the tree's (a stale build)."""
     if not LIB_PATH.exists():
         raise RuntimeError(
             f"{LIB_PATH} is not built: run `python __graft_entry__.py` (build()) or "
@@ -233,6 +256,10 @@ def lib() -> ctypes.CDLL:
         fn.argtypes = args
     if handle.bpt_abi_version() != ABI_VERSION:
         raise RuntimeError(f"libbpt_amd.so ABI {handle.bpt_abi_version()} != binding {ABI_VERSION}: rebuild")
+    built, tree = handle.bpt_source_hash().decode(), source_hash()
+    if source_files() and built != tree:
+        raise StaleLibraryError(f"{LIB_PATH} was built from sources {built}, the tree holds {tree}: rebuild it "
+                                "(python bytes-per-token_amd/bpt_amd/_build.py)")
     return handle
 
 

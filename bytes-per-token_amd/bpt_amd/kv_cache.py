@@ -30,6 +30,7 @@ import torch
 from .paged_attention import paged_decode_attention, quantize_append
 
 _FORMATS = {torch.float8_e4m3fn: "fp8", torch.int8: "int8", torch.bfloat16: "bf16"}
+HEAD_DIM = 128  # the one head size the paged decode kernels are built for
 
 
 class OutOfBlocksError(RuntimeError):
@@ -73,6 +74,8 @@ class PagedQuantKVCache:
         self.head_dim = head_dim if cfg is None else cfg.head_dim
         if None in (self.num_layers, self.num_kv_heads, self.head_dim):
             raise ValueError("give cfg, or num_layers, num_kv_heads and head_dim")
+        if self.head_dim != HEAD_DIM:  # refuse here, before any attend() could write into the pools
+            raise ValueError(f"head_dim {self.head_dim} not supported: the paged decode kernels take {HEAD_DIM}")
         if block_size < 1 or block_size & (block_size - 1):
             raise ValueError(f"block_size {block_size} must be a power of two")
         self.kv_dtype = kv_dtype
@@ -180,6 +183,6 @@ class PagedQuantKVCache:
         )
         out = paged_decode_attention(
             q.transpose(1, 2), self.k[layer], self.v[layer], meta.block_table, meta.context_lens,
-            self.k_scale[layer], self.v_scale[layer], scale=scale, max_context=meta.kv_len,
-        )  # [B, Q, Hq, D] bf16
-        return out.transpose(1, 2).to(q.dtype)
+            self.k_scale[layer], self.v_scale[layer], scale=scale, max_context=meta.kv_len, out_dtype=q.dtype,
+        )  # [B, Q, Hq, D] in q's dtype: the kernel rounds once, from float32 (integration/kv_cache.py:177-181)
+        return out.transpose(1, 2)

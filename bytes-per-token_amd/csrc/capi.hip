@@ -214,6 +214,11 @@ const char* bpt_last_error(void) { return g_error.c_str(); }
 
 int bpt_abi_version(void) { return BPT_ABI_VERSION; }
 
+#ifndef BPT_SOURCE_HASH
+#define BPT_SOURCE_HASH "unknown"
+#endif
+const char* bpt_source_hash(void) { return BPT_SOURCE_HASH; }
+
 int bpt_decode_plan(bpt_decode_args* args, size_t* workspace_bytes, size_t* counters_bytes) {
   Plan pl;
   int rc = make_plan(args, &pl);

@@ -8,68 +8,41 @@ namespace bpt {
 
 __device__ __forceinline__ int sread(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
-// Cross-workgroup exchange of split-K partials. Workgroups run on different XCDs, whose L2 caches are
-// not coherent with each other. BPT_WS_COHERENT (default): partials are stored and loaded as
-// device-scope relaxed atomics, which gfx950 performs coherently (sc1) without whole-cache maintenance,
-// and publishing only waits for this wave's stores to complete. Otherwise: plain accesses bracketed by
-// device-scope fences (an L2 writeback on the writer, an L2 invalidate on the reader).
-#ifndef BPT_WS_COHERENT
-#define BPT_WS_COHERENT 1
-#endif
+// Cross-workgroup exchange of split-K partials. Workgroups run on different XCDs, whose L2 caches are not
+// coherent with each other. Partials are stored and loaded as agent-scope relaxed (monotonic) atomics, which
+// gfx950 performs coherently at the memory side (the sc1 bit): the stores write through the L2, the loads miss
+// it. Publishing a partial waits for this wave's stores to complete (s_waitcnt vmcnt(0)) before the arrival
+// counter is bumped with an agent-scope atomic; the last arriver then loads every partial with agent-scope
+// atomic loads. This is what LLVM's memory model lowers release / acquire to on this target (a release is
+// "buffer_wbl2 sc1; s_waitcnt vmcnt(0)", an acquire "buffer_inv sc1"), minus the L2 writeback and invalidate,
+// which only non-atomic accesses need: every access to the partials here is itself an agent-scope atomic.
 
 __device__ __forceinline__ void ws_store(float* ptr, float v) {
-#if BPT_WS_COHERENT
   __hip_atomic_store(ptr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#else
-  *ptr = v;
-#endif
 }
 
 // Two adjacent floats (8-byte aligned) in one coherent 8-byte load.
 __device__ __forceinline__ void ws_load2(const float* ptr, float& a, float& b) {
-#if BPT_WS_COHERENT
   const uint64_t bits = __hip_atomic_load((const uint64_t*)ptr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#else
-  const uint64_t bits = *(const uint64_t*)ptr;
-#endif
   a = __uint_as_float((uint32_t)bits);
   b = __uint_as_float((uint32_t)(bits >> 32));
 }
 
 // Two adjacent floats (8-byte aligned) in one coherent 8-byte store.
 __device__ __forceinline__ void ws_store2(float* ptr, float a, float b) {
-#if BPT_WS_COHERENT
   const uint64_t bits = (uint64_t)__float_as_uint(a) | ((uint64_t)__float_as_uint(b) << 32);
   __hip_atomic_store((uint64_t*)ptr, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#else
-  ptr[0] = a;
-  ptr[1] = b;
-#endif
 }
 
 __device__ __forceinline__ float ws_load(const float* ptr) {
-#if BPT_WS_COHERENT
   return __hip_atomic_load(ptr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#else
-  return *ptr;
-#endif
 }
 
-__device__ __forceinline__ void ws_publish() {
-#if BPT_WS_COHERENT
-  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-#else
-  __threadfence();
-#endif
-}
+// Every partial store of this wave has completed (and is visible at the memory side).
+__device__ __forceinline__ void ws_publish() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-__device__ __forceinline__ void ws_acquire() {
-#if BPT_WS_COHERENT
-  __asm__ volatile("" ::: "memory");
-#else
-  __threadfence();
-#endif
-}
+// Keeps the compiler from hoisting the partial loads above the arrival that licenses them.
+__device__ __forceinline__ void ws_acquire() { __asm__ volatile("" ::: "memory"); }
 
 // A load the whole wave makes from one address, through the scalar cache (the data is read-only here).
 template <typename T>
@@ -90,6 +63,17 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 // score seen (log2 units): weights stay below 2^12, well inside f16, and small ones keep f16 precision.
 constexpr float kBias = 4.0f;
 constexpr float kSlack = 8.0f;
+
+// Per-token value scales ride in the f16 weights (w = 2^(score - base) * vscale). The reference point then
+// tracks score + vscale_bound(vscale) instead of the score, where vscale < 2^vscale_bound: the f16 weights
+// stay below 2^(kSlack + kBias) whatever the scale, and scales far below one keep the weights' precision.
+// The weight sums (f32) keep the bare 2^(score - base), so the log-sum-exp is unchanged. The bound is
+// clamped to [-kVscaleExpMax, kVscaleExpMax] so those sums stay finite: scales up to 2^64 are exact.
+constexpr int kVscaleExpMax = 64;
+__device__ __forceinline__ float vscale_bound(float vscale) {
+  const int e = __builtin_amdgcn_frexp_expf(vscale);  // vscale = m * 2^e with m in [0.5, 1); 0 for 0
+  return (float)(e < -kVscaleExpMax ? -kVscaleExpMax : (e > kVscaleExpMax ? kVscaleExpMax : e));
+}
 
 // Round-to-nearest-even float -> bf16 pair.
 __device__ __forceinline__ bf16x2 pack_bf16(float a, float b) {

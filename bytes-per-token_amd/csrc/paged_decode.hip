@@ -229,13 +229,15 @@ __device__ __forceinline__ void compute_chunk(const ChunkRegs<CL>& c, int kk, in
 
   // ---- online softmax. m is a reference point, moved only when a score passes it by kSlack: weights
   // are 2^(score - m + kBias) <= 2^(kSlack + kBias), so the accumulators are rarely rescaled and the
-  // packed f16 weights never overflow. ------------------------------------------------------------------
+  // packed f16 weights never overflow. Per-token value scales ride in the f16 weights of the FP8 path, so
+  // there m tracks score + vscale_bound(vscale) (the weight sums keep the bare exponentials). ------------
+  constexpr bool kScaledF16 = kDotV && SK == kScaleTokenHead;
   float pw[CL][RG];
 #pragma unroll
   for (int r = 0; r < RG; ++r) {
-    float mc = s[0][r];
+    float mc = kNegInf;
 #pragma unroll
-    for (int i = 1; i < CL; ++i) mc = fmaxf(mc, s[i][r]);
+    for (int i = 0; i < CL; ++i) mc = fmaxf(mc, kScaledF16 ? s[i][r] + vscale_bound(c.vs[i]) : s[i][r]);
     const bool move = mc > m[r] + kSlack;
     if (__any(move)) {
       const float mn = move ? mc : m[r];

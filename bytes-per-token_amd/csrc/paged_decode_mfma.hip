@@ -237,9 +237,12 @@ __device__ __forceinline__ void mfma_compute(MChunk& c, U4 (&sk)[2][16][8], floa
   after_scores();
 
   // ---- online softmax of row n over this chunk's 32 tokens (8 here, 24 on the row's other lanes) -------
-  float mx = sc[0];
+  // With per-token value scales the reference point tracks score + vscale_bound(vscale), so that the f16
+  // weights e * vscale stay below 2^(kSlack + kBias).
+  float mx = kNegInf;
 #pragma unroll
-  for (int j = 1; j < 8; ++j) mx = fmaxf(mx, sc[j]);
+  for (int j = 0; j < 8; ++j)
+    mx = fmaxf(mx, SK == kScaleTokenHead ? sc[j] + vscale_bound(vs4[j >> 2][j & 3]) : sc[j]);
   mx = fmaxf(mx, shfl_xor_f(mx, 16));
   mx = fmaxf(mx, shfl_xor_f(mx, 32));
   const bool move = mx > m + kSlack;

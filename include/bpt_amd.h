@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define BPT_ABI_VERSION 6
+#define BPT_ABI_VERSION 7
 
 /* return codes */
 #define BPT_OK 0
@@ -76,7 +76,7 @@ typedef enum { BPT_IDX_I32 = 0, BPT_IDX_I64 = 1 } bpt_index_dtype;
  *   context_lens [B] int32: tokens in the cache for each sequence, the Q new ones included. Query i of
  *                sequence b sits at position context_lens[b] - Q + i and sees slots 0 .. that position.
  *                NULL: every sequence holds max_context tokens.
- *   out          [B, Q, Hq, D] (strides out_stride_{b,q,h}), BF16 or F32
+ *   out          [B, Q, Hq, D] (strides out_stride_{b,q,h}), BF16, F16 or F32
  *
  * max_context bounds context_lens and sizes the launch (no device->host read); lengths above it, or
  * above max_blocks_per_seq * page_size, are truncated to that bound. Page ids are clamped into
@@ -98,7 +98,7 @@ typedef struct {
   int32_t kv_dtype;     /* bpt_kv_dtype   */
   int32_t scale_kind;   /* bpt_scale_kind */
   int32_t q_dtype;      /* bpt_float_dtype */
-  int32_t out_dtype;    /* bpt_float_dtype: BF16 or F32 */
+  int32_t out_dtype;    /* bpt_float_dtype */
   int32_t table_dtype;  /* bpt_index_dtype */
 
   int32_t batch, num_queries, num_q_heads, num_kv_heads, head_dim, page_size;
@@ -284,6 +284,10 @@ const char* bpt_last_error(void);
 
 /* BPT_ABI_VERSION of the built library. */
 int bpt_abi_version(void);
+
+/* Hash of the sources the library was compiled from (the .hip and .h files of csrc and include), so that a binding
+ * can refuse a library built from other sources. No reference counterpart. */
+const char* bpt_source_hash(void);
 
 /* ---- conversion and measurement primitives (used by the tests and the benchmark) ---------------- */
 

@@ -40,7 +40,8 @@ def pytest_collection_modifyitems(config: pytest.Config, items: list[pytest.Item
 
 @pytest.fixture(scope="session")
 def built_lib():
-    """The library, built in-tree first if nothing is built yet."""
+    """The library, built in-tree first if nothing is built yet. A library built from other sources than the
+    tree's is refused (StaleLibraryError), failing every test that uses it."""
     from bpt_amd import _build, _lib
 
     if not _lib.LIB_PATH.exists():

@@ -27,6 +27,15 @@ def test_every_declared_symbol_is_exported(built_lib):
     assert built_lib.bpt_abi_version() == _lib.ABI_VERSION
 
 
+def test_library_matches_the_sources_and_a_stale_one_is_refused(built_lib, monkeypatch):
+    """The library carries the hash of the sources it was built from; loading one built from other sources
+    raises instead of silently running old kernels."""
+    assert built_lib.bpt_source_hash().decode() == _lib.source_hash()
+    monkeypatch.setattr(_lib, "source_hash", lambda: "0123456789abcdef")
+    with pytest.raises(_lib.StaleLibraryError, match="rebuild"):
+        _lib.lib.__wrapped__()
+
+
 def cpu_case(fmt="fp8", b=2, nq=1, hq=16, hkv=8, d=128, nb=64, page=16, max_blocks=8):
     dtype = {"fp8": torch.float8_e4m3fn, "int8": torch.int8, "bf16": torch.bfloat16}[fmt]
     q = torch.zeros((b, nq, hq, d), dtype=torch.bfloat16)

@@ -43,8 +43,8 @@ def oracle_out(w):
 
 
 def make_case(fmt, lengths, hq=16, hkv=8, nq=1, page=16, scales="head", seed=0, pool_extra=5, head_major=False,
-              table_dtype=torch.int32, outliers=True):
-    """A small random paged cache in the given format, quantized with torch ops."""
+              table_dtype=torch.int32, outliers=True, v_mag=1.0):
+    """A small random paged cache in the given format, quantized with torch ops (values ~ N(0, v_mag^2))."""
     from bpt_amd import workloads
 
     gen = torch.Generator().manual_seed(seed)
@@ -63,7 +63,7 @@ def make_case(fmt, lengths, hq=16, hkv=8, nq=1, page=16, scales="head", seed=0, 
     kf = torch.randn((nb, page, hkv, d), generator=g, device=DEV)
     if outliers:
         kf[..., torch.randperm(d, generator=gen)[:4].to(DEV)] *= 8.0
-    vf = torch.randn((nb, page, hkv, d), generator=g, device=DEV)
+    vf = torch.randn((nb, page, hkv, d), generator=g, device=DEV) * v_mag
     ks = vs = None
     if fmt == "bf16":
         kc, vc = kf.to(torch.bfloat16), vf.to(torch.bfloat16)
@@ -349,3 +349,19 @@ def test_matrix_core_path_page_sizes_and_q_dtypes(fmt, scales, page):
     for dt in (torch.float16, torch.float32):
         got, want = run_case(c, q=c["q"].to(dt))
         check(got, want, f"page {page}, q {dt}")
+
+
+@pytest.mark.parametrize("v_mag", [1e-5, 1e-3, 1e4])
+@pytest.mark.parametrize("fmt,nq,hq,hkv", [("fp8", 1, 16, 8), ("fp8", 1, 8, 8), ("int8", 1, 16, 8), ("int8", 3, 16, 8),
+                                           ("int8", 1, 8, 8)])
+def test_per_token_value_scales_far_from_one(fmt, nq, hq, hkv, v_mag):
+    """Per-token value scales of 1e-5 .. 1e4 times those of unit values, on both kernels (FP8 with 2 rows and
+    INT8 with 6 rows on the matrix cores, FP8 with 1 row and INT8 with 1..2 rows on the vector kernel). The
+    scales ride in f16 softmax weights there, so they must neither overflow f16 (large values) nor fall into
+    its subnormals (small ones). Attention is linear in V, so outputs are compared at unit scale:
+    |got - want| / v_mag <= 2e-3 + 1e-2 |want| / v_mag."""
+    c = make_case(fmt, [1030, 5, 64, 2000, 33], nq=nq, hq=hq, hkv=hkv, scales="token", v_mag=v_mag)
+    got, want = run_case(c, out_dtype=torch.float32)
+    check(got / v_mag, want / v_mag, f"{fmt} Q={nq} Hq={hq} Hkv={hkv} values x{v_mag:g}")
+    got, want = run_case(c, out_dtype=torch.float32, num_splits=3)
+    check(got / v_mag, want / v_mag, f"{fmt} Q={nq} Hq={hq} Hkv={hkv} values x{v_mag:g}, 3 splits")
