@@ -212,6 +212,7 @@ SIGNATURES = {
         [ctypes.POINTER(DecodeArgs), ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)],
     ),
     "bpt_paged_decode": (_i32, [ctypes.POINTER(DecodeArgs), _vp]),
+    "bpt_paged_decode_noalloc": (_i32, [ctypes.POINTER(DecodeArgs), _vp]),
     "bpt_paged_decode_timed": (_i32, [ctypes.POINTER(DecodeArgs), _vp, _vp, _vp]),
     "bpt_quant_append": (_i32, [ctypes.POINTER(AppendArgs), _vp]),
     "bpt_kivi_plan": (

@@ -5,6 +5,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "../../include/bpt_amd.h"
@@ -233,10 +234,21 @@ int bpt_decode_plan(bpt_decode_args* args, size_t* workspace_bytes, size_t* coun
 
 namespace {
 
-int paged_decode(const bpt_decode_args* a, void* stream, const bpt::LaunchEvents& ev, const char* fn) {
+// Where a call's split-K partials and arrival counters live: the caller's buffers (bpt_paged_decode) or this
+// device's scratch array (bpt_paged_decode_noalloc).
+struct Buffers {
+  void* workspace;
+  size_t workspace_bytes;
+  void* counters;
+  size_t counters_bytes;
+};
+
+int paged_decode(const bpt_decode_args* a, void* stream, const bpt::LaunchEvents& ev, const char* fn,
+                 const Buffers* own = nullptr) {
   Plan pl;
   int rc = make_plan(a, &pl);
   if (rc) return rc;
+  const Buffers buf = own ? *own : Buffers{a->workspace, a->workspace_bytes, a->counters, a->counters_bytes};
   if (a->batch == 0) {
     if (ev.start) {  // nothing to launch: the interval is empty
       hipError_t e = hipEventRecord(ev.start, (hipStream_t)stream);
@@ -257,12 +269,12 @@ int paged_decode(const bpt_decode_args* a, void* stream, const bpt::LaunchEvents
   if (!aligned16(a->k_cache) || !aligned16(a->v_cache) || (a->kv_stride_block * eb) % 16 ||
       (a->kv_stride_token * eb) % 16 || (a->kv_stride_head * eb) % 16)
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: cache pointers and strides must be 16-byte aligned", fn);
-  if (!a->workspace || a->workspace_bytes < pl.workspace || ((uintptr_t)a->workspace & 255u))
+  if (!buf.workspace || buf.workspace_bytes < pl.workspace || ((uintptr_t)buf.workspace & 255u))
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: a 256-byte aligned workspace of %zu bytes is required (got %zu)", fn,
-                pl.workspace, a->workspace_bytes);
-  if (!a->counters || a->counters_bytes < pl.counters || ((uintptr_t)a->counters & 3u))
+                pl.workspace, buf.workspace_bytes);
+  if (!buf.counters || buf.counters_bytes < pl.counters || ((uintptr_t)buf.counters & 3u))
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: a zeroed counter buffer of %zu bytes is required (got %zu)", fn,
-                pl.counters, a->counters_bytes);
+                pl.counters, buf.counters_bytes);
   if (!aligned_to(a->q, a->q_stride_b, a->q_stride_q, a->q_stride_h, float_bytes(a->q_dtype)))
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: q rows must be 16-byte aligned (pointer and strides)", fn);
 
@@ -288,9 +300,9 @@ int paged_decode(const bpt_decode_args* a, void* stream, const bpt::LaunchEvents
   p.o_sb = a->out_stride_b;
   p.o_sq = a->out_stride_q;
   p.o_sh = a->out_stride_h;
-  p.ws_out = (float*)a->workspace;
-  p.ws_lse = (float*)a->workspace + pl.ws_out_floats;
-  p.counters = (unsigned*)a->counters;
+  p.ws_out = (float*)buf.workspace;
+  p.ws_lse = (float*)buf.workspace + pl.ws_out_floats;
+  p.counters = (unsigned*)buf.counters;
   p.B = a->batch;
   p.Q = a->num_queries;
   p.Hq = a->num_q_heads;
@@ -326,6 +338,85 @@ int paged_decode(const bpt_decode_args* a, void* stream, const bpt::LaunchEvents
 }  // namespace
 
 int bpt_paged_decode(const bpt_decode_args* a, void* stream) { return paged_decode(a, stream, {}, "bpt_paged_decode"); }
+
+}  // extern "C"
+
+// ---- bpt_paged_decode_noalloc: the split-K partials and counters in a device-resident array ---------------
+//
+// `scratch` holds, on every GPU the library runs on, kScratchWorkspace bytes of partials followed by
+// kScratchCounters bytes of arrival counters. The counters sit at a fixed offset, so the invariant that every
+// completed call leaves them zero holds across calls of any shape; they are cleared once per device, by a
+// fill kernel on the first call's stream. In host code `scratch` names a host-side stand-in: its device
+// address, different on each GPU, comes from hipGetSymbolAddress and is the only form passed to kernels.
+namespace {
+
+constexpr size_t kScratchWorkspace = (size_t)30 << 20;
+constexpr size_t kScratchCounters = (size_t)2 << 20;
+constexpr int kMaxDevices = 64;
+
+}  // namespace
+
+static __device__ __align__(256) uint8_t scratch[kScratchWorkspace + kScratchCounters];
+
+namespace {
+
+__global__ void zero_words_kernel(uint32_t* p, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+std::mutex g_scratch_mutex;
+uint8_t* g_scratch[kMaxDevices];  // device address of `scratch` on each GPU, once set up
+
+// This device's scratch address; on the device's first call, looks it up (with the device current) and queues
+// the counters' clear on `stream`.
+int scratch_for(hipStream_t stream, uint8_t** out, const char* fn) {
+  hipDevice_t dev = 0;
+  hipError_t e = hipStreamGetDevice(stream, &dev);
+  if (e != hipSuccess) return hip_fail(fn, e);
+  if (dev < 0 || dev >= kMaxDevices) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: device %d out of range", fn, (int)dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch[dev]) {
+    int cur = 0;
+    e = hipGetDevice(&cur);
+    if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+    void* ptr = nullptr;
+    if (e == hipSuccess) e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (cur != dev) {
+      const hipError_t e2 = hipSetDevice(cur);
+      if (e == hipSuccess) e = e2;
+    }
+    if (e != hipSuccess) return hip_fail(fn, e);
+    uint32_t* counters = (uint32_t*)((uint8_t*)ptr + kScratchWorkspace);
+    hipLaunchKernelGGL(zero_words_kernel, dim3(256), dim3(256), 0, stream, counters, kScratchCounters / 4);
+    e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(fn, e);
+    g_scratch[dev] = (uint8_t*)ptr;
+  }
+  *out = g_scratch[dev];
+  return BPT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int bpt_paged_decode_noalloc(const bpt_decode_args* a, void* stream) {
+  const char* fn = "bpt_paged_decode_noalloc";
+  Plan pl;
+  int rc = make_plan(a, &pl);
+  if (rc) return rc;
+  if (pl.workspace > kScratchWorkspace || pl.counters > kScratchCounters)
+    return fail(BPT_ERR_INVALID_ARGUMENT,
+                "%s: the call needs %zu bytes of partials and %zu of counters; the device scratch holds %zu and %zu "
+                "(use bpt_paged_decode with a caller workspace)",
+                fn, pl.workspace, pl.counters, kScratchWorkspace, kScratchCounters);
+  if (a->batch == 0) return BPT_OK;
+  uint8_t* base = nullptr;
+  rc = scratch_for((hipStream_t)stream, &base, fn);
+  if (rc) return rc;
+  const Buffers own{base, kScratchWorkspace, base + kScratchWorkspace, kScratchCounters};
+  return paged_decode(a, stream, {}, fn, &own);
+}
 
 int bpt_paged_decode_timed(const bpt_decode_args* a, void* stream, void* start_event, void* stop_event) {
   const char* fn = "bpt_paged_decode_timed";

@@ -267,6 +267,15 @@ int bpt_decode_plan(bpt_decode_args* args, size_t* workspace_bytes, size_t* coun
 /* Paged decode attention: one kernel launch, split-K partials combined in the same launch. */
 int bpt_paged_decode(const bpt_decode_args* args, void* stream);
 
+/* bpt_paged_decode with no caller workspace: the split-K partials and arrival counters live in a device-
+ * resident array of the library (30 MiB of partials and 2 MiB of counters on each GPU it runs on, held until the
+ * process ends), so the call allocates nothing: for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference. The
+ * workspace and counters fields of args are ignored; a call whose bpt_decode_plan sizes exceed the array's
+ * returns BPT_ERR_INVALID_ARGUMENT. Calls on one GPU share the array: calls that may overlap (different
+ * streams) race and must not be issued. */
+int bpt_paged_decode_noalloc(const bpt_decode_args* args, void* stream);
+
 /* Quantize-on-write of new K/V rows into their (page, slot). */
 int bpt_quant_append(const bpt_append_args* args, void* stream);
 
