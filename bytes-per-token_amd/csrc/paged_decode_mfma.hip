@@ -470,10 +470,12 @@ __global__ __launch_bounds__(NW * 64, kMfmaWavesPerSimd) void decode_mfma_kernel
       s_m[wave][n] = m;
       s_l[wave][n] = l;
     }
+    if (n < rows) {  // the merge reads real rows only
 #pragma unroll
-    for (int mu = 0; mu < 8; ++mu) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) s_o[wave][n][32 * kq + 8 * i + mu] = o[mu][i];
+      for (int i = 0; i < 4; ++i) {
+        *(f32x4*)&s_o[wave][n][32 * kq + 8 * i] = f32x4{o[0][i], o[1][i], o[2][i], o[3][i]};
+        *(f32x4*)&s_o[wave][n][32 * kq + 8 * i + 4] = f32x4{o[4][i], o[5][i], o[6][i], o[7][i]};
+      }
     }
     __syncthreads();
 
