@@ -136,7 +136,7 @@ class AppendArgs(ctypes.Structure):
     ]
 
 
-KIVI_INT4, KIVI_INT8, KIVI_F16, KIVI_BF16 = 0, 1, 2, 3
+KIVI_INT4, KIVI_INT8, KIVI_F16, KIVI_BF16, KIVI_F32 = 0, 1, 2, 3, 4
 
 
 class KiviArgs(ctypes.Structure):
@@ -230,7 +230,7 @@ SIGNATURES = {
     "bpt_copy_probe": (_i32, [_vp, _vp, ctypes.c_uint64, _vp]),
 }
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 
 class BptError(RuntimeError):

@@ -11,12 +11,14 @@ Mirrors fastserve's kernels/kv_attention.py (paths relative to its src/fastserve
   launch that writes the merged result directly (the splits of one row are combined inside the kernel).
 * `kv` is anything with QuantKV's fields (kernels/reference.py:66-100): bits 4 / 8 with uint8 codes
   [B, Hkv, T, D] (bits 4: [B, Hkv, T, D/2], channel d low nibble, d + D/2 high) and float16 grids
-  k_scale / k_zero [B, Hkv, T/group, D], v_scale / v_zero [B, Hkv, T]; or bits 16 with float16 / bfloat16
-  keys and values and no grids. fastserve's own QuantKV objects work unchanged.
+  k_scale / k_zero [B, Hkv, T/group, D], v_scale / v_zero [B, Hkv, T]; or bits 16 with float16 / bfloat16 /
+  float32 keys and values and no grids. fastserve's own QuantKV objects work unchanged.
 
-`num_warps` is accepted for signature parity and ignored: the launch shape is the library's. Limits: head
-dim 128, at most 16 query heads per KV head, key group and split multiples of 32 tokens, bits-16 caches in
-float16 or bfloat16.
+`num_warps` is accepted for signature parity and ignored: the launch shape is the library's. Head dim 128
+with 4 / 8-bit codes or float16 / bfloat16 caches runs on the matrix-core kernel (key group and split
+multiples of 32 tokens); any other even head dim up to 256 (fastserve's tiny test model has 16) and float32
+bits-16 caches (a float32 model's QuantizedKVCache) run on a float32 kernel with one workgroup per (sequence,
+KV head, split). At most 16 query heads per KV head.
 """
 
 from __future__ import annotations
@@ -28,7 +30,7 @@ from typing import Any
 import torch
 
 from . import _lib
-from ._lib import F_BF16, F_F16, F_F32, KIVI_BF16, KIVI_F16, KIVI_INT4, KIVI_INT8
+from ._lib import F_BF16, F_F16, F_F32, KIVI_BF16, KIVI_F16, KIVI_F32, KIVI_INT4, KIVI_INT8
 from .paged_attention import cached_buffer
 
 _Q_CODES = {torch.bfloat16: F_BF16, torch.float16: F_F16, torch.float32: F_F32}
@@ -56,7 +58,10 @@ def _format(kv: Any) -> int:
             return KIVI_F16
         if kv.k_codes.dtype == torch.bfloat16:
             return KIVI_BF16
-        raise ValueError(f"a bits-16 cache must hold float16 or bfloat16 keys and values, got {kv.k_codes.dtype}")
+        if kv.k_codes.dtype == torch.float32:
+            return KIVI_F32
+        raise ValueError(f"a bits-16 cache must hold float16, bfloat16 or float32 keys and values, got "
+                         f"{kv.k_codes.dtype}")
     raise ValueError(f"bits must be 4, 8 or 16, got {kv.bits}")
 
 

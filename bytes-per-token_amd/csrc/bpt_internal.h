@@ -157,6 +157,8 @@ struct KiviParams {
   int grid;
   float qscale;  // sm_scale * log2(e)
   int q_dtype;
+  int D, split;       // head dim; tokens per split
+  int gshift_tokens;  // log2(tokens per key group)
 };
 
 // Launch-ready form of bpt_norm_quant_args.
@@ -177,6 +179,7 @@ constexpr int kKivi4 = 0;
 constexpr int kKivi8 = 1;
 constexpr int kKiviF16 = 2;
 constexpr int kKiviBf16 = 3;
+constexpr int kKiviF32 = 4;
 
 int decode_rows_per_load(int kv_dtype);
 int decode_chunk_tokens(int kv_dtype, int rows_per_group);
@@ -197,6 +200,8 @@ hipError_t launch_decode(const DecodeParams& p, int kv_dtype, int scale_kind, in
 hipError_t launch_decode_mfma(const DecodeParams& p, int kv_dtype, int scale_kind, hipStream_t stream,
                               const LaunchEvents& ev = {});
 hipError_t launch_kivi(const KiviParams& p, int fmt, hipStream_t stream);
+// Any even head dim up to 256 and float32 bits-16 caches: one workgroup per (sequence, KV head, split).
+hipError_t launch_kivi_any(const KiviParams& p, int fmt, hipStream_t stream);
 hipError_t launch_norm_quant(const NormQuantParams& p, bool vec8, hipStream_t stream);
 hipError_t launch_append(const AppendParams& p, int kv_dtype, int scale_kind, int head_dim, hipStream_t stream);
 hipError_t launch_fp8_table(float* out, hipStream_t stream);

@@ -137,6 +137,7 @@ int make_plan(const bpt_decode_args* a, Plan* pl) {
 }
 
 struct KiviPlan {
+  bool any;  // the float32 kernel for head dims other than 128 and float32 caches (kivi_any.hip)
   int G, grid, len_cap, eb;
   size_t ws_out_floats, ws_lse_floats, workspace, counters;
 };
@@ -147,7 +148,7 @@ int make_kivi_plan(const bpt_kivi_args* a, KiviPlan* pl) {
   if (a->struct_size != sizeof(bpt_kivi_args))
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: struct_size %u != %zu (stale binding)", fn, a->struct_size,
                 sizeof(bpt_kivi_args));
-  if (a->format < BPT_KIVI_INT4 || a->format > BPT_KIVI_BF16)
+  if (a->format < BPT_KIVI_INT4 || a->format > BPT_KIVI_F32)
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: unknown format %d", fn, a->format);
   if (a->q_dtype < BPT_F_BF16 || a->q_dtype > BPT_F_F32)
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: q_dtype must be bf16, f16 or f32", fn);
@@ -161,23 +162,27 @@ int make_kivi_plan(const bpt_kivi_args* a, KiviPlan* pl) {
   pl->G = a->num_q_heads / a->num_kv_heads;
   if (pl->G > 16)
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: %d query heads per KV head (at most 16)", fn, pl->G);
-  if (a->head_dim != bpt::kHeadDim)
-    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: head_dim %d not supported (128)", fn, a->head_dim);
+  if (a->head_dim < 2 || a->head_dim > 256 || a->head_dim % 2)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: head_dim %d not supported (an even number up to 256)", fn,
+                a->head_dim);
   const bool quant = a->format == BPT_KIVI_INT4 || a->format == BPT_KIVI_INT8;
+  pl->any = a->head_dim != bpt::kHeadDim || a->format == BPT_KIVI_F32;
   if (a->group < 1 || a->split < 1 || a->split % a->group)
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: split %d must be a multiple of the key group %d", fn, a->split,
                 a->group);
-  if (a->split % bpt::kMfmaChunk)
-    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: split %d must be a multiple of %d tokens", fn, a->split,
-                bpt::kMfmaChunk);
   if (a->num_splits < 1) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: num_splits must be >= 1", fn);
-  if (a->tokens % bpt::kMfmaChunk)
-    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: the cache's %d tokens must be a multiple of %d", fn, a->tokens,
-                bpt::kMfmaChunk);
+  if (!pl->any) {
+    if (a->split % bpt::kMfmaChunk)
+      return fail(BPT_ERR_INVALID_ARGUMENT, "%s: split %d must be a multiple of %d tokens", fn, a->split,
+                  bpt::kMfmaChunk);
+    if (a->tokens % bpt::kMfmaChunk)
+      return fail(BPT_ERR_INVALID_ARGUMENT, "%s: the cache's %d tokens must be a multiple of %d", fn, a->tokens,
+                  bpt::kMfmaChunk);
+  }
   if (quant) {
-    if (a->group % bpt::kMfmaChunk || !is_pow2(a->group))
-      return fail(BPT_ERR_INVALID_ARGUMENT, "%s: key group %d must be a power of two of at least %d tokens", fn,
-                  a->group, bpt::kMfmaChunk);
+    if (!is_pow2(a->group) || (!pl->any && a->group % bpt::kMfmaChunk))
+      return fail(BPT_ERR_INVALID_ARGUMENT, "%s: key group %d must be a power of two%s", fn, a->group,
+                  pl->any ? "" : " of at least 32 tokens");
     if (a->tokens % a->group)
       return fail(BPT_ERR_INVALID_ARGUMENT, "%s: %d tokens are not a whole number of groups of %d", fn, a->tokens,
                   a->group);
@@ -186,15 +191,21 @@ int make_kivi_plan(const bpt_kivi_args* a, KiviPlan* pl) {
                   a->tokens);
   }
   if (!std::isfinite(a->sm_scale)) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: sm_scale must be finite", fn);
-  pl->eb = quant ? 1 : 2;
+  pl->eb = quant ? 1 : (a->format == BPT_KIVI_F32 ? 4 : 2);
   const int64_t reach = (int64_t)a->num_splits * a->split;
   pl->len_cap = (int)(reach < a->tokens ? reach : a->tokens);
+  const int64_t segs = (int64_t)a->batch * a->num_kv_heads * a->num_splits;
+  if (segs > 0x7fffffffLL) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: batch x heads x splits too large", fn);
+  if (pl->any) {  // one workgroup per (sequence, KV head, split); no partials cross workgroups
+    pl->grid = (int)segs;
+    pl->ws_out_floats = pl->ws_lse_floats = 0;
+    pl->workspace = pl->counters = 0;
+    return BPT_OK;
+  }
   const int64_t max_nb = (pl->len_cap + bpt::kMfmaChunk - 1) / bpt::kMfmaChunk;
   const int64_t seq_chunks = (int64_t)a->batch * max_nb;
   if (seq_chunks > 0x7fffffffLL / a->num_kv_heads)
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: batch x tokens x heads too large", fn);
-  const int64_t segs = (int64_t)a->batch * a->num_kv_heads * a->num_splits;
-  if (segs > 0x7fffffffLL) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: batch x heads x splits too large", fn);
   int64_t grid = (int64_t)bpt::kComputeUnits * bpt::kDecodeGroupsPerCu;
   const int64_t bound_c = seq_chunks * a->num_kv_heads;
   if (bound_c < grid) grid = bound_c;
@@ -448,24 +459,29 @@ int bpt_kivi_decode(const bpt_kivi_args* a, void* stream) {
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: q, codes, lengths, out and lse must be non-NULL", fn);
   if (quant && (!a->k_scale || !a->k_zero || !a->v_scale || !a->v_zero))
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: 4- and 8-bit codes need their key and value grids", fn);
-  if (!aligned16(a->k_codes) || !aligned16(a->v_codes) || (a->code_stride_b * pl.eb) % 16 ||
-      (a->code_stride_h * pl.eb) % 16 || (a->code_stride_t * pl.eb) % 16)
-    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: code tensors and their strides must be 16-byte aligned", fn);
-  if (quant && (!aligned16(a->k_scale) || !aligned16(a->k_zero) || !aligned16(a->v_scale) || !aligned16(a->v_zero) ||
-                a->kgrid_stride_b % 8 || a->kgrid_stride_h % 8 || a->kgrid_stride_g % 8 || a->vgrid_stride_b % 4 ||
-                a->vgrid_stride_h % 4))
-    return fail(BPT_ERR_INVALID_ARGUMENT,
-                "%s: grids must be 16-byte aligned, key-grid strides multiples of 8 and value-grid strides of 4", fn);
-  // One (sequence, KV head)'s codes and grids are addressed with 32-bit offsets.
-  if ((int64_t)a->tokens * a->code_stride_t * pl.eb >= (int64_t)1 << 31 ||
-      (quant && (int64_t)a->num_groups * a->kgrid_stride_g >= (int64_t)1 << 30))
-    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: one KV head's codes or grids span 2 GiB or more", fn);
-  if (!a->workspace || a->workspace_bytes < pl.workspace || ((uintptr_t)a->workspace & 255u))
-    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: a 256-byte aligned workspace of %zu bytes is required (got %zu)", fn,
-                pl.workspace, a->workspace_bytes);
-  if (!a->counters || a->counters_bytes < pl.counters || ((uintptr_t)a->counters & 3u))
-    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: a zeroed counter buffer of %zu bytes is required (got %zu)", fn,
-                pl.counters, a->counters_bytes);
+  if (pl.any) {  // element-aligned tensors are enough for the float32 kernel
+    if (((uintptr_t)a->k_codes | (uintptr_t)a->v_codes) % pl.eb)
+      return fail(BPT_ERR_INVALID_ARGUMENT, "%s: code tensors must be aligned to their element size", fn);
+  } else {
+    if (!aligned16(a->k_codes) || !aligned16(a->v_codes) || (a->code_stride_b * pl.eb) % 16 ||
+        (a->code_stride_h * pl.eb) % 16 || (a->code_stride_t * pl.eb) % 16)
+      return fail(BPT_ERR_INVALID_ARGUMENT, "%s: code tensors and their strides must be 16-byte aligned", fn);
+    if (quant && (!aligned16(a->k_scale) || !aligned16(a->k_zero) || !aligned16(a->v_scale) ||
+                  !aligned16(a->v_zero) || a->kgrid_stride_b % 8 || a->kgrid_stride_h % 8 || a->kgrid_stride_g % 8 ||
+                  a->vgrid_stride_b % 4 || a->vgrid_stride_h % 4))
+      return fail(BPT_ERR_INVALID_ARGUMENT,
+                  "%s: grids must be 16-byte aligned, key-grid strides multiples of 8 and value-grid strides of 4", fn);
+    // One (sequence, KV head)'s codes and grids are addressed with 32-bit offsets.
+    if ((int64_t)a->tokens * a->code_stride_t * pl.eb >= (int64_t)1 << 31 ||
+        (quant && (int64_t)a->num_groups * a->kgrid_stride_g >= (int64_t)1 << 30))
+      return fail(BPT_ERR_INVALID_ARGUMENT, "%s: one KV head's codes or grids span 2 GiB or more", fn);
+    if (!a->workspace || a->workspace_bytes < pl.workspace || ((uintptr_t)a->workspace & 255u))
+      return fail(BPT_ERR_INVALID_ARGUMENT, "%s: a 256-byte aligned workspace of %zu bytes is required (got %zu)",
+                  fn, pl.workspace, a->workspace_bytes);
+    if (!a->counters || a->counters_bytes < pl.counters || ((uintptr_t)a->counters & 3u))
+      return fail(BPT_ERR_INVALID_ARGUMENT, "%s: a zeroed counter buffer of %zu bytes is required (got %zu)", fn,
+                  pl.counters, a->counters_bytes);
+  }
 
   bpt::KiviParams p;
   p.q = a->q;
@@ -509,7 +525,11 @@ int bpt_kivi_decode(const bpt_kivi_args* a, void* stream) {
   p.grid = pl.grid;
   p.qscale = a->sm_scale * bpt::kLog2e;
   p.q_dtype = a->q_dtype;
-  hipError_t e = bpt::launch_kivi(p, a->format, (hipStream_t)stream);
+  p.D = a->head_dim;
+  p.split = a->split;
+  p.gshift_tokens = quant ? log2i(a->group) : 0;
+  hipError_t e = pl.any ? bpt::launch_kivi_any(p, a->format, (hipStream_t)stream)
+                        : bpt::launch_kivi(p, a->format, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(fn, e);
   return BPT_OK;
 }

@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define BPT_ABI_VERSION 7
+#define BPT_ABI_VERSION 8
 
 /* return codes */
 #define BPT_OK 0
@@ -174,7 +174,8 @@ typedef enum {
   BPT_KIVI_INT4 = 0, /* uint8 [B, Hkv, T, D/2]: channel d in the low nibble, d + D/2 in the high one      */
   BPT_KIVI_INT8 = 1, /* uint8 [B, Hkv, T, D]                                                           */
   BPT_KIVI_F16 = 2,  /* bits 16: float16 keys and values [B, Hkv, T, D], no grids                      */
-  BPT_KIVI_BF16 = 3  /* bits 16: bfloat16 keys and values, no grids                                    */
+  BPT_KIVI_BF16 = 3, /* bits 16: bfloat16 keys and values, no grids                                    */
+  BPT_KIVI_F32 = 4   /* bits 16: float32 keys and values, no grids (a float32 model's cache)             */
 } bpt_kivi_format;
 
 /*
@@ -192,15 +193,17 @@ typedef enum {
  *   lse          float32 [B, Hq, S] (strides lse_stride_{b,h,s}): log sum exp (natural log) of that split's
  *                scores sm_scale * q.k, -inf for an empty split
  *
- * D = 128; Hq a multiple of Hkv with at most 16 query heads per KV head; T and split multiples of 32
- * (split also of group); for INT4 / INT8, group a power of two of at least 32, T a multiple of group and
- * num_groups * group >= T. One KV head's codes must span less than 2 GiB.
- * Every cached byte is read once for all query heads of its KV head. The tokens are shared out over the
- * launched workgroups regardless of the split; a split that several workgroups cover is combined exactly
- * in the same launch. Buffers: as for bpt_paged_decode (bpt_kivi_plan gives the sizes; counters zero
- * before the first call and left zero by every call). Code tensors and grids must be 16-byte aligned,
- * code strides multiples of 16 bytes, key-grid strides multiples of 8 elements and value-grid strides
- * multiples of 4 elements.
+ * Hq a multiple of Hkv with at most 16 query heads per KV head; split a multiple of group; for INT4 / INT8,
+ * T a multiple of group and num_groups * group >= T.
+ * Two kernels. D = 128 with INT4 / INT8 / F16 / BF16 codes takes the matrix-core kernel: T and split
+ * multiples of 32, for INT4 / INT8 group a power of two of at least 32; one KV head's codes must span less
+ * than 2 GiB; code tensors and grids 16-byte aligned, code strides multiples of 16 bytes, key-grid strides
+ * multiples of 8 elements and value-grid strides multiples of 4. Every cached byte is read once for all query
+ * heads of its KV head; the tokens are shared out over the launched workgroups regardless of the split, and
+ * a split that several workgroups cover is combined exactly in the same launch (buffers: as for
+ * bpt_paged_decode; bpt_kivi_plan gives the sizes; counters zero before the first call and left zero by every
+ * call). Any other even D up to 256, and F32 caches, take a float32 kernel with one workgroup per (sequence,
+ * KV head, split); group a power of two; it needs no workspace or counters (bpt_kivi_plan reports 0 bytes).
  */
 typedef struct {
   uint32_t struct_size; /* sizeof(bpt_kivi_args) */

@@ -21,12 +21,12 @@ pytestmark = pytest.mark.gpu
 D = 128
 
 
-def make_cache(batch, kv_heads, tokens, bits, seed=0, half=torch.float16, v_mul=1.0, group=32):
+def make_cache(batch, kv_heads, tokens, bits, seed=0, half=torch.float16, v_mul=1.0, group=32, d=D):
     """(device cache with QuantKV's fields, oracle QuantKV) holding the same codes."""
     g = np.random.default_rng(seed)
-    k = g.standard_normal((batch, kv_heads, tokens, D)).astype(np.float32)
-    k[..., 3] += 20.0  # an outlier channel, as Qwen3's keys have
-    v = (g.standard_normal((batch, kv_heads, tokens, D)) * v_mul).astype(np.float32)
+    k = g.standard_normal((batch, kv_heads, tokens, d)).astype(np.float32)
+    k[..., 3 % d] += 20.0  # an outlier channel, as Qwen3's keys have
+    v = (g.standard_normal((batch, kv_heads, tokens, d)) * v_mul).astype(np.float32)
     if bits == 16:
         kt = torch.from_numpy(k).to(half)
         vt = torch.from_numpy(v).to(half)
@@ -44,9 +44,9 @@ def make_cache(batch, kv_heads, tokens, bits, seed=0, half=torch.float16, v_mul=
     return dev, ref
 
 
-def make_q(batch, q_heads, seed, dtype=torch.bfloat16):
+def make_q(batch, q_heads, seed, dtype=torch.bfloat16, d=D):
     g = np.random.default_rng(seed)
-    q = torch.from_numpy(g.standard_normal((batch, q_heads, D)).astype(np.float32)).to(dtype)
+    q = torch.from_numpy(g.standard_normal((batch, q_heads, d)).astype(np.float32)).to(dtype)
     return q.cuda(), q.float().numpy()
 
 
@@ -172,6 +172,51 @@ def test_bad_arguments_raise_value_error():
         kivi.decode_attention(q, dev, lens, 0.1, split=48)
     with pytest.raises(ValueError, match="int32"):
         kivi.decode_attention(q, dev, lens.long(), 0.1)
-    f32 = SimpleNamespace(**{**dev.__dict__, "bits": 16, "k_codes": dev.k_codes.float(), "v_codes": dev.v_codes.float()})
-    with pytest.raises(ValueError, match="float16 or bfloat16"):
-        kivi.attend(q, f32, lens, 0.1)
+    f64 = SimpleNamespace(**{**dev.__dict__, "bits": 16, "k_codes": dev.k_codes.double(), "v_codes": dev.v_codes.double()})
+    with pytest.raises(ValueError, match="float16, bfloat16 or float32"):
+        kivi.attend(q, f64, lens, 0.1)
+    odd, _ = make_cache(1, 8, 64, 16, d=258)
+    with pytest.raises(ValueError, match="head_dim"):
+        kivi.attend(make_q(1, 16, 1, d=258)[0], odd, lens, 0.1)
+
+
+@pytest.mark.parametrize("bits", [4, 8, 16])
+@pytest.mark.parametrize("batch,q_heads,kv_heads,tokens,d", [
+    (3, 4, 2, 160, 16),  # a tiny head (fastserve tests/kernels/test_kernels_gpu.py:87-106)
+    (2, 4, 4, 64, 32),   # no GQA
+    (2, 16, 8, 96, 64),
+])
+def test_small_head_dims(batch, q_heads, kv_heads, tokens, d, bits):
+    """Head dims other than 128 take the float32 kernel; the reference tests' small shapes, two seeds, their
+    splits (one group per split ... one split per KV head)."""
+    for seed in range(2):
+        dev, ref = make_cache(batch, kv_heads, tokens, bits, seed=seed, d=d)
+        q, qn = make_q(batch, q_heads, seed + 7, d=d)
+        full = [tokens] * batch
+        check(q, qn, dev, ref, full)
+        for split in sorted({32, 64, tokens}):
+            check(q, qn, dev, ref, full, split=split)
+        check(q, qn, dev, ref, [tokens, 1, 37][:batch], split=32)  # ragged rows, one of a single token
+
+
+@pytest.mark.parametrize("d", [16, 128])
+def test_float32_caches(d):
+    """Bits-16 caches in float32 (a float32 model's QuantizedKVCache, fastserve integration/kv_cache.py:84-92)
+    take the float32 kernel, at the tiny model's head dim and at 128."""
+    for q_dtype in (torch.float32, torch.bfloat16):
+        dev, ref = make_cache(2, 2, 128, 16, seed=31, half=torch.float32, d=d)
+        q, qn = make_q(2, 4, 32, dtype=q_dtype, d=d)
+        check(q, qn, dev, ref, [128, 90])
+        check(q, qn, dev, ref, [128, 90], split=32)
+        check(q, qn, dev, ref, [96, 96], tokens=96)
+
+
+@pytest.mark.parametrize("bits", [4, 8, 16])
+def test_tiny_model_decode_steps(bits):
+    """fastserve's in-model kernel test (tests/kernels/test_kernels_gpu.py:148-167) in miniature: the tiny
+    Qwen3's cache (2 KV heads, head dim 16, float32, 2 sequences, room for 128 tokens) as its decode steps
+    see it while the stored tokens grow through whole key groups; float32 q, tokens = the stored count."""
+    dev, ref = make_cache(2, 2, 128, bits, seed=41, half=torch.float32, d=16)
+    for stored in (32, 64, 96, 128):
+        q, qn = make_q(2, 4, 42 + stored, dtype=torch.float32, d=16)
+        check(q, qn, dev, ref, [stored, stored], tokens=stored)

@@ -41,13 +41,25 @@ def test_kivi_plan_sizes(built_lib):
     assert plan(small)[0] == 0 and small.grid_groups == 8 * 2  # never more workgroups than chunks
 
 
+def test_kivi_plan_other_head_dims_and_float32_take_the_float32_kernel(built_lib):
+    """Head dims other than 128, and float32 caches, run one workgroup per (sequence, KV head, split) with no
+    workspace; the 32-token rules of the matrix-core kernel do not apply to them."""
+    for over in (dict(head_dim=16), dict(head_dim=64), dict(format=_lib.KIVI_F32)):
+        a = kivi_args(**over)
+        rc, ws, cnt = plan(a)
+        assert rc == 0 and ws == 0 and cnt == 0 and a.grid_groups == 2 * 8 * 32
+    a = kivi_args(head_dim=16, tokens=4090, format=_lib.KIVI_F32, split=10, group=2, num_splits=409)
+    assert plan(a)[0] == 0 and a.grid_groups == 2 * 8 * 409
+
+
 @pytest.mark.parametrize(
     "over,msg",
     [
         (dict(group=48, split=96), "power of two"),
         (dict(group=64, num_groups=64, split=96), "multiple of the key group"),
         (dict(group=64, split=64, num_groups=64, tokens=4064), "whole number of groups"),
-        (dict(head_dim=64), "head_dim"),
+        (dict(head_dim=258), "head_dim"),
+        (dict(head_dim=63), "head_dim"),
         (dict(num_q_heads=136), "query heads per KV head"),
         (dict(tokens=4090), "multiple of 32"),
         (dict(num_groups=100), "do not cover"),
