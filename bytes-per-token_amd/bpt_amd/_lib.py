@@ -188,6 +188,38 @@ class KiviArgs(ctypes.Structure):
     ]
 
 
+class KiviQuantArgs(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("bits", _i32),
+        ("src_dtype", _i32),
+        ("batch", _i32),
+        ("num_kv_heads", _i32),
+        ("tokens", _i32),
+        ("head_dim", _i32),
+        ("group", _i32),
+        ("k", _vp),
+        ("v", _vp),
+        ("src_stride_b", _i64),
+        ("src_stride_h", _i64),
+        ("src_stride_t", _i64),
+        ("k_codes", _vp),
+        ("v_codes", _vp),
+        ("code_stride_b", _i64),
+        ("code_stride_h", _i64),
+        ("code_stride_t", _i64),
+        ("k_scale", _vp),
+        ("k_zero", _vp),
+        ("kgrid_stride_b", _i64),
+        ("kgrid_stride_h", _i64),
+        ("kgrid_stride_g", _i64),
+        ("v_scale", _vp),
+        ("v_zero", _vp),
+        ("vgrid_stride_b", _i64),
+        ("vgrid_stride_h", _i64),
+    ]
+
+
 class NormQuantArgs(ctypes.Structure):
     _fields_ = [
         ("struct_size", ctypes.c_uint32),
@@ -221,6 +253,7 @@ SIGNATURES = {
     ),
     "bpt_kivi_decode": (_i32, [ctypes.POINTER(KiviArgs), _vp]),
     "bpt_rms_norm_int8": (_i32, [ctypes.POINTER(NormQuantArgs), _vp]),
+    "bpt_kivi_quantize": (_i32, [ctypes.POINTER(KiviQuantArgs), _vp]),
     "bpt_last_error": (ctypes.c_char_p, []),
     "bpt_abi_version": (_i32, []),
     "bpt_source_hash": (ctypes.c_char_p, []),
@@ -230,7 +263,7 @@ SIGNATURES = {
     "bpt_copy_probe": (_i32, [_vp, _vp, ctypes.c_uint64, _vp]),
 }
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 
 class BptError(RuntimeError):

@@ -9,6 +9,10 @@ Mirrors fastserve's kernels/kv_attention.py (paths relative to its src/fastserve
   integration/kv_cache.py:39 injects into QuantizedKVCache.
 * `attend(q, kv, lengths, scale, **launch)` is :248-252 (merge_partials of the above). Here it is one
   launch that writes the merged result directly (the splits of one row are combined inside the kernel).
+* `quantize_kv(k, v, bits, group=32)` is kernels/reference.py:132-160 (the write half: codes and float16
+  grids, bit-exact with its formulas), and `quantize_kv_into(k, v, kv, start)` the same written straight into
+  a cache at token `start`, which is what integration/kv_cache.py:147-156 QuantizedKVCache._append does with
+  each completed key group.
 * `kv` is anything with QuantKV's fields (kernels/reference.py:66-100): bits 4 / 8 with uint8 codes
   [B, Hkv, T, D] (bits 4: [B, Hkv, T, D/2], channel d low nibble, d + D/2 high) and float16 grids
   k_scale / k_zero [B, Hkv, T/group, D], v_scale / v_zero [B, Hkv, T]; or bits 16 with float16 / bfloat16 /
@@ -25,6 +29,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+from dataclasses import dataclass
 from typing import Any
 
 import torch
@@ -34,6 +39,110 @@ from ._lib import F_BF16, F_F16, F_F32, KIVI_BF16, KIVI_F16, KIVI_F32, KIVI_INT4
 from .paged_attention import cached_buffer
 
 _Q_CODES = {torch.bfloat16: F_BF16, torch.float16: F_F16, torch.float32: F_F32}
+
+
+@dataclass
+class QuantKV:
+    """One layer's cached keys and values for B sequences, with the fields of fastserve's QuantKV
+    (kernels/reference.py:66-100): bits 4 / 8 uint8 codes [B, Hkv, T, D] ([..., D/2] for 4 bits) with float16
+    grids k_scale / k_zero [B, Hkv, T/group, D] and v_scale / v_zero [B, Hkv, T]; bits 16 the keys and values."""
+
+    bits: int
+    group: int
+    k_codes: torch.Tensor
+    v_codes: torch.Tensor
+    k_scale: torch.Tensor | None = None
+    k_zero: torch.Tensor | None = None
+    v_scale: torch.Tensor | None = None
+    v_zero: torch.Tensor | None = None
+
+    @property
+    def tokens(self) -> int:
+        return self.k_codes.shape[2]
+
+    @property
+    def head_dim(self) -> int:
+        return self.k_codes.shape[3] * (2 if self.bits == 4 else 1)
+
+    def bytes_per_token(self) -> float:
+        """Bytes one token occupies across this layer's KV heads, grids included."""
+        ts = [self.k_codes, self.v_codes, self.k_scale, self.k_zero, self.v_scale, self.v_zero]
+        return sum(t.numel() * t.element_size() for t in ts if t is not None) / (self.k_codes.shape[0] * self.tokens)
+
+
+def quantize_kv(k: torch.Tensor, v: torch.Tensor, bits: int, group: int = 32) -> QuantKV:
+    """k, v [B, Hkv, T, D] stored in `bits` bits (kernels/reference.py:132-160); T a whole number of groups.
+
+    bits 4 / 8: one launch of the quantize-on-write kernel into freshly allocated codes and grids. bits 16:
+    the keys and values themselves (contiguous), as the reference stores them."""
+    if bits == 16:
+        return QuantKV(16, group, k.contiguous(), v.contiguous())
+    if bits not in (4, 8):
+        raise ValueError(f"bits must be 4, 8 or 16, got {bits}")
+    b, h, t, d = k.shape
+    if t % group:
+        raise ValueError(f"{t} tokens are not a whole number of groups of {group}")
+    dev = k.device
+    width = d // 2 if bits == 4 else d
+    kv = QuantKV(
+        bits, group,
+        torch.empty((b, h, t, width), dtype=torch.uint8, device=dev),
+        torch.empty((b, h, t, width), dtype=torch.uint8, device=dev),
+        torch.empty((b, h, t // group, d), dtype=torch.float16, device=dev),
+        torch.empty((b, h, t // group, d), dtype=torch.float16, device=dev),
+        torch.empty((b, h, t), dtype=torch.float16, device=dev),
+        torch.empty((b, h, t), dtype=torch.float16, device=dev),
+    )
+    quantize_kv_into(k, v, kv, 0)
+    return kv
+
+
+def quantize_kv_into(k: torch.Tensor, v: torch.Tensor, kv: Any, start: int) -> None:
+    """Quantize k, v [B, Hkv, n, D] (n a whole number of kv.group tokens) into cache `kv` (QuantKV's fields) at
+    tokens start .. start + n: the codes, key grids start/group .. and value grids, in one launch. Bits 16
+    caches get the values copied. Integration/kv_cache.py:147-156 does this with reference.quantize_kv and
+    slice assignments."""
+    b, h, n, d = k.shape
+    _require(tuple(v.shape) == (b, h, n, d) and v.dtype == k.dtype and v.stride() == k.stride(),
+             "k and v must be [B, Hkv, n, D] with one dtype and layout")
+    _require(kv.k_codes.shape[0] == b and kv.k_codes.shape[1] == h, "the cache's batch and KV heads must match")
+    _require(start >= 0 and start % kv.group == 0 and start + n <= kv.k_codes.shape[2],
+             f"tokens {start} .. {start + n} must start on a key group and fit the cache")
+    if kv.bits == 16:
+        kv.k_codes[:, :, start:start + n].copy_(k)
+        kv.v_codes[:, :, start:start + n].copy_(v)
+        return
+    _require(kv.bits in (4, 8), f"bits must be 4, 8 or 16, got {kv.bits}")
+    _require(n % kv.group == 0, f"{n} tokens are not a whole number of groups of {kv.group}")
+    _require(k.dtype in _Q_CODES and k.stride(-1) == 1, "k and v must be bf16, f16 or f32 with contiguous channels")
+    dev = k.device
+    _require(dev.type == "cuda", "quantize_kv runs on a GPU: k must be a cuda tensor")
+    kc = kv.k_codes[:, :, start:start + n]
+    vc = kv.v_codes[:, :, start:start + n]
+    g0, g1 = start // kv.group, (start + n) // kv.group
+    ks, kz = kv.k_scale[:, :, g0:g1], kv.k_zero[:, :, g0:g1]
+    vs, vz = kv.v_scale[:, :, start:start + n], kv.v_zero[:, :, start:start + n]
+    _require(kc.dtype == torch.uint8 and kc.stride() == vc.stride() and kc.stride(-1) == 1, "codes: uint8, shared layout")
+    _require(kc.shape[3] * (2 if kv.bits == 4 else 1) == d, f"codes hold {kc.shape[3]} bytes per token, k has D={d}")
+    _require(all(t.dtype == torch.float16 for t in (ks, kz, vs, vz)), "grids must be float16")
+    _require(ks.stride() == kz.stride() and ks.stride(-1) == 1, "key grids: shared layout, contiguous channels")
+    _require(vs.stride() == vz.stride() and vs.stride(-1) == 1, "value grids: shared layout, unit token stride")
+    for t in (v, kc, vc, ks, kz, vs, vz):
+        _require(t.device == dev, f"every tensor must be on {dev}")
+    a = _lib.KiviQuantArgs()
+    a.struct_size = ctypes.sizeof(_lib.KiviQuantArgs)
+    a.bits, a.src_dtype = kv.bits, _Q_CODES[k.dtype]
+    a.batch, a.num_kv_heads, a.tokens, a.head_dim, a.group = b, h, n, d, kv.group
+    a.k, a.v = k.data_ptr(), v.data_ptr()
+    a.src_stride_b, a.src_stride_h, a.src_stride_t = k.stride(0), k.stride(1), k.stride(2)
+    a.k_codes, a.v_codes = kc.data_ptr(), vc.data_ptr()
+    a.code_stride_b, a.code_stride_h, a.code_stride_t = kc.stride(0), kc.stride(1), kc.stride(2)
+    a.k_scale, a.k_zero = ks.data_ptr(), kz.data_ptr()
+    a.kgrid_stride_b, a.kgrid_stride_h, a.kgrid_stride_g = ks.stride(0), ks.stride(1), ks.stride(2)
+    a.v_scale, a.v_zero = vs.data_ptr(), vz.data_ptr()
+    a.vgrid_stride_b, a.vgrid_stride_h = vs.stride(0), vs.stride(1)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    _lib.check(_lib.lib().bpt_kivi_quantize(ctypes.byref(a), ctypes.c_void_p(stream)))
 
 
 def default_split(batch: int, kv_heads: int, tokens: int, group: int = 32, max_programs: int = 16384) -> int:

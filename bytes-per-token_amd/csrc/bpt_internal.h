@@ -161,6 +161,24 @@ struct KiviParams {
   int gshift_tokens;  // log2(tokens per key group)
 };
 
+// Launch-ready form of bpt_kivi_quant_args: KIVI quantize-on-write of keys and values [B, Hkv, T, D].
+struct KiviQuantParams {
+  const void* k;
+  const void* v;
+  int64_t x_sb, x_sh, x_st;  // elements (channel stride 1)
+  int src_dtype;
+  uint8_t* kc;
+  uint8_t* vc;
+  int64_t c_sb, c_sh, c_st;  // bytes
+  uint16_t* ks;              // float16 key grid [B, Hkv, T / group, D]
+  uint16_t* kz;
+  int64_t g_sb, g_sh, g_sg;  // elements
+  uint16_t* vs;              // float16 value grid [B, Hkv, T]
+  uint16_t* vz;
+  int64_t t_sb, t_sh;  // elements (token stride 1)
+  int B, Hkv, T, D, group, bits;
+};
+
 // Launch-ready form of bpt_norm_quant_args.
 struct NormQuantParams {
   const void* x;
@@ -203,6 +221,7 @@ hipError_t launch_kivi(const KiviParams& p, int fmt, hipStream_t stream);
 // Any even head dim up to 256 and float32 bits-16 caches: one workgroup per (sequence, KV head, split).
 hipError_t launch_kivi_any(const KiviParams& p, int fmt, hipStream_t stream);
 hipError_t launch_norm_quant(const NormQuantParams& p, bool vec8, hipStream_t stream);
+hipError_t launch_kivi_quantize(const KiviQuantParams& p, hipStream_t stream);
 hipError_t launch_append(const AppendParams& p, int kv_dtype, int scale_kind, int head_dim, hipStream_t stream);
 hipError_t launch_fp8_table(float* out, hipStream_t stream);
 hipError_t launch_fp8_encode(const float* x, float scale, uint8_t* out, int64_t n, hipStream_t stream);

@@ -534,6 +534,59 @@ int bpt_kivi_decode(const bpt_kivi_args* a, void* stream) {
   return BPT_OK;
 }
 
+int bpt_kivi_quantize(const bpt_kivi_quant_args* a, void* stream) {
+  const char* fn = "bpt_kivi_quantize";
+  if (!a) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: args is NULL", fn);
+  if (a->struct_size != sizeof(bpt_kivi_quant_args))
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: struct_size %u != %zu (stale binding)", fn, a->struct_size,
+                sizeof(bpt_kivi_quant_args));
+  if (a->bits != 4 && a->bits != 8) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: bits must be 4 or 8, got %d", fn, a->bits);
+  if (a->src_dtype < BPT_F_BF16 || a->src_dtype > BPT_F_F32)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: keys and values must be bf16, f16 or f32", fn);
+  if (a->batch < 0 || a->num_kv_heads < 1 || a->tokens < 0 || a->group < 1)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: batch, tokens >= 0; num_kv_heads, group >= 1", fn);
+  if (!is_pow2(a->head_dim) || a->head_dim < 2 || a->head_dim > 256)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: head_dim %d must be a power of two up to 256", fn, a->head_dim);
+  if (a->tokens % a->group)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: %d tokens are not a whole number of groups of %d", fn, a->tokens,
+                a->group);
+  if ((int64_t)a->batch * a->num_kv_heads * (a->tokens / a->group) >= (int64_t)1 << 31)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: too many key groups", fn);
+  if ((int64_t)a->batch * a->num_kv_heads * a->tokens == 0) return BPT_OK;
+  if (!a->k || !a->v || !a->k_codes || !a->v_codes || !a->k_scale || !a->k_zero || !a->v_scale || !a->v_zero)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: inputs, codes and grids must be non-NULL", fn);
+  bpt::KiviQuantParams p;
+  p.k = a->k;
+  p.v = a->v;
+  p.x_sb = a->src_stride_b;
+  p.x_sh = a->src_stride_h;
+  p.x_st = a->src_stride_t;
+  p.src_dtype = a->src_dtype;
+  p.kc = (uint8_t*)a->k_codes;
+  p.vc = (uint8_t*)a->v_codes;
+  p.c_sb = a->code_stride_b;
+  p.c_sh = a->code_stride_h;
+  p.c_st = a->code_stride_t;
+  p.ks = (uint16_t*)a->k_scale;
+  p.kz = (uint16_t*)a->k_zero;
+  p.g_sb = a->kgrid_stride_b;
+  p.g_sh = a->kgrid_stride_h;
+  p.g_sg = a->kgrid_stride_g;
+  p.vs = (uint16_t*)a->v_scale;
+  p.vz = (uint16_t*)a->v_zero;
+  p.t_sb = a->vgrid_stride_b;
+  p.t_sh = a->vgrid_stride_h;
+  p.B = a->batch;
+  p.Hkv = a->num_kv_heads;
+  p.T = a->tokens;
+  p.D = a->head_dim;
+  p.group = a->group;
+  p.bits = a->bits;
+  hipError_t e = bpt::launch_kivi_quantize(p, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(fn, e);
+  return BPT_OK;
+}
+
 int bpt_rms_norm_int8(const bpt_norm_quant_args* a, void* stream) {
   const char* fn = "bpt_rms_norm_int8";
   if (!a) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: args is NULL", fn);

@@ -23,6 +23,8 @@
  *                        with float16 grids, or float16 / bfloat16 keys and values): one partial
  *                        (out, lse) per split, as that launcher returns them.
  *   bpt_kivi_plan        the workspace / counter sizing for bpt_kivi_decode (host only).
+ *   bpt_kivi_quantize    kernels/reference.py:103-160 quantize_kv (KIVI codes and float16 grids), where
+ *                        integration/kv_cache.py:139-158 QuantizedKVCache._append quantizes completed groups.
  *   bpt_rms_norm_int8    kernels/norm_quant.py:43-109 rms_norm_int8 (kernel 1), defined by
  *                        kernels/reference.py:44-55: RMSNorm fused with per-token INT8 quantization.
  */
@@ -36,7 +38,7 @@
 extern "C" {
 #endif
 
-#define BPT_ABI_VERSION 8
+#define BPT_ABI_VERSION 9
 
 /* return codes */
 #define BPT_OK 0
@@ -241,6 +243,38 @@ typedef struct {
 } bpt_kivi_args;
 
 /*
+ * KIVI quantize-on-write (kernels/reference.py:103-160 quantize_kv): keys and values [B, Hkv, T, D] stored as
+ * asymmetric `bits`-bit codes with float16 grids, one grid per key channel per `group` tokens and one per value
+ * token: lo = min(min x, 0), hi = max(max x, 0), scale = f16((hi - lo) / (2^bits - 1)) (1 where not > 0),
+ * zero = clamp(round_half_even(-lo / scale), 0, 2^bits - 1), code = clamp(round_half_even(x / scale) + zero,
+ * 0, 2^bits - 1), float32 IEEE divisions: bit-exact with the reference formulas. 4-bit codes pair channel d
+ * (low nibble) with d + D/2 (high nibble).
+ *   k, v          [B, Hkv, T, D] BF16 / F16 / F32 (strides src_stride_{b,h,t} in elements, channel stride 1)
+ *   k/v_codes     uint8 [B, Hkv, T, D] (bits 8) or [B, Hkv, T, D/2] (bits 4), strides code_stride_{b,h,t} bytes
+ *   k_scale/zero  float16 [B, Hkv, T/group, D], strides kgrid_stride_{b,h,g} (channel stride 1)
+ *   v_scale/zero  float16 [B, Hkv, T], strides vgrid_stride_{b,h} (token stride 1)
+ * bits 4 or 8; D a power of two up to 256; T a whole number of groups (the outputs may be views into a larger
+ * cache at any token offset that is a multiple of group).
+ */
+typedef struct {
+  uint32_t struct_size; /* sizeof(bpt_kivi_quant_args) */
+  int32_t bits, src_dtype;
+  int32_t batch, num_kv_heads, tokens, head_dim, group;
+  const void* k;
+  const void* v;
+  int64_t src_stride_b, src_stride_h, src_stride_t;
+  void* k_codes;
+  void* v_codes;
+  int64_t code_stride_b, code_stride_h, code_stride_t;
+  void* k_scale; /* float16 */
+  void* k_zero;
+  int64_t kgrid_stride_b, kgrid_stride_h, kgrid_stride_g;
+  void* v_scale; /* float16 */
+  void* v_zero;
+  int64_t vgrid_stride_b, vgrid_stride_h;
+} bpt_kivi_quant_args;
+
+/*
  * RMSNorm + per-token symmetric INT8, one pass over each row, float32 arithmetic:
  *   y = x * rsqrt(mean(x^2) + eps) * weight;  scale = max(max|y| / 127, 1e-12);
  *   codes = clamp(round_half_even(y / scale), -128, 127)
@@ -287,6 +321,10 @@ int bpt_kivi_plan(bpt_kivi_args* args, size_t* workspace_bytes, size_t* counters
 
 /* Decode attention over a KIVI cache: one launch, every split's (out, lse) written. */
 int bpt_kivi_decode(const bpt_kivi_args* args, void* stream);
+
+/* KIVI quantize-on-write of completed key groups (one launch): replaces kernels/reference.py:132-160
+ * quantize_kv where integration/kv_cache.py:147 QuantizedKVCache._append calls it. */
+int bpt_kivi_quantize(const bpt_kivi_quant_args* args, void* stream);
 
 /* RMSNorm fused with per-token INT8 quantization (one launch). */
 int bpt_rms_norm_int8(const bpt_norm_quant_args* args, void* stream);
