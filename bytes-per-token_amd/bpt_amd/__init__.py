@@ -12,7 +12,14 @@ from . import kivi
 from .cascade import cascade_decode_attention
 from .kv_cache import OutOfBlocksError, PagedMeta, PagedQuantKVCache
 from .norm_quant import rms_norm_int8
-from .paged_attention import decode_kernel_name, decode_plan, kv_read_bytes, paged_decode_attention, quantize_append
+from .paged_attention import (
+    decode_kernel_name,
+    decode_plan,
+    kv_read_bytes,
+    paged_decode_attention,
+    paged_prepare,
+    quantize_append,
+)
 
 __all__ = [
     "cascade_decode_attention",
@@ -24,6 +31,7 @@ __all__ = [
     "kivi",
     "kv_read_bytes",
     "paged_decode_attention",
+    "paged_prepare",
     "quantize_append",
     "rms_norm_int8",
 ]

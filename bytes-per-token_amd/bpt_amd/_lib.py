@@ -188,6 +188,30 @@ class KiviArgs(ctypes.Structure):
     ]
 
 
+class PrepareArgs(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("batch", _i32),
+        ("num_queries", _i32),
+        ("n_blocks", _i32),
+        ("num_slots", _i32),
+        ("max_blocks", _i32),
+        ("page_size", _i32),
+        ("positions_dtype", _i32),
+        ("table", _vp),
+        ("table_stride", _i64),
+        ("reserved", _vp),
+        ("slots", _vp),
+        ("positions", _vp),
+        ("pos_stride_b", _i64),
+        ("pos_stride_q", _i64),
+        ("block_table", _vp),
+        ("write_blocks", _vp),
+        ("write_offsets", _vp),
+        ("context_lens", _vp),
+    ]
+
+
 class KiviQuantArgs(ctypes.Structure):
     _fields_ = [
         ("struct_size", ctypes.c_uint32),
@@ -254,6 +278,7 @@ SIGNATURES = {
     "bpt_kivi_decode": (_i32, [ctypes.POINTER(KiviArgs), _vp]),
     "bpt_rms_norm_int8": (_i32, [ctypes.POINTER(NormQuantArgs), _vp]),
     "bpt_kivi_quantize": (_i32, [ctypes.POINTER(KiviQuantArgs), _vp]),
+    "bpt_paged_prepare": (_i32, [ctypes.POINTER(PrepareArgs), _vp]),
     "bpt_last_error": (ctypes.c_char_p, []),
     "bpt_abi_version": (_i32, []),
     "bpt_source_hash": (ctypes.c_char_p, []),
@@ -263,7 +288,7 @@ SIGNATURES = {
     "bpt_copy_probe": (_i32, [_vp, _vp, ctypes.c_uint64, _vp]),
 }
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 
 class BptError(RuntimeError):

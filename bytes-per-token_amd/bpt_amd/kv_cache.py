@@ -6,7 +6,12 @@ The drop-in for fastserve's engine (paths relative to its src/fastserve/):
   a block table per sequence, `reserve` / `can_reserve` / `free`, block 0 handed out first, freed blocks
   reused, `OutOfBlocksError` when the pool is empty.
 * `prepare(rows, positions)` builds the per-forward metadata once for all layers (engine/kv_cache.py:140-156:
-  write blocks and offsets by position, block tables padded with block 0) plus each row's context length.
+  write blocks and offsets by position, block tables padded with block 0) plus each row's context length, on
+  the device: every sequence's block table lives in a row ("slot") of a device table written by `reserve`, and
+  one kernel (bpt_paged_prepare) gathers the rows' tables and derives the write slots and lengths from the
+  positions. With device positions nothing is read back to the host, so a whole decode step (prepare plus every
+  layer's attend) can be captured in a HIP graph; host positions are checked on the host first, as fastserve's
+  prepare does.
 * `attend(layer, q, k, v, meta, scale)` is the cache-owned attention hook the model calls when a cache has
   one (engine/model.py:72-74, contract of integration/kv_cache.py:160-168): the step's keys and values are
   quantized into their slots first (store before attend), then one fused paged decode attention reads the
@@ -27,7 +32,7 @@ from typing import Any
 
 import torch
 
-from .paged_attention import paged_decode_attention, quantize_append
+from .paged_attention import paged_decode_attention, paged_prepare, quantize_append
 
 _FORMATS = {torch.float8_e4m3fn: "fp8", torch.int8: "int8", torch.bfloat16: "bf16"}
 HEAD_DIM = 128  # the one head size the paged decode kernels are built for
@@ -39,11 +44,11 @@ class OutOfBlocksError(RuntimeError):
 
 @dataclass(frozen=True)
 class PagedMeta:
-    write_blocks: torch.Tensor  # [batch, q_len] int32: physical block receiving each new token
+    write_blocks: torch.Tensor  # [batch, q_len] int32: physical block receiving each new token (-1: none)
     write_offsets: torch.Tensor  # [batch, q_len] int32: slot inside that block
     block_table: torch.Tensor  # [batch, n_blocks] int32: physical blocks of logical blocks 0 .. n_blocks - 1
     context_lens: torch.Tensor  # [batch] int32: tokens in the cache once this step is written
-    kv_len: int  # the longest row's context length
+    kv_len: int  # a bound on the longest row's context length, known on the host (its reserved tokens)
 
 
 class PagedQuantKVCache:
@@ -66,6 +71,8 @@ class PagedQuantKVCache:
         head_dim: int | None = None,
         k_scale: torch.Tensor | None = None,
         v_scale: torch.Tensor | None = None,
+        max_seqs: int = 256,
+        max_blocks_per_seq: int | None = None,
     ):
         if kv_dtype not in _FORMATS:
             raise ValueError(f"kv_dtype must be float8_e4m3fn, int8 or bfloat16, got {kv_dtype}")
@@ -107,6 +114,15 @@ class PagedQuantKVCache:
             self.k_scale = self.v_scale = [None] * self.num_layers
         self.free_blocks = list(range(num_blocks - 1, -1, -1))  # a stack: pop() hands out block 0 first
         self.tables: dict[Any, list[int]] = {}  # sequence id -> its block table
+        # The same tables on the device: one row ("slot") per live sequence, and its reserved block count.
+        self.max_seqs = max_seqs
+        self.max_blocks_per_seq = min(num_blocks, 4096) if max_blocks_per_seq is None else max_blocks_per_seq
+        self.table_dev = torch.zeros((max_seqs, self.max_blocks_per_seq), dtype=torch.int32, device=self.device)
+        self.reserved_dev = torch.zeros(max_seqs, dtype=torch.int32, device=self.device)
+        self.slot_of: dict[Any, int] = {}
+        self.free_slots = list(range(max_seqs - 1, -1, -1))
+        self._rows_key: tuple | None = None  # the rows of the last prepare and their device slots
+        self._rows_slots: torch.Tensor | None = None
 
     # -- memory management (host side) -----------------------------------------------------------------------
 
@@ -118,16 +134,32 @@ class PagedQuantKVCache:
         return self.blocks_needed(num_tokens) - have <= len(self.free_blocks)
 
     def reserve(self, seq_id: Any, num_tokens: int) -> None:
-        """Make sure `seq_id` owns enough blocks to hold positions [0, num_tokens)."""
-        table = self.tables.setdefault(seq_id, [])
-        missing = self.blocks_needed(num_tokens) - len(table)
+        """Make sure `seq_id` owns enough blocks to hold positions [0, num_tokens). New blocks are also written to
+        the sequence's row of the device table (call it outside graph capture: it copies from the host)."""
+        table = self.tables.get(seq_id)
+        missing = self.blocks_needed(num_tokens) - (len(table) if table is not None else 0)
         if missing > len(self.free_blocks):
             raise OutOfBlocksError(f"need {missing} blocks, {len(self.free_blocks)} free")
+        if table is None:
+            if not self.free_slots:
+                raise OutOfBlocksError(f"all {self.max_seqs} sequence slots are in use")
+            self.slot_of[seq_id] = self.free_slots.pop()
+            table = self.tables[seq_id] = []
+        if len(table) + max(missing, 0) > self.max_blocks_per_seq:
+            raise ValueError(f"sequence {seq_id!r} would need more than {self.max_blocks_per_seq} blocks")
+        start = len(table)
         table.extend(self.free_blocks.pop() for _ in range(missing))
+        if missing > 0:
+            slot = self.slot_of[seq_id]
+            self.table_dev[slot, start : len(table)] = torch.tensor(table[start:], dtype=torch.int32)
+        self.reserved_dev[self.slot_of[seq_id]] = len(table)
 
     def free(self, seq_id: Any) -> None:
-        """Return a finished sequence's blocks to the pool."""
+        """Return a finished sequence's blocks (and its slot) to the pool."""
         self.free_blocks.extend(reversed(self.tables.pop(seq_id, [])))
+        slot = self.slot_of.pop(seq_id, None)
+        if slot is not None:
+            self.free_slots.append(slot)
 
     def bytes_per_token(self) -> int:
         """Bytes one token occupies across all layers and KV heads (codes, plus INT8's per-token scales)."""
@@ -138,32 +170,56 @@ class PagedQuantKVCache:
     # -- the per-forward metadata and the attention hook ------------------------------------------------------
 
     def prepare(self, rows: list[Any], positions: torch.Tensor) -> PagedMeta:
-        """Metadata for one forward pass. positions: [batch, q_len], consecutive within each row."""
-        pos = positions.detach().to("cpu", torch.int64)
-        if pos.dim() != 2 or pos.shape[0] != len(rows):
-            raise ValueError(f"positions must be [{len(rows)}, q_len], got {tuple(pos.shape)}")
-        if pos.shape[1] > 1 and not bool((pos[:, 1:] - pos[:, :-1] == 1).all()):
-            raise ValueError("the positions of a row must be consecutive (one new token after another)")
-        if bool((pos < 0).any()):
-            raise ValueError("positions must be non-negative")
-        kv_len = int(pos.max()) + 1
-        n_blocks = self.blocks_needed(kv_len)
-        tables = []
-        for i, seq_id in enumerate(rows):
-            table = self.tables.get(seq_id, [])
-            if len(table) * self.block_size < int(pos[i].max()) + 1:
-                raise ValueError(f"sequence {seq_id!r} has too few blocks: call reserve() first")
-            tables.append(table[:n_blocks] + [0] * (n_blocks - len(table)))  # pad; padded slots are never read
-        block_table = torch.tensor(tables, dtype=torch.int64)
-        write_blocks = torch.gather(block_table, 1, pos // self.block_size)
+        """Metadata for one forward pass. positions: [batch, q_len], consecutive within each row.
+
+        Host positions are checked on the host first, as engine/kv_cache.py:140-146 does (consecutive,
+        non-negative, reserved), and give the reference's exact kv_len and table width. Device positions are
+        never read back: kv_len is then the rows' reserved tokens (a bound the launch is sized by), a position
+        outside its row's reserved blocks gets no write slot and lengths are clamped to the reserved tokens.
+        On a GPU cache the tables come from one kernel (bpt_paged_prepare); a CPU cache (allocator tests) builds
+        the same tables with torch index operations."""
+        if positions.dim() != 2 or positions.shape[0] != len(rows):
+            raise ValueError(f"positions must be [{len(rows)}, q_len], got {tuple(positions.shape)}")
+        missing = [s for s in rows if s not in self.tables]
+        if missing:
+            raise ValueError(f"sequence {missing[0]!r} has too few blocks: call reserve() first")
+        if positions.device.type == "cpu":
+            pos = positions.to(torch.int64)
+            if pos.shape[1] > 1 and not bool((pos[:, 1:] - pos[:, :-1] == 1).all()):
+                raise ValueError("the positions of a row must be consecutive (one new token after another)")
+            if bool((pos < 0).any()):
+                raise ValueError("positions must be non-negative")
+            for i, seq_id in enumerate(rows):
+                if len(self.tables[seq_id]) * self.block_size < int(pos[i].max()) + 1:
+                    raise ValueError(f"sequence {seq_id!r} has too few blocks: call reserve() first")
+            kv_len = int(pos.max()) + 1 if pos.numel() else 0
+            n_blocks = self.blocks_needed(kv_len)
+        elif self.device.type == "cpu":
+            raise ValueError("a CPU cache takes host positions")
+        else:
+            pos = positions
+            n_blocks = max((len(self.tables[s]) for s in rows), default=0)  # the reserved blocks: a host bound
+            kv_len = n_blocks * self.block_size
+        b, nq = pos.shape
+        if self.device.type == "cpu":
+            tables = [self.tables[s][:n_blocks] + [0] * (n_blocks - len(self.tables[s][:n_blocks])) for s in rows]
+            block_table = torch.tensor(tables, dtype=torch.int32).reshape(b, n_blocks)
+            write_blocks = torch.gather(block_table.long(), 1, pos // self.block_size).to(torch.int32)
+            return PagedMeta(write_blocks=write_blocks, write_offsets=(pos % self.block_size).to(torch.int32),
+                             block_table=block_table, context_lens=(pos[:, -1] + 1).to(torch.int32), kv_len=kv_len)
+        key = tuple(rows)
+        if key != self._rows_key:  # rows change between steps only when the batch does
+            self._rows_slots = torch.tensor([self.slot_of[s] for s in rows], dtype=torch.int32, device=self.device)
+            self._rows_key = key
         dev = self.device
-        return PagedMeta(
-            write_blocks=write_blocks.to(dev, torch.int32),
-            write_offsets=(pos % self.block_size).to(dev, torch.int32),
-            block_table=block_table.to(dev, torch.int32),
-            context_lens=(pos[:, -1] + 1).to(dev, torch.int32),
-            kv_len=kv_len,
-        )
+        block_table = torch.empty((b, max(n_blocks, 1)), dtype=torch.int32, device=dev)
+        write_blocks = torch.empty((b, nq), dtype=torch.int32, device=dev)
+        write_offsets = torch.empty((b, nq), dtype=torch.int32, device=dev)
+        context_lens = torch.empty(b, dtype=torch.int32, device=dev)
+        paged_prepare(self.table_dev, self.reserved_dev, self._rows_slots, pos.to(dev), self.block_size, block_table,
+                      write_blocks, write_offsets, context_lens)
+        return PagedMeta(write_blocks=write_blocks, write_offsets=write_offsets, block_table=block_table,
+                         context_lens=context_lens, kv_len=kv_len)
 
     def update(self, layer: int, k: torch.Tensor, v: torch.Tensor, meta: PagedMeta):
         raise NotImplementedError("a quantized cache never returns float keys and values: use attend()")

@@ -328,6 +328,48 @@ def quantize_append(
     _lib.check(_lib.lib().bpt_quant_append(ctypes.byref(a), ctypes.c_void_p(_stream(dev))))
 
 
+def paged_prepare(
+    table: torch.Tensor,
+    reserved: torch.Tensor,
+    slots: torch.Tensor,
+    positions: torch.Tensor,
+    page_size: int,
+    block_table: torch.Tensor,
+    write_blocks: torch.Tensor,
+    write_offsets: torch.Tensor,
+    context_lens: torch.Tensor,
+) -> None:
+    """Per-forward paged metadata on the device (bpt_paged_prepare; engine/kv_cache.py:140-156 without the host
+    round trip): from each row's slot of the device table [num_slots, max_blocks] (reserved[slot] blocks held)
+    and the positions [B, Q], fill block_table [B, n_blocks] (padded with block 0), write_blocks / write_offsets
+    [B, Q] (-1 outside the reserved blocks) and context_lens [B]. One launch, no host read."""
+    _require(table.dtype == torch.int32 and table.dim() == 2 and table.stride(1) == 1, "table: int32 [slots, blocks]")
+    _require(reserved.dtype == torch.int32 and reserved.is_contiguous() and reserved.numel() == table.shape[0],
+             "reserved: int32 [slots]")
+    _require(positions.dim() == 2 and positions.dtype in _INDEX_CODES, "positions: int32 / int64 [B, Q]")
+    b, nq = positions.shape
+    _require(slots.dtype == torch.int32 and slots.is_contiguous() and slots.numel() == b, f"slots: int32 [{b}]")
+    for name, t, shape in (("block_table", block_table, None), ("write_blocks", write_blocks, (b, nq)),
+                           ("write_offsets", write_offsets, (b, nq)), ("context_lens", context_lens, (b,))):
+        _require(t.dtype == torch.int32 and t.is_contiguous() and (shape is None or tuple(t.shape) == shape),
+                 f"{name}: contiguous int32")
+    _require(block_table.dim() == 2 and block_table.shape[0] == b, f"block_table: [{b}, n_blocks]")
+    dev = positions.device
+    for name, t in (("table", table), ("reserved", reserved), ("slots", slots), ("block_table", block_table)):
+        _require(t.device == dev, f"{name} is not on {dev}")
+    a = _lib.PrepareArgs()
+    a.struct_size = ctypes.sizeof(_lib.PrepareArgs)
+    a.batch, a.num_queries, a.n_blocks = b, nq, block_table.shape[1]
+    a.num_slots, a.max_blocks, a.page_size = table.shape[0], table.shape[1], page_size
+    a.positions_dtype = _INDEX_CODES[positions.dtype]
+    a.table, a.table_stride = table.data_ptr(), table.stride(0)
+    a.reserved, a.slots = reserved.data_ptr(), slots.data_ptr()
+    a.positions, a.pos_stride_b, a.pos_stride_q = positions.data_ptr(), positions.stride(0), positions.stride(1)
+    a.block_table, a.write_blocks = block_table.data_ptr(), write_blocks.data_ptr()
+    a.write_offsets, a.context_lens = write_offsets.data_ptr(), context_lens.data_ptr()
+    _lib.check(_lib.lib().bpt_paged_prepare(ctypes.byref(a), ctypes.c_void_p(_stream(dev))))
+
+
 def kv_read_bytes(context_lens_host, num_kv_heads: int, head_dim: int, kv_dtype: torch.dtype, per_token_scales: bool,
                   num_queries: int = 1) -> int:
     """Algorithmic KV bytes one call must read: codes for K and V, plus scales (q, out, tables excluded)."""

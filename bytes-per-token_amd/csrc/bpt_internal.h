@@ -179,6 +179,22 @@ struct KiviQuantParams {
   int B, Hkv, T, D, group, bits;
 };
 
+// Launch-ready form of bpt_prepare_args: per-forward paged metadata from device positions.
+struct PrepareParams {
+  const int32_t* table;     // [num_slots, table_stride] block ids of each slot's sequence
+  int64_t table_stride;
+  const int32_t* reserved;  // [num_slots] blocks reserved per slot
+  const int32_t* slots;     // [B] each row's slot
+  const void* positions;    // [B, Q] int32 / int64
+  int64_t pos_sb, pos_sq;
+  int pos_i64;
+  int32_t* block_table;     // [B, n_blocks]
+  int32_t* write_blocks;    // [B, Q]
+  int32_t* write_offsets;   // [B, Q]
+  int32_t* context_lens;    // [B]
+  int B, Q, n_blocks, num_slots, max_blocks, P, logP;
+};
+
 // Launch-ready form of bpt_norm_quant_args.
 struct NormQuantParams {
   const void* x;
@@ -222,6 +238,7 @@ hipError_t launch_kivi(const KiviParams& p, int fmt, hipStream_t stream);
 hipError_t launch_kivi_any(const KiviParams& p, int fmt, hipStream_t stream);
 hipError_t launch_norm_quant(const NormQuantParams& p, bool vec8, hipStream_t stream);
 hipError_t launch_kivi_quantize(const KiviQuantParams& p, hipStream_t stream);
+hipError_t launch_paged_prepare(const PrepareParams& p, hipStream_t stream);
 hipError_t launch_append(const AppendParams& p, int kv_dtype, int scale_kind, int head_dim, hipStream_t stream);
 hipError_t launch_fp8_table(float* out, hipStream_t stream);
 hipError_t launch_fp8_encode(const float* x, float scale, uint8_t* out, int64_t n, hipStream_t stream);

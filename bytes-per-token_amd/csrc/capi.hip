@@ -534,6 +534,47 @@ int bpt_kivi_decode(const bpt_kivi_args* a, void* stream) {
   return BPT_OK;
 }
 
+int bpt_paged_prepare(const bpt_prepare_args* a, void* stream) {
+  const char* fn = "bpt_paged_prepare";
+  if (!a) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: args is NULL", fn);
+  if (a->struct_size != sizeof(bpt_prepare_args))
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: struct_size %u != %zu (stale binding)", fn, a->struct_size,
+                sizeof(bpt_prepare_args));
+  if (a->batch < 0 || a->num_queries < 1 || a->n_blocks < 0 || a->num_slots < 1 || a->max_blocks < 0 ||
+      a->table_stride < a->max_blocks)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: bad sizes (table_stride must cover max_blocks)", fn);
+  if (!is_pow2(a->page_size)) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: page_size must be a power of two", fn);
+  if (a->positions_dtype != BPT_IDX_I32 && a->positions_dtype != BPT_IDX_I64)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: positions must be int32 or int64", fn);
+  if (a->batch == 0) return BPT_OK;
+  if (!a->table || !a->reserved || !a->slots || !a->positions || !a->write_blocks || !a->write_offsets ||
+      !a->context_lens || (a->n_blocks > 0 && !a->block_table))
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: tables, slots, positions and outputs must be non-NULL", fn);
+  bpt::PrepareParams p;
+  p.table = a->table;
+  p.table_stride = a->table_stride;
+  p.reserved = a->reserved;
+  p.slots = a->slots;
+  p.positions = a->positions;
+  p.pos_sb = a->pos_stride_b;
+  p.pos_sq = a->pos_stride_q;
+  p.pos_i64 = a->positions_dtype == BPT_IDX_I64;
+  p.block_table = a->block_table;
+  p.write_blocks = a->write_blocks;
+  p.write_offsets = a->write_offsets;
+  p.context_lens = a->context_lens;
+  p.B = a->batch;
+  p.Q = a->num_queries;
+  p.n_blocks = a->n_blocks;
+  p.num_slots = a->num_slots;
+  p.max_blocks = a->max_blocks;
+  p.P = a->page_size;
+  p.logP = log2i(a->page_size);
+  hipError_t e = bpt::launch_paged_prepare(p, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(fn, e);
+  return BPT_OK;
+}
+
 int bpt_kivi_quantize(const bpt_kivi_quant_args* a, void* stream) {
   const char* fn = "bpt_kivi_quantize";
   if (!a) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: args is NULL", fn);

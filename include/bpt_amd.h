@@ -16,6 +16,8 @@
  *   bpt_quant_append     engine/kv_cache.py:158-161 PagedKVCache.update (scatter write by write_blocks /
  *                        write_offsets) fused with the quantizers kv/quant.py:44-45 (FP8 cast) and
  *                        quant/w8a8.py:55-74 / kernels/reference.py:44-55 (per-token INT8, amax/127).
+ *   bpt_paged_prepare    engine/kv_cache.py:140-156 PagedKVCache.prepare (the per-forward PagedMeta), built on
+ *                        the device from device positions.
  *   bpt_decode_plan      kernels/kv_attention.py:178-187 default_split (tokens per program) and the
  *                        out/lse allocation of :218-220, as a host-only planning call.
  *   bpt_kivi_decode      kernels/kv_attention.py:190-245 decode_attention (launcher) and :56-175 (the
@@ -38,7 +40,7 @@
 extern "C" {
 #endif
 
-#define BPT_ABI_VERSION 9
+#define BPT_ABI_VERSION 10
 
 /* return codes */
 #define BPT_OK 0
@@ -243,6 +245,36 @@ typedef struct {
 } bpt_kivi_args;
 
 /*
+ * Per-forward paged metadata from device positions (engine/kv_cache.py:140-156 PagedKVCache.prepare, built on
+ * the device). The cache keeps each live sequence's block table as one row ("slot") of `table` [num_slots,
+ * table_stride] int32 and the number of blocks reserved for it in `reserved` [num_slots] int32.
+ *   slots         [B] int32: the slot of each row of this forward pass (clamped into the table)
+ *   positions     [B, Q] int32 / int64 (strides pos_stride_{b,q}): the positions this pass writes and queries
+ *   block_table   out [B, n_blocks] int32: the slot's blocks, 0 past the reserved ones (fastserve's padding)
+ *   write_blocks  out [B, Q] int32: the block of each position, -1 outside the reserved blocks (such rows are
+ *                 skipped by bpt_quant_append)
+ *   write_offsets out [B, Q] int32: position % page_size
+ *   context_lens  out [B] int32: the last position + 1, clamped to the reserved tokens
+ * page_size a power of two; max_blocks (<= table_stride) bounds the blocks read per slot. Nothing is read
+ * back to the host: the call is one launch and can be captured in a graph.
+ */
+typedef struct {
+  uint32_t struct_size; /* sizeof(bpt_prepare_args) */
+  int32_t batch, num_queries, n_blocks, num_slots, max_blocks, page_size;
+  int32_t positions_dtype; /* bpt_index_dtype */
+  const int32_t* table;
+  int64_t table_stride;
+  const int32_t* reserved;
+  const int32_t* slots;
+  const void* positions;
+  int64_t pos_stride_b, pos_stride_q;
+  int32_t* block_table;
+  int32_t* write_blocks;
+  int32_t* write_offsets;
+  int32_t* context_lens;
+} bpt_prepare_args;
+
+/*
  * KIVI quantize-on-write (kernels/reference.py:103-160 quantize_kv): keys and values [B, Hkv, T, D] stored as
  * asymmetric `bits`-bit codes with float16 grids, one grid per key channel per `group` tokens and one per value
  * token: lo = min(min x, 0), hi = max(max x, 0), scale = f16((hi - lo) / (2^bits - 1)) (1 where not > 0),
@@ -312,6 +344,9 @@ int bpt_paged_decode(const bpt_decode_args* args, void* stream);
  * returns BPT_ERR_INVALID_ARGUMENT. Calls on one GPU share the array: calls that may overlap (different
  * streams) race and must not be issued. */
 int bpt_paged_decode_noalloc(const bpt_decode_args* args, void* stream);
+
+/* Per-forward paged metadata (block tables, write slots, context lengths) from device positions: one launch. */
+int bpt_paged_prepare(const bpt_prepare_args* args, void* stream);
 
 /* Quantize-on-write of new K/V rows into their (page, slot). */
 int bpt_quant_append(const bpt_append_args* args, void* stream);

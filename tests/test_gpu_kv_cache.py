@@ -108,3 +108,136 @@ def test_prefill_decode_and_verify_steps(fmt):
     cache.free("b")
     cache.reserve("d", 3)
     assert cache.tables["d"][0] in set(range(64))
+
+
+def test_device_prepare_matches_the_paging_oracle():
+    """bpt_paged_prepare from device positions gives fastserve's metadata (engine/kv_cache.py:140-156, the
+    paging oracle): the tables are padded to the reserved blocks (a host-known bound), positions outside the
+    reserved blocks get no write slot."""
+    cache = PagedQuantKVCache(num_layers=1, num_kv_heads=HKV, head_dim=D, num_blocks=64, block_size=4,
+                              kv_dtype=torch.int8, device=DEV)
+    lengths = {"x": 9, "y": 1, "z": 17}
+    for s, n in lengths.items():
+        cache.reserve(s, n + 3)
+    rows = ["z", "x", "y"]
+    starts = [lengths[s] for s in rows]
+    positions = torch.tensor([[p + i for i in range(3)] for p in starts])
+    host = cache.prepare(rows, positions)
+    dev = cache.prepare(rows, positions.to(DEV))
+    wb, wo, bt, kv_len = paged.prepare([cache.tables[s] for s in rows], positions.numpy(), 4)
+    assert host.kv_len == kv_len and dev.kv_len == max(len(cache.tables[s]) for s in rows) * 4 >= kv_len
+    for meta in (host, dev):
+        assert np.array_equal(meta.write_blocks.cpu().numpy(), wb)
+        assert np.array_equal(meta.write_offsets.cpu().numpy(), wo)
+        assert np.array_equal(meta.block_table.cpu().numpy()[:, : bt.shape[1]], bt)
+        assert meta.context_lens.tolist() == [s + 3 for s in starts]
+    tables = [cache.tables[s] for s in rows]
+    pad = dev.block_table.cpu().numpy()
+    for i, t in enumerate(tables):  # past a row's own blocks: block 0, as fastserve pads
+        assert list(pad[i, : len(t)]) == t and (pad[i, len(t):] == 0).all()
+    # A position past the reserved blocks: no write slot, length clamped to the reserved tokens.
+    over = torch.tensor([[11]], device=DEV)  # "x" holds 12 reserved tokens in 3 blocks; 11 is the last slot
+    cache.reserve("w", 4)
+    meta = cache.prepare(["w"], torch.tensor([[9]], device=DEV))
+    assert meta.write_blocks.item() == -1 and meta.context_lens.item() == 4
+    meta = cache.prepare(["x"], over)
+    assert meta.write_blocks.item() == cache.tables["x"][2] and meta.context_lens.item() == 12
+
+
+def test_float32_model_gets_float32_attention():
+    """q in float32 gets float32 output, rounded once from the kernel's float32 result (fastserve merges in
+    float32 and casts once, integration/kv_cache.py:177-181), not a bfloat16 intermediate. On a bf16 cache
+    (float32 value sums) the output is within 1e-4 relative of the oracle, far inside bfloat16's rounding."""
+    cache = PagedQuantKVCache(num_layers=1, num_kv_heads=HKV, head_dim=D, num_blocks=48, block_size=16,
+                              kv_dtype=torch.bfloat16, device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(3)
+    cache.reserve("a", 300)
+    cache.reserve("b", 300)
+    pos = torch.tensor([[i for i in range(200)]] * 2)
+    k = torch.randn((2, HKV, 200, D), generator=g, device=DEV)
+    q = torch.randn((2, HQ, 200, D), generator=g, device=DEV)
+    meta = cache.prepare(["a", "b"], pos)
+    cache.attend(0, q.to(torch.bfloat16), k.to(torch.bfloat16), k.to(torch.bfloat16), meta, scale=SCALE)
+    step = cache.prepare(["a", "b"], torch.tensor([[200], [200]]))
+    qd = torch.randn((2, HQ, 1, D), generator=g, device=DEV)
+    kd = torch.randn((2, HKV, 1, D), generator=g, device=DEV).to(torch.bfloat16).float()
+    out = cache.attend(0, qd, kd, kd, step, scale=SCALE)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float32
+    want, _ = attention.paged_decode(
+        qd.transpose(1, 2).cpu().numpy(), codes_np(cache.k[0], "bf16"), codes_np(cache.v[0], "bf16"),
+        step.block_table.cpu().numpy(), step.context_lens.cpu().numpy(), None, None, "bf16", SCALE)
+    got = out.transpose(1, 2).cpu().numpy()
+    np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-5)
+    assert (out.to(torch.bfloat16).float() != out).any()  # not bfloat16 values
+
+
+@pytest.mark.parametrize("fmt", ["fp8", "int8"])
+def test_decode_steps_captured_in_a_hip_graph(fmt):
+    """prepare (from device positions) plus attend for 2 layers, captured once in a HIP graph and replayed for
+    four decode steps with new positions, queries, keys and values each time, eager work between replays; every
+    replay's stored codes are the oracle's and its attention the oracle's."""
+    dtype = {"fp8": torch.float8_e4m3fn, "int8": torch.int8}[fmt]
+    scales = {}
+    if fmt == "fp8":
+        scales = dict(k_scale=torch.full((LAYERS, HKV), 5.0 / 448), v_scale=torch.full((LAYERS, HKV), 4.0 / 448))
+    cache = PagedQuantKVCache(num_layers=LAYERS, num_kv_heads=HKV, head_dim=D, num_blocks=64, block_size=16,
+                              kv_dtype=dtype, device=DEV, **scales)
+    rows, prefill = ["a", "b", "c"], [37, 5, 20]
+    shadow = Shadow()
+    gen = torch.Generator(device=DEV).manual_seed(11)
+    for s, n in zip(rows, prefill):
+        cache.reserve(s, n + 8)  # room for the captured steps: no reserve() inside the graph
+        pos = torch.arange(n)[None]
+        meta = cache.prepare([s], pos)
+        for layer in range(LAYERS):
+            k = torch.randn((1, HKV, n, D), generator=gen, device=DEV).to(torch.bfloat16)
+            v = torch.randn((1, HKV, n, D), generator=gen, device=DEV).to(torch.bfloat16)
+            q = torch.randn((1, HQ, n, D), generator=gen, device=DEV).to(torch.bfloat16)
+            cache.attend(layer, q, k, v, meta, scale=SCALE)
+            shadow.write(layer, s, 0, k[0].float().cpu().numpy(), v[0].float().cpu().numpy())
+    # Static inputs of the captured step.
+    positions = torch.zeros((3, 1), dtype=torch.int64, device=DEV)
+    qs = [torch.zeros((3, HQ, 1, D), dtype=torch.bfloat16, device=DEV) for _ in range(LAYERS)]
+    ks = [torch.zeros((3, HKV, 1, D), dtype=torch.bfloat16, device=DEV) for _ in range(LAYERS)]
+    vs = [torch.zeros((3, HKV, 1, D), dtype=torch.bfloat16, device=DEV) for _ in range(LAYERS)]
+    side = torch.cuda.Stream()
+    lengths = dict(zip(rows, prefill))
+
+    def step():
+        meta = cache.prepare(rows, positions)
+        return meta, [cache.attend(layer, qs[layer], ks[layer], vs[layer], meta, scale=SCALE) for layer in range(LAYERS)]
+
+    def set_inputs():
+        positions.copy_(torch.tensor([[lengths[s]] for s in rows], device=DEV))
+        for layer in range(LAYERS):
+            qs[layer].copy_(torch.randn(qs[layer].shape, generator=gen, device=DEV).to(torch.bfloat16))
+            ks[layer].copy_(torch.randn(ks[layer].shape, generator=gen, device=DEV).to(torch.bfloat16))
+            vs[layer].copy_(torch.randn(vs[layer].shape, generator=gen, device=DEV).to(torch.bfloat16))
+
+    def check_step(meta, outs):
+        for layer in range(LAYERS):
+            for i, s in enumerate(rows):
+                shadow.write(layer, s, lengths[s], ks[layer][i].float().cpu().numpy(), vs[layer][i].float().cpu().numpy())
+                check_codes(cache, shadow, layer, s, lengths[s] + 1, fmt)
+            check_attention(cache, layer, qs[layer], meta, outs[layer], fmt)
+        for s in rows:
+            lengths[s] += 1
+
+    # One eager step on the side stream (it also creates the cached workspaces there), then the capture.
+    set_inputs()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        meta, outs = step()
+    side.synchronize()
+    check_step(meta, outs)
+    graph = torch.cuda.CUDAGraph()
+    set_inputs()  # the capture records the work; nothing runs until the first replay
+    with torch.cuda.graph(graph, stream=side):
+        meta, outs = step()
+    for _ in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        check_step(meta, outs)
+        torch.zeros(1 << 20, device=DEV).sum().item()  # eager work between replays
+        set_inputs()
