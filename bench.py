@@ -7,10 +7,13 @@ resident in HBM and the L2 / Infinity Cache evicted by a 1 GiB streaming read be
 the timed events). `value` = algorithmic KV bytes read per call / mean event-timed call duration.
 
 Also reported: the dominant kernel's roofline (HBM-bound; algorithmic bytes / its event-timed duration
-against 8 TB/s), the oracle timed on the host CPU over a bounded sample of the same workload, µs/call +
-GB/s for all five measured shapes, the KIVI (contiguous 4/8/16-bit cache) decode at the shapes of
-fastserve's kernel-2 benchmark, and the fused RMSNorm + INT8 quantizer at the shapes of its kernel-1
-benchmark. Prints ONE JSON line.
+against 8 TB/s); two read floors timed the same way after the same flush: a contiguous streaming read of
+exactly the call's KV bytes (read_floor_us) and a read of exactly the call's pages through its block table
+with no attention math (page_read_floor_us); the CPU baseline, the PyTorch float32 restatement of
+fastserve's CPU path (padded gather + attention, torch.set_num_threads) on the host cores over a bounded
+sample of every workload; µs/call + GB/s for all five measured shapes; the KIVI (contiguous 4/8/16-bit
+cache) decode at the shapes of fastserve's kernel-2 benchmark, and the fused RMSNorm + INT8 quantizer at
+the shapes of its kernel-1 benchmark. Prints ONE JSON line.
 """
 
 from __future__ import annotations
@@ -174,6 +177,26 @@ def timed_calls(call, flush, steps: int, warmup: int, call_ev=None):
     return [s.elapsed_time(e) for s, e in zip(starts, ends)], wall
 
 
+def read_floors(w, flush, iters: int, warmup: int) -> dict:
+    """The two read floors of workload `w`'s decode call, each the median of `iters` cold launches timed by
+    events recorded around the kernel (as the decode call is): a streaming read of exactly the call's KV
+    bytes, and a read of exactly its pages (K / V rows and per-token scales) through its block table."""
+    import torch
+
+    from bpt_amd import measure
+
+    nbytes = w.kv_bytes()
+    contiguous = measure.ReadProbe(nbytes, device="cuda:0")
+    pages = measure.PageReadProbe(*w.args(), **w.kwargs())
+    out = {}
+    for key, probe in (("read_floor_us", contiguous), ("page_read_floor_us", pages)):
+        total, _ = timed_calls(probe.run, flush, iters, warmup, lambda s, e, p=probe: p.run(events=(s, e)))
+        out[key] = round(statistics.median(total) * 1e3, 2)
+    del contiguous, pages
+    torch.cuda.empty_cache()
+    return out
+
+
 def measure_workload(name: str, flush, iters: int, warmup: int) -> dict:
     import torch
 
@@ -207,6 +230,9 @@ def measure_workload(name: str, flush, iters: int, warmup: int) -> dict:
         "scales": w.shape.scales,
         "sum_context": sum(w.lengths),
     }
+    row.update(read_floors(w, flush, iters, warmup))
+    row["pct_of_read_floor"] = round(100 * row["read_floor_us"] / row["us_per_call"], 1)
+    row["pct_of_page_read_floor"] = round(100 * row["page_read_floor_us"] / row["us_per_call"], 1)
     if w.unique_tokens != sum(w.lengths):
         ub = w.kv_bytes(unique=True)
         row["unique_kv_bytes"] = ub
@@ -306,58 +332,84 @@ def measure_norm_quant(flush, iters: int, warmup: int) -> dict:
     return table
 
 
+def cpu_model() -> str:
+    """The host CPU as /proc/cpuinfo names it: model name, family / model / stepping, cache size."""
+    fields = {}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if not line.strip():
+                    break  # the first processor's block is enough
+                key, _, val = line.partition(":")
+                fields[key.strip()] = val.strip()
+    except OSError:
+        pass
+    name = fields.get("model name") or platform.processor() or "unknown"
+    ids = ", ".join(f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping", "cache size") if k in fields)
+    return f"{name} ({ids})" if ids else name
+
+
+def cpu_threads() -> int:
+    """Host threads for the CPU baseline: the cores this process may run on, at most 16 (one GPU's share of
+    the host)."""
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    return max(1, min(avail, 16))
+
+
 def cpu_baseline(name: str, budget_s: float) -> dict:
-    """The oracle (numpy float32) on the host over the first sequences of the same workload."""
-    import numpy as np
+    """fastserve's CPU path restated in PyTorch float32 (oracle.torch_paged: the batch's pages gathered into a
+    padded contiguous view, dequantized, causal GQA attention) on the host, over the first sequences of
+    workload `name`, sized to about `budget_s` seconds."""
+    import torch
 
     from bpt_amd import workloads
-    from oracle import attention
+    from oracle import torch_paged
 
-    try:
-        from threadpoolctl import threadpool_info
-
-        threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
-    except Exception:  # threadpoolctl missing: numpy's BLAS thread count is unknown
-        threads = os.cpu_count() or 1
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
     w = workloads.make(name, device="cuda:0", seed=0)
-    o = workloads.to_oracle(w)
+    fmt = w.shape.kv_format
+    cpu = dict(q=w.q.cpu(), k=w.k_cache.cpu(), v=w.v_cache.cpu(), table=w.block_table.cpu(),
+               lens=w.context_lens.cpu(), ks=None if w.k_scale is None else w.k_scale.cpu(),
+               vs=None if w.v_scale is None else w.v_scale.cpu())
+    q4 = cpu["q"] if cpu["q"].dim() == 4 else cpu["q"][:, None]
     lengths = w.lengths
+    per_token = w.kv_bytes() / max(sum(lengths), 1)  # algorithmic bytes per cached token
 
     def run(n):
         t = time.perf_counter()
-        attention.paged_decode(o["q"][:n], o["k_pool"], o["v_pool"], o["block_table"][:n], o["context_lens"][:n],
-                               o["k_scale"], o["v_scale"], o["kv_format"], o["scale"])
+        torch_paged.paged_decode(q4[:n], cpu["k"], cpu["v"], cpu["table"][:n], cpu["lens"][:n], cpu["ks"],
+                                 cpu["vs"], fmt, w.sm_scale)
         return time.perf_counter() - t
 
-    n = min(4, len(lengths))
+    n = 1
     first = run(n)
-    per_seq = first / n
-    n = max(1, min(len(lengths), int(budget_s / 4 / max(per_seq, 1e-6))))
-    times = []
+    while n < len(lengths) and first * 2 < budget_s / 4:  # grow the sample while one run stays short
+        n = min(len(lengths), n * 2)
+        first = run(n)
+    times = [first]
     t_end = time.perf_counter() + budget_s
     while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 10):
         times.append(run(n))
     med = statistics.median(times)
-    cpu_model = platform.processor() or "unknown"
-    try:
-        with open("/proc/cpuinfo") as f:
-            cpu_model = next(line.split(":", 1)[1].strip() for line in f if line.startswith("model name"))
-    except (OSError, StopIteration):
-        pass
-    hkv = w.shape.kv_heads
-    elem = 2 if w.shape.kv_format == "bf16" else 1
-    nbytes = sum(lengths[:n]) * hkv * 128 * 2 * elem
-    del w, o
+    sample_tokens = sum(lengths[:n])
+    nbytes = sample_tokens * per_token
+    del w, cpu
     return {
         "value": round(nbytes / med / 1e9, 3),
         "unit": "GB/s",
-        "cores": int(threads),
+        "cores": threads,
         "kind": "port",
-        "sample": f"oracle paged_decode (numpy float32, BLAS threads={threads}) over the first {n} of the "
-        f"{len(lengths)} sequences ({sum(lengths[:n])} tokens), median of {len(times)} runs: "
-        f"{med * 1e3:.1f} ms per run",
-        "us_per_call_full_workload_est": round(med / sum(lengths[:n]) * sum(lengths) * 1e6, 1),
-        "cpu": f"{cpu_model}, {os.cpu_count()} logical CPUs visible",
+        "sample": f"oracle.torch_paged.paged_decode (PyTorch {torch.__version__} float32, torch.set_num_threads("
+        f"{threads})) over the first {n} of the {len(lengths)} sequences ({sample_tokens} cached tokens, "
+        f"padded to the longest as fastserve's engine does), median of {len(times)} runs: {med * 1e3:.2f} ms "
+        "per run",
+        "ms_per_run": round(med * 1e3, 3),
+        "us_per_call_full_workload_est": round(med * (sum(lengths) / max(sample_tokens, 1)) * 1e6, 1),
+        "cpu": f"{cpu_model()}, {os.cpu_count()} logical CPUs visible, {threads} used",
     }
 
 
@@ -414,6 +466,8 @@ def main() -> int:
     value = nbytes / (ms_per_step * 1e-3) / 1e9
     log(f"{ms_per_step * 1e3:.1f} us/call ({value:.0f} GB/s)")
 
+    floors = read_floors(w, flush, args.steps, args.warmup)
+    log(f"read floors: {floors['read_floor_us']} us contiguous, {floors['page_read_floor_us']} us through the pages")
     read_gbps = measure.measured_read_gbps(4 << 30)
     log(f"read probe: {read_gbps:.0f} GB/s")
     from bpt_amd import decode_plan
@@ -458,6 +512,10 @@ def main() -> int:
         "pct_of_peak": round(100 * value / PEAK_GBPS, 1),
         "pct_of_measured_read": round(100 * value / read_gbps, 1),
         "measured_read_gbps": round(read_gbps, 1),
+        "read_floor_us": floors["read_floor_us"],
+        "page_read_floor_us": floors["page_read_floor_us"],
+        "pct_of_read_floor": round(100 * floors["read_floor_us"] / (ms_per_step * 1e3), 1),
+        "pct_of_page_read_floor": round(100 * floors["page_read_floor_us"] / (ms_per_step * 1e3), 1),
         "wall_s_timed_region": round(wall, 4),
         "roofline": {
             "bound": "hbm",
@@ -487,6 +545,13 @@ def main() -> int:
     if not args.no_cpu_baseline:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(args.workload, args.cpu_seconds)
+        if "configs" in result:
+            for name, row in result["configs"].items():
+                if name == args.workload:
+                    row["cpu_baseline"] = result["cpu_baseline"]
+                    continue
+                log(f"cpu baseline {name}")
+                row["cpu_baseline"] = cpu_baseline(name, args.cpu_seconds / 2)
     print(json.dumps(result), flush=True)
     return 0
 

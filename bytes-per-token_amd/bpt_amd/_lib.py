@@ -285,10 +285,12 @@ SIGNATURES = {
     "bpt_fp8_decode_table": (_i32, [_vp, _vp]),
     "bpt_fp8_encode": (_i32, [_vp, ctypes.c_float, _vp, _i64, _vp]),
     "bpt_read_probe": (_i32, [_vp, ctypes.c_uint64, _vp, ctypes.POINTER(_i64), _vp]),
+    "bpt_read_probe_timed": (_i32, [_vp, ctypes.c_uint64, _vp, _vp, _vp, _vp]),
+    "bpt_page_read_probe": (_i32, [ctypes.POINTER(DecodeArgs), _vp, ctypes.POINTER(_i64), _vp, _vp, _vp]),
     "bpt_copy_probe": (_i32, [_vp, _vp, ctypes.c_uint64, _vp]),
 }
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 
 class BptError(RuntimeError):

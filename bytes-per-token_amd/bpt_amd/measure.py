@@ -36,12 +36,45 @@ class ReadProbe:
         self.partial = torch.empty(groups.value, dtype=torch.float32, device=device)
         self.device = self.buf.device
 
-    def run(self) -> None:
-        _lib.check(
-            _lib.lib().bpt_read_probe(
-                self.buf.data_ptr(), self.nbytes, self.partial.data_ptr(), None, _stream(self.device)
+    def run(self, events: tuple | None = None) -> None:
+        """One full read; with `events` (two raw hipEvent_t handles) they are recorded around the kernel."""
+        if events is None:
+            _lib.check(
+                _lib.lib().bpt_read_probe(
+                    self.buf.data_ptr(), self.nbytes, self.partial.data_ptr(), None, _stream(self.device)
+                )
             )
-        )
+        else:
+            _lib.check(
+                _lib.lib().bpt_read_probe_timed(
+                    self.buf.data_ptr(), self.nbytes, self.partial.data_ptr(), _stream(self.device),
+                    ctypes.c_void_p(events[0]), ctypes.c_void_p(events[1]),
+                )
+            )
+
+
+class PageReadProbe:
+    """Reads every K / V row (and per-token scale) that paged_decode_attention over the same arguments reads,
+    through the same block table and lengths, with no attention math: the read floor of the call's pages."""
+
+    def __init__(self, q, k_cache, v_cache, block_table, context_lens, k_scale=None, v_scale=None, *, scale,
+                 max_context, num_splits=None):
+        from .paged_attention import _decode_args
+
+        q4 = q[:, None] if q.dim() == 3 else q
+        self.args, _ = _decode_args(q4, k_cache, v_cache, block_table, context_lens, k_scale, v_scale, scale,
+                                    max_context, num_splits, torch.bfloat16)
+        self._keep = (k_cache, v_cache, block_table, context_lens, k_scale, v_scale)
+        groups = ctypes.c_int64(0)
+        _lib.check(_lib.lib().bpt_page_read_probe(ctypes.byref(self.args), None, ctypes.byref(groups), None, None,
+                                                  None))
+        self.partial = torch.empty(max(groups.value, 1), dtype=torch.float32, device=q.device)
+        self.device = q.device
+
+    def run(self, events: tuple | None = None) -> None:
+        ev = (None, None) if events is None else (ctypes.c_void_p(events[0]), ctypes.c_void_p(events[1]))
+        _lib.check(_lib.lib().bpt_page_read_probe(ctypes.byref(self.args), self.partial.data_ptr(), None,
+                                                  _stream(self.device), *ev))
 
 
 def copy_probe(dst: torch.Tensor, src: torch.Tensor, nbytes: int) -> None:

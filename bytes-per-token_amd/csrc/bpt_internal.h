@@ -222,11 +222,11 @@ struct LaunchEvents {
   hipEvent_t start = nullptr, stop = nullptr;
 };
 
-template <typename K, typename P>
+template <typename K, typename... A>
 inline void launch_kernel(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t stream, const LaunchEvents& ev,
-                          const P& p) {
-  if (ev.start) hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, stream, ev.start, ev.stop, 0u, p);
-  else hipLaunchKernelGGL(kernel, grid, block, lds, stream, p);
+                          const A&... args) {
+  if (ev.start) hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, stream, ev.start, ev.stop, 0u, args...);
+  else hipLaunchKernelGGL(kernel, grid, block, lds, stream, args...);
 }
 
 hipError_t launch_decode(const DecodeParams& p, int kv_dtype, int scale_kind, int rows_per_group, hipStream_t stream,
@@ -243,7 +243,11 @@ hipError_t launch_append(const AppendParams& p, int kv_dtype, int scale_kind, in
 hipError_t launch_fp8_table(float* out, hipStream_t stream);
 hipError_t launch_fp8_encode(const float* x, float scale, uint8_t* out, int64_t n, hipStream_t stream);
 int64_t read_probe_groups(uint64_t bytes);
-hipError_t launch_read_probe(const void* buf, uint64_t bytes, float* partial, hipStream_t stream);
+hipError_t launch_read_probe(const void* buf, uint64_t bytes, float* partial, hipStream_t stream,
+                             const LaunchEvents& ev = {});
+int64_t page_read_probe_groups(int B, int Hkv, int len_cap);
+hipError_t launch_page_read_probe(const DecodeParams& p, int row_bytes, bool with_scales, float* partial,
+                                  hipStream_t stream, const LaunchEvents& ev = {});
 hipError_t launch_copy_probe(void* dst, const void* src, uint64_t bytes, hipStream_t stream);
 
 }  // namespace bpt

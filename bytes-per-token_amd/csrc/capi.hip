@@ -750,6 +750,74 @@ int bpt_read_probe(const void* buf, uint64_t bytes, float* partial_sums, int64_t
   return e == hipSuccess ? BPT_OK : hip_fail("bpt_read_probe", e);
 }
 
+int bpt_read_probe_timed(const void* buf, uint64_t bytes, float* partial_sums, void* stream, void* start_event,
+                         void* stop_event) {
+  const char* fn = "bpt_read_probe_timed";
+  if (bytes % 16 || bytes == 0) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: bytes must be a positive multiple of 16", fn);
+  if (!buf || !aligned16(buf) || !partial_sums)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: a 16-byte aligned buffer and partial_sums are required", fn);
+  if (!start_event || !stop_event) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: both events are required", fn);
+  bpt::LaunchEvents ev;
+  ev.start = (hipEvent_t)start_event;
+  ev.stop = (hipEvent_t)stop_event;
+  hipError_t e = bpt::launch_read_probe(buf, bytes, partial_sums, (hipStream_t)stream, ev);
+  return e == hipSuccess ? BPT_OK : hip_fail(fn, e);
+}
+
+int bpt_page_read_probe(const bpt_decode_args* a, float* partial_sums, int64_t* num_groups, void* stream,
+                        void* start_event, void* stop_event) {
+  const char* fn = "bpt_page_read_probe";
+  Plan pl;
+  int rc = make_plan(a, &pl);
+  if (rc) return rc;
+  const int64_t g = bpt::page_read_probe_groups(a->batch, a->num_kv_heads, pl.len_cap);
+  if (num_groups) *num_groups = g;
+  if (!partial_sums) return BPT_OK;
+  if (!a->k_cache || !a->v_cache || !a->block_table)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: caches and block_table must be non-NULL", fn);
+  const bool per_token = a->kv_dtype != BPT_KV_BF16 && a->scale_kind == BPT_SCALE_PER_TOKEN_HEAD;
+  if (per_token && (!a->k_scale || !a->v_scale))
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: per-token scales are required for this cache", fn);
+  const int eb = a->kv_dtype == BPT_KV_BF16 ? 2 : 1;
+  if (!aligned16(a->k_cache) || !aligned16(a->v_cache) || (a->kv_stride_block * eb) % 16 ||
+      (a->kv_stride_token * eb) % 16 || (a->kv_stride_head * eb) % 16)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: cache pointers and strides must be 16-byte aligned", fn);
+  if ((start_event == nullptr) != (stop_event == nullptr))
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: give both events or neither", fn);
+  bpt::DecodeParams p{};
+  p.k = (const uint8_t*)a->k_cache;
+  p.v = (const uint8_t*)a->v_cache;
+  p.kv_sblk = a->kv_stride_block * eb;
+  p.kv_stok = a->kv_stride_token * eb;
+  p.kv_shead = a->kv_stride_head * eb;
+  p.ks = a->k_scale;
+  p.vs = a->v_scale;
+  p.sc_sblk = a->scale_stride_block;
+  p.sc_stok = a->scale_stride_token;
+  p.sc_shead = a->scale_stride_head;
+  p.table = a->block_table;
+  p.table_sb = a->table_stride_b;
+  p.table_i64 = a->table_dtype == BPT_IDX_I64;
+  p.lens = a->context_lens;
+  p.B = a->batch;
+  p.Hkv = a->num_kv_heads;
+  p.P = a->page_size;
+  p.logP = log2i(a->page_size);
+  p.num_blocks = a->num_blocks;
+  p.len_cap = pl.len_cap;
+  p.len_offset = a->len_offset;
+  bpt::LaunchEvents ev;
+  ev.start = (hipEvent_t)start_event;
+  ev.stop = (hipEvent_t)stop_event;
+  if (g == 0 && ev.start) {
+    hipError_t e = hipEventRecord(ev.start, (hipStream_t)stream);
+    if (e == hipSuccess) e = hipEventRecord(ev.stop, (hipStream_t)stream);
+    return e == hipSuccess ? BPT_OK : hip_fail(fn, e);
+  }
+  hipError_t e = bpt::launch_page_read_probe(p, a->head_dim * eb, per_token, partial_sums, (hipStream_t)stream, ev);
+  return e == hipSuccess ? BPT_OK : hip_fail(fn, e);
+}
+
 int bpt_copy_probe(void* dst, const void* src, uint64_t bytes, void* stream) {
   if (bytes % 16 || !dst || !src || !aligned16(dst) || !aligned16(src))
     return fail(BPT_ERR_INVALID_ARGUMENT, "bpt_copy_probe: 16-byte aligned buffers, bytes a multiple of 16");

@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define BPT_ABI_VERSION 10
+#define BPT_ABI_VERSION 11
 
 /* return codes */
 #define BPT_OK 0
@@ -393,6 +393,22 @@ int bpt_paged_decode_timed(const bpt_decode_args* args, void* stream, void* star
  * in *num_groups so the caller can size partial_sums (call with partial_sums = NULL to query). */
 int bpt_read_probe(const void* buf, uint64_t bytes, float* partial_sums, int64_t* num_groups,
                    void* stream);
+
+/* bpt_read_probe of `bytes` (a positive multiple of 16) whose launch records two HIP events around the kernel's
+ * own execution, as bpt_paged_decode_timed does: the contiguous-read floor for a byte count, timed the way
+ * the decode kernel is. partial_sums holds the workgroup count bpt_read_probe reports. No reference
+ * counterpart. */
+int bpt_read_probe_timed(const void* buf, uint64_t bytes, float* partial_sums, void* stream, void* start_event,
+                         void* stop_event);
+
+/* The page-read probe: every K and V row (and per-token scale) that bpt_paged_decode over the same args
+ * reads, fetched through the same block table and context lengths with no attention math (one float per
+ * workgroup into partial_sums). It is the read floor of a decode call's own access pattern. Call with
+ * partial_sums = NULL to get the workgroup count in *num_groups. Optional events as bpt_read_probe_timed
+ * (both or neither). Uses only the cache, scale, table and length fields of args. No reference
+ * counterpart. */
+int bpt_page_read_probe(const bpt_decode_args* args, float* partial_sums, int64_t* num_groups, void* stream,
+                        void* start_event, void* stop_event);
 
 /* dst <- src, `bytes` a multiple of 16: the known-size kernel that calibrates HBM byte counters. */
 int bpt_copy_probe(void* dst, const void* src, uint64_t bytes, void* stream);

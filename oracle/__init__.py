@@ -17,10 +17,13 @@ Each function cites the fastserve file:line (relative to src/fastserve/) whose a
 * attention.py  partial_attention / merge_partials (kernels/reference.py:186-211), causal multi-query
                 attention by absolute position (engine/attention.py:12-47), the paged decode the HIP kernel
                 computes, and default_split (kernels/kv_attention.py:178-187)
+* torch_paged.py the same paged decode in float32 PyTorch, computed as fastserve's CPU path does (padded
+                gather engine/kv_cache.py:140-169, attention engine/attention.py:12-47): the timed CPU baseline
 
 How each is pinned (tests/test_oracle_*.py): the FP8 codec against torch's float8_e4m3fn cast on all 256
 codes, every tie and multi-scale randoms; the INT8 quantizer against the reference tests' known answers and
 a brute-force nearest-code search; attention against float64 brute-force loops, closed forms (uniform
 scores give the mean of V, one visible token gives its value), split-merge exactness, empty rows, the GQA
-head mapping and causal visibility; default_split against the reference tests' known answers.
+head mapping and causal visibility; default_split against the reference tests' known answers; torch_paged
+against attention.paged_decode on every cache format.
 """

@@ -167,6 +167,47 @@ def test_quantized_paged_decode_reads_the_cache_as_stored(fmt):
     np.testing.assert_allclose(out, want, rtol=1e-6, atol=1e-6)
 
 
+@pytest.mark.parametrize("fmt,scales", [("bf16", None), ("fp8", "head"), ("fp8", "token"), ("int8", "token"),
+                                         ("int8", "head")])
+def test_torch_restatement_equals_the_numpy_oracle(fmt, scales):
+    """oracle.torch_paged (the CPU baseline's PyTorch path, padded batch like fastserve's engine) gives the
+    numpy oracle's result on ragged lengths (one of them empty), several queries and every cache format."""
+    import torch
+
+    from oracle import torch_paged
+
+    lengths = [13, 1, 8, 0, 22]
+    nq = 2
+    k, v, k_pool_f, v_pool_f, table = paged_inputs(lengths, hkv=2, d=16, page=4, seed=6)
+    lens = np.array([max(t, 0) for t in lengths])
+    if fmt == "bf16":
+        k_pool = torch.from_numpy(k_pool_f).bfloat16()
+        v_pool = torch.from_numpy(v_pool_f).bfloat16()
+        kn, vn = k_pool.float().numpy(), v_pool.float().numpy()
+        ks = vs = None
+    elif scales == "head":
+        ks = quant.per_head_scale(k_pool_f, 448.0 if fmt == "fp8" else 127.0)
+        vs = quant.per_head_scale(v_pool_f, 448.0 if fmt == "fp8" else 127.0)
+        enc = quant.fp8_per_head if fmt == "fp8" else quant.int8_per_head
+        kn, vn = enc(k_pool_f, ks), enc(v_pool_f, vs)
+    else:
+        kn, ks = quant.per_token(k_pool_f, fmt)
+        vn, vs = quant.per_token(v_pool_f, fmt)
+        ks, vs = ks[..., 0], vs[..., 0]
+    if fmt != "bf16":
+        as_torch = (lambda c: torch.from_numpy(c).view(torch.float8_e4m3fn)) if fmt == "fp8" else torch.from_numpy
+        k_pool, v_pool = as_torch(kn), as_torch(vn)
+    q = rand(len(lengths), nq, 4, 16, seed=12)
+    want, want_lse = attention.paged_decode(q, kn, vn, table, lens, ks, vs, fmt, 0.3)
+    got, got_lse = torch_paged.paged_decode(
+        torch.from_numpy(q), k_pool, v_pool, torch.from_numpy(table), torch.from_numpy(lens).int(),
+        None if ks is None else torch.from_numpy(ks), None if vs is None else torch.from_numpy(vs), fmt, 0.3)
+    np.testing.assert_allclose(got.numpy(), want, rtol=1e-5, atol=1e-6)
+    np.testing.assert_array_equal(np.isneginf(got_lse.numpy()), np.isneginf(want_lse))
+    fin = np.isfinite(want_lse)
+    np.testing.assert_allclose(got_lse.numpy()[fin], want_lse[fin], rtol=1e-5, atol=1e-6)
+
+
 def test_default_split_known_answers():
     gold = GOLDEN["default_split"]
     for c in gold["cases"]:
