@@ -51,22 +51,13 @@ __device__ __forceinline__ void load_vec(const void* base, int64_t idx, int dtyp
   }
 }
 
-// y / scale: the product with the row's reciprocal (computed once, correctly rounded), refined once with
-// the exact remainder fma(-q, scale, y). This is the correctly rounded quotient nearly always and one ulp
-// from it otherwise, which can move a code only when y / scale sits exactly half-way between two codes.
-__device__ __forceinline__ float quotient(float y, float scale, float inv) {
-  const float q = y * inv;
-  return fmaf(fmaf(-q, scale, y), inv, q);
-}
-
 // Codes of VEC elements of one row, written at element e.
 template <int VEC>
 __device__ __forceinline__ void store_codes(int8_t* row, int e, int d, const float (&y)[VEC], float scale) {
-  const float inv = __fdiv_rn(1.0f, scale);
   uint32_t c[VEC];
 #pragma unroll
   for (int j = 0; j < VEC; ++j) {
-    float q = rintf(quotient(y[j], scale, inv));
+    float q = rintf(__fdiv_rn(y[j], scale));  // IEEE division, as torch's y / scale
     q = q > 127.0f ? 127.0f : (q < -128.0f ? -128.0f : q);
     c[j] = (uint32_t)(int)q & 0xffu;
   }

@@ -25,7 +25,8 @@
 //
 // Compute: FP8 and BF16 keys are dotted with q held as bf16 pairs (v_dot2_f32_bf16; FP8 codes convert to
 // bf16 exactly); FP8 values are decoded to f16 two tokens at a time and accumulated with v_dot2_f32_f16
-// over token pairs; INT8 uses f32 FMAs. Scales fold out of the inner loop: a per-head K scale and
+// over token pairs, the weights as f16 plus their f16 rounding remainders (22 significant bits); INT8
+// uses f32 FMAs. Scales fold out of the inner loop: a per-head K scale and
 // sm_scale * log2(e) multiply the reduced score, a per-head V scale multiplies the final output, per-token
 // scales multiply the reduced score (K) and the softmax weight (V). Softmax runs in base 2 with a lazily
 // moved reference point; the workspace lse is in log2 units.
@@ -264,9 +265,12 @@ __device__ __forceinline__ void compute_chunk(const ChunkRegs<CL>& c, int kk, in
     // channel c of both rows, and one dot product adds both rows' weighted contributions to channel c.
 #pragma unroll
     for (int i = 0; i < CL; i += 2) {
-      f16x2 pp[RG];
+      f16x2 pp[RG], pr[RG];  // weights in f16 and their rounding remainders (22 significant bits together)
 #pragma unroll
-      for (int r = 0; r < RG; ++r) pp[r] = f16x2{(_Float16)pw[i][r], (_Float16)pw[i + 1][r]};
+      for (int r = 0; r < RG; ++r) {
+        pp[r] = f16x2{(_Float16)pw[i][r], (_Float16)pw[i + 1][r]};
+        pr[r] = f16x2{(_Float16)(pw[i][r] - (float)pp[r].x), (_Float16)(pw[i + 1][r] - (float)pp[r].y)};
+      }
       const uint32_t a[4] = {c.v[i].x, c.v[i].y, c.v[i].z, c.v[i].w};
       const uint32_t b[4] = {c.v[i + 1].x, c.v[i + 1].y, c.v[i + 1].z, c.v[i + 1].w};
 #pragma unroll
@@ -283,6 +287,10 @@ __device__ __forceinline__ void compute_chunk(const ChunkRegs<CL>& c, int kk, in
           acc[r][4 * d + 1] = __builtin_amdgcn_fdot2(v1, pp[r], acc[r][4 * d + 1], false);
           acc[r][4 * d + 2] = __builtin_amdgcn_fdot2(v2, pp[r], acc[r][4 * d + 2], false);
           acc[r][4 * d + 3] = __builtin_amdgcn_fdot2(v3, pp[r], acc[r][4 * d + 3], false);
+          acc[r][4 * d + 0] = __builtin_amdgcn_fdot2(v0, pr[r], acc[r][4 * d + 0], false);
+          acc[r][4 * d + 1] = __builtin_amdgcn_fdot2(v1, pr[r], acc[r][4 * d + 1], false);
+          acc[r][4 * d + 2] = __builtin_amdgcn_fdot2(v2, pr[r], acc[r][4 * d + 2], false);
+          acc[r][4 * d + 3] = __builtin_amdgcn_fdot2(v3, pr[r], acc[r][4 * d + 3], false);
         }
       }
     }

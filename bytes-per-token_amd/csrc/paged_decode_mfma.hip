@@ -18,7 +18,8 @@
 //    two shuffles and keep partial weight sums that are added at the end.
 //  * output O^T += V^T P^T with v_mfma_f32_16x16x32_f16: the contraction index k = 8 kq + j is mapped to
 //    the lane's own score tokens (j < 4: 4 kq + j, j >= 4: 16 + 4 kq + j - 4), so P^T comes straight
-//    from this lane's weights (f16). V^T needs tokens contiguous per lane: V rows are loaded whole like K
+//    from this lane's weights, as f16 plus a second product with their f16 rounding remainders (22
+//    significant bits, float32-accurate outputs). V^T needs tokens contiguous per lane: V rows are loaded whole like K
 //    and passed through the same LDS tile, from which the lane reads channels 8 n' .. 8 n' + 7
 //    (n' = l % 16) of its eight tokens (8 bytes each); it transposes 4 x 4 byte blocks with v_perm and
 //    decodes FP8 -> f16 exactly; M-tile mu holds channels 8 n' + mu. The accumulator then gives lane l
@@ -255,12 +256,14 @@ __device__ __forceinline__ void mfma_compute(MChunk& c, U4 (&sk)[2][16][8], floa
     m = mn;
   }
   const float base = (m == kNegInf ? 0.0f : m) - kBias;
-  f16x8 pb;
+  f16x8 pb, pr;  // the weights in f16 and their rounding remainders: 22 significant bits between them
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const float e = fast_exp2(sc[j] - base);
     l += e;
-    pb[j] = (_Float16)(SK == kScaleTokenHead ? e * vs4[j >> 2][j & 3] : e);
+    const float w = SK == kScaleTokenHead ? e * vs4[j >> 2][j & 3] : e;
+    pb[j] = (_Float16)w;
+    pr[j] = (_Float16)(w - (float)pb[j]);
   }
 
   // ---- O^T += V^T P^T: eight M-tiles of 16 channels (tile mu: channels 8 n' + mu) -------------------------
@@ -296,6 +299,7 @@ __device__ __forceinline__ void mfma_compute(MChunk& c, U4 (&sk)[2][16][8], floa
     const uint32_t d1 = mu < 4 ? lo[1][mu & 3] : hi[1][mu & 3];
     const f16x8 a = KV == kKvInt8 ? int8x8_to_f16(d0, d1) : fp8x8_to_f16(d0, d1);
     o[mu] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb, o[mu], 0, 0, 0);
+    o[mu] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pr, o[mu], 0, 0, 0);
   }
 }
 

@@ -365,3 +365,23 @@ def test_per_token_value_scales_far_from_one(fmt, nq, hq, hkv, v_mag):
     check(got / v_mag, want / v_mag, f"{fmt} Q={nq} Hq={hq} Hkv={hkv} values x{v_mag:g}")
     got, want = run_case(c, out_dtype=torch.float32, num_splits=3)
     check(got / v_mag, want / v_mag, f"{fmt} Q={nq} Hq={hq} Hkv={hkv} values x{v_mag:g}, 3 splits")
+
+
+@pytest.mark.parametrize("fmt,scales,nq,hq,hkv", [
+    ("fp8", "head", 1, 16, 8),    # matrix cores, 2 rows
+    ("fp8", "token", 5, 16, 8),   # matrix cores, 10 rows, per-token scales
+    ("fp8", "head", 1, 8, 8),     # vector kernel, 1 row
+    ("fp8", "token", 1, 8, 8),
+    ("int8", "token", 1, 16, 8),  # vector kernel
+    ("int8", "head", 3, 16, 8),   # matrix cores, 6 rows
+    ("bf16", None, 1, 16, 8),
+])
+def test_float32_output_is_float32_accurate(fmt, scales, nq, hq, hkv):
+    """With float32 output the kernels stay within 1e-4 of the largest output (float32 arithmetic, the
+    softmax weights of the packed f16 value products carried as f16 plus their f16 rounding remainder), some
+    20 times inside the bf16-output tolerance the other tests use."""
+    c = make_case(fmt, [1030, 5, 64, 2000, 33], nq=nq, hq=hq, hkv=hkv, scales=scales)
+    for splits in (None, 4):
+        got, want = run_case(c, out_dtype=torch.float32, num_splits=splits)
+        err = np.abs(got.cpu().numpy() - want).max()
+        assert err <= 1e-4 * np.abs(want).max(), f"{fmt} {scales} Q={nq} Hq={hq}: {err:.3e} vs max {np.abs(want).max():.3e}"
