@@ -102,6 +102,10 @@ __device__ __forceinline__ void fetch_pages(const DecodeParams& p, int b, int kk
 // Issue chunk kk's 16-byte K and V loads (and per-token scales) into c. PU: each load's page and the row
 // offset of its first token are wave-uniform, so the address is a scalar base plus this lane's constant
 // 32-bit offset (slot rows down, part * 16 bytes across).
+// Rows at or past len: INT8 codes are loaded anyway from the (valid) page fetch_pages chose, since any byte
+// is a finite code, their scores are masked and their value scale is zeroed, so they weigh nothing; this
+// keeps the loads unconditional. FP8 and BF16 rows there are zero-filled instead (stale bytes could hold
+// NaN codes, and NaN times a zero weight is NaN).
 template <int KV, int SK, int CL, bool PU>
 __device__ __forceinline__ void issue_chunk(const DecodeParams& p, const ChunkPages<CL>& g, int h, int kk, int len,
                                             int slot, int part, ChunkRegs<CL>& c) {
@@ -113,7 +117,7 @@ __device__ __forceinline__ void issue_chunk(const DecodeParams& p, const ChunkPa
     const int t = tb + i * RPL + slot;
     c.ks[i] = 1.0f;
     c.vs[i] = 1.0f;
-    if (t < len) {
+    if (KV == kKvInt8 || t < len) {
       if constexpr (PU) {
         const int w0 = (tb + i * RPL) & (p.P - 1);  // wave-uniform: this lane's row is w0 + slot
         const int64_t base = (int64_t)g.e[i] * p.kv_sblk + (int64_t)w0 * p.kv_stok + head_off;
@@ -124,7 +128,7 @@ __device__ __forceinline__ void issue_chunk(const DecodeParams& p, const ChunkPa
           const int64_t sb = (int64_t)g.e[i] * p.sc_sblk + (int64_t)w0 * p.sc_stok + (int64_t)h * p.sc_shead;
           const uint32_t so = (uint32_t)(slot * p.sc_stok);
           c.ks[i] = p.ks[sb + so];
-          c.vs[i] = p.vs[sb + so];
+          c.vs[i] = t < len ? p.vs[sb + so] : 0.0f;
         }
       } else {
         const int within = t & (p.P - 1);
@@ -134,7 +138,7 @@ __device__ __forceinline__ void issue_chunk(const DecodeParams& p, const ChunkPa
         if constexpr (SK == kScaleTokenHead) {
           const int64_t so = (int64_t)g.e[i] * p.sc_sblk + (int64_t)within * p.sc_stok + (int64_t)h * p.sc_shead;
           c.ks[i] = p.ks[so];
-          c.vs[i] = p.vs[so];
+          c.vs[i] = t < len ? p.vs[so] : 0.0f;
         }
       }
     } else {
@@ -488,14 +492,17 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeP
     }
 
     // Chunks k + wave, k + wave + NW, ... of this piece; chunk kk's loads are in flight on entry to its
-    // iteration, the next chunk's pages are fetched while it is computed, then its loads are issued.
-    for (int kk = k + wave; kk < k_end;) {
+    // iteration, the next chunk's pages are fetched while it is computed, then its loads are issued. The
+    // last chunk is peeled off so that the loop body issues unconditionally (no register copies of the
+    // chunk buffer for a skipped issue).
+    int kk = k + wave;
+    for (; kk + NW < k_end; kk += NW) {
       const int kn = kk + NW;
-      if (kn < k_end) fetch_pages<KV, CL, PU>(p, b, kn, len, slot, gp);
+      fetch_pages<KV, CL, PU>(p, b, kn, len, slot, gp);
       compute_chunk<KV, SK, RG, CL, QS>(cr, kk, slot, q, rlen, m, l, acc);
-      if (kn < k_end) issue_chunk<KV, SK, CL, PU>(p, gp, h, kn, len, slot, part, cr);
-      kk = kn;
+      issue_chunk<KV, SK, CL, PU>(p, gp, h, kn, len, slot, part, cr);
     }
+    if (kk < k_end) compute_chunk<KV, SK, RG, CL, QS>(cr, kk, slot, q, rlen, m, l, acc);
 
     // The next piece (if the range holds chunks of the next segment): its q rows and this wave's first
     // chunk go in flight now.
