@@ -53,6 +53,16 @@ constexpr int kDecodeGroupsPerCu = BPT_DECODE_GROUPS_PER_CU;
 constexpr int kManyRows = 8;
 constexpr int kMfmaManyRowWaves = 8;
 constexpr int kDecodeMinChunksManyRows = BPT_DECODE_MIN_CHUNKS_MANY_ROWS;
+// Workgroups per CU of the vector kernel. INT8 caches run three (12 waves per CU, three per SIMD; those
+// kernels are compiled to fit 168 VGPRs for it) with one row per group, and with two when pages hold whole
+// 8-row loads and q is bf16 (the other two-row instances would spill at 168); everything else runs two.
+// INT8's per-chunk work leaves two waves per SIMD short of memory-level parallelism: on the INT8 workload
+// three took the call from 202 to 192 us.
+constexpr int kDecodeGroupsPerCuInt8 = 3;
+constexpr int decode_groups_per_cu(bool int8, int rows_per_group, bool page_uniform, bool q_split) {
+  return int8 && (rows_per_group == 1 || (rows_per_group == 2 && page_uniform && !q_split)) ? kDecodeGroupsPerCuInt8
+                                                                                            : kDecodeGroupsPerCu;
+}
 // Waves per matrix-core workgroup for segments of `rows` rows, and workgroups per CU.
 constexpr int mfma_waves(int rows) { return rows >= kManyRows ? kMfmaManyRowWaves : kDecodeWaves; }
 constexpr int mfma_groups_per_cu(int rows) { return rows >= kManyRows ? 1 : kDecodeGroupsPerCu; }

@@ -105,13 +105,17 @@ int make_plan(const bpt_decode_args* a, Plan* pl) {
   if (seq_cost > 0x7fffffffLL / (hr > 0 ? hr : 1))
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: batch x context x heads too large", fn);
   const int64_t bound_c = seq_chunks * hr;
+  const int groups_per_cu =
+      pl->mfma ? bpt::mfma_groups_per_cu(pl->rows)
+               : bpt::decode_groups_per_cu(a->kv_dtype == BPT_KV_INT8, pl->rows_per_group,
+                                           a->page_size >= bpt::decode_rows_per_load(a->kv_dtype),
+                                           a->q_dtype != BPT_F_BF16);
   if (a->num_splits > 0) {
     // num_splits partitions for a max_context sequence. When that gives more partitions than resident
     // workgroups, each workgroup takes several consecutive ones whole: inside a workgroup the online
     // softmax simply continues across their boundary (the log-sum-exp merge of the two partials, done in
     // registers), so the partials that go through memory are those of the resident workgroups.
-    const int64_t max_grid =
-        (int64_t)bpt::kComputeUnits * (pl->mfma ? bpt::mfma_groups_per_cu(pl->rows) : bpt::kDecodeGroupsPerCu);
+    const int64_t max_grid = (int64_t)bpt::kComputeUnits * groups_per_cu;
     int64_t per = (max_nb + a->num_splits - 1) / a->num_splits;
     if (per < 1) per = 1;
     const int64_t parts = (bound_c + per - 1) / per;
@@ -121,8 +125,7 @@ int make_plan(const bpt_decode_args* a, Plan* pl) {
     pl->grid = (int)(grid < 1 ? 1 : grid);
   } else {
     pl->per_forced = 0;
-    int64_t grid =
-        (int64_t)bpt::kComputeUnits * (pl->mfma ? bpt::mfma_groups_per_cu(pl->rows) : bpt::kDecodeGroupsPerCu);
+    int64_t grid = (int64_t)bpt::kComputeUnits * groups_per_cu;
     const int64_t min_chunks = pl->mfma && pl->rows >= bpt::kManyRows ? bpt::kDecodeMinChunksManyRows : 1;
     const int64_t fill = (bound_c + min_chunks - 1) / min_chunks;
     if (fill < grid) grid = fill;

@@ -24,9 +24,10 @@
 // summed over the 8 lanes of a slot with DPP. BF16 pools use 16 lanes per row (8 channels each).
 //
 // Compute: FP8 and BF16 keys are dotted with q held as bf16 pairs (v_dot2_f32_bf16; FP8 codes convert to
-// bf16 exactly); FP8 values are decoded to f16 two tokens at a time and accumulated with v_dot2_f32_f16
-// over token pairs, the weights as f16 plus their f16 rounding remainders (22 significant bits); INT8
-// uses f32 FMAs. Scales fold out of the inner loop: a per-head K scale and
+// bf16 exactly), and so are INT8 keys when q is bf16 (codes converted exactly through f32); FP8 values are
+// decoded to f16 two tokens at a time and accumulated with v_dot2_f32_f16 over token pairs, the weights as
+// f16 plus their f16 rounding remainders (22 significant bits); INT8 values (and INT8 keys under an f16 /
+// f32 q) use f32 FMAs. Scales fold out of the inner loop: a per-head K scale and
 // sm_scale * log2(e) multiply the reduced score, a per-head V scale multiplies the final output, per-token
 // scales multiply the reduced score (K) and the softmax weight (V). Softmax runs in base 2 with a lazily
 // moved reference point; the workspace lse is in log2 units.
@@ -150,11 +151,12 @@ __device__ __forceinline__ void issue_chunk(const DecodeParams& p, const ChunkPa
 
 // The query rows of a piece in the form the score path consumes. Dot-product paths (FP8, BF16 caches)
 // keep q unscaled as bf16 pairs: exact for a bf16 q; for an f16 / f32 q (QS) a second pair holds the
-// rounding remainder, so hi + lo carries 16 significant bits. The INT8 path keeps floats pre-scaled.
+// rounding remainder, so hi + lo carries 16 significant bits. INT8 caches under an f16 / f32 q keep
+// pre-scaled floats instead.
 template <int KV, int RG, bool QS>
 struct QRows {
   static constexpr int VEC = KvTraits<KV>::kVec;
-  static constexpr bool kDot = KV != kKvInt8;
+  static constexpr bool kDot = KV != kKvInt8 || !QS;  // INT8 with a bf16 q: codes made bf16, q exact
   bf16x2 hi[RG][kDot ? VEC / 2 : 1];
   bf16x2 lo[RG][(kDot && QS) ? VEC / 2 : 1];
   float f[RG][kDot ? 1 : VEC];
@@ -170,7 +172,7 @@ __device__ __forceinline__ void compute_chunk(const ChunkRegs<CL>& c, int kk, in
   constexpr int LPR = KvTraits<KV>::kLanesPerRow;
   constexpr int RPL = KvTraits<KV>::kRowsPerLoad;
   constexpr int CH = CL * RPL;
-  constexpr bool kDotK = KV != kKvInt8;  // scores from packed bf16 dot products
+  constexpr bool kDotK = QRows<KV, RG, QS>::kDot;  // scores from packed bf16 dot products
   constexpr bool kDotV = KV == kKvFp8;   // values through packed f16 dot products over token pairs
   static_assert(!kDotV || CL % 2 == 0, "token pairs need an even number of loads per chunk");
   const int tb = kk * CH + slot;
@@ -187,6 +189,17 @@ __device__ __forceinline__ void compute_chunk(const ChunkRegs<CL>& c, int kk, in
         for (int j = 0; j < 4; ++j) {
           kp[2 * j] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[j], 1.0f, false);
           kp[2 * j + 1] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[j], 1.0f, true);
+        }
+      } else if constexpr (KV == kKvInt8) {
+        // int8 -> f32 (exact), then the high halves of two f32 values form one bf16 pair (exact: |code| <= 128
+        // needs 8 significant bits).
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float f[4];
+#pragma unroll
+          for (int b = 0; b < 4; ++b) f[b] = (float)(int8_t)((w[j] >> (8 * b)) & 0xffu);
+          kp[2 * j] = __builtin_bit_cast(bf16x2, __builtin_amdgcn_perm(__float_as_uint(f[1]), __float_as_uint(f[0]), 0x07060302u));
+          kp[2 * j + 1] = __builtin_bit_cast(bf16x2, __builtin_amdgcn_perm(__float_as_uint(f[3]), __float_as_uint(f[2]), 0x07060302u));
         }
       } else {
 #pragma unroll
@@ -388,7 +401,9 @@ __device__ __forceinline__ void load_q_rows(const DecodeParams& p, QRows<KV, RG,
 }
 
 template <int KV, int SK, int RG, bool PU, bool QS>
-__global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(const DecodeParams p) {
+__global__ __launch_bounds__(kDecodeWaves * 64,
+                             decode_groups_per_cu(KV == kKvInt8, RG, PU, QS) == kDecodeGroupsPerCuInt8 ? 3 : 1)
+void decode_kernel(const DecodeParams p) {
   constexpr int NW = kDecodeWaves;
   constexpr int NT = NW * 64;
   constexpr int D = kHeadDim;
@@ -589,16 +604,17 @@ template <int KV, int SK, int RG>
 static hipError_t launch_t(const DecodeParams& p, bool page_uniform, hipStream_t stream, const LaunchEvents& ev) {
   dim3 grid(p.grid), block(kDecodeWaves * 64);
   const size_t lds = (size_t)(2 * p.B + 1) * sizeof(int);  // the line's cost prefix sum and the lengths
-  // A non-bf16 q needs the hi + lo split on the dot-product paths; the INT8 path reads q as floats.
-  const bool qs = KV != kKvInt8 && p.q_dtype != kFBf16;
+  // A non-bf16 q needs the hi + lo split on the FP8 / BF16 dot-product paths; INT8 caches take the dot path
+  // with a bf16 q (exact) and otherwise read q as pre-scaled floats.
+  const bool qs = p.q_dtype != kFBf16;
   if (page_uniform && !qs)
     launch_kernel(decode_kernel<KV, SK, RG, true, false>, grid, block, lds, stream, ev, p);
   else if (page_uniform)
-    launch_kernel(decode_kernel<KV, SK, RG, true, KV != kKvInt8>, grid, block, lds, stream, ev, p);
+    launch_kernel(decode_kernel<KV, SK, RG, true, true>, grid, block, lds, stream, ev, p);
   else if (!qs)
     launch_kernel(decode_kernel<KV, SK, RG, false, false>, grid, block, lds, stream, ev, p);
   else
-    launch_kernel(decode_kernel<KV, SK, RG, false, KV != kKvInt8>, grid, block, lds, stream, ev, p);
+    launch_kernel(decode_kernel<KV, SK, RG, false, true>, grid, block, lds, stream, ev, p);
   return hipGetLastError();
 }
 

@@ -88,6 +88,21 @@ def test_plan_auto_launches_two_groups_per_cu_at_most(built_lib):
     assert grid == 8 * -(-64 // chunk_bf16)  # never more groups than chunks that could exist
 
 
+def test_plan_gives_int8_vector_segments_three_groups_per_cu(built_lib):
+    """INT8 on the vector kernel runs three workgroups per CU where its kernels fit 168 VGPRs (one row per
+    group; two rows with whole 8-row loads per page and a bf16 q), two otherwise."""
+    def grid_of(nq=1, hq=16, page=16, q_dtype=torch.bfloat16):
+        q, k, v, table, lens, ks, vs = cpu_case("int8", b=64, nq=nq, hq=hq, nb=8192, page=page, max_blocks=512)
+        return decode_plan(q.to(q_dtype), k, v, table, lens, ks, vs, scale=0.1, max_context=8192)[0]
+
+    assert grid_of() == 768                              # 2 rows, page 16, bf16 q
+    assert grid_of(hq=8) == 768                          # 1 row
+    assert grid_of(hq=8, q_dtype=torch.float32) == 768   # 1 row, f32 q
+    assert grid_of(q_dtype=torch.float32) == 512         # 2 rows, f32 q
+    assert grid_of(page=4) == 512                        # 2 rows, pages smaller than a load
+    assert grid_of(hq=32) == 512                         # 4 rows
+
+
 @pytest.mark.parametrize("max_context", [0, 1, 100, 4096, 32768])
 def test_plan_workspace_grows_with_the_launch(built_lib, max_context):
     q, k, v, table, lens, ks, vs = cpu_case(b=32, max_blocks=4096, nb=8192)

@@ -385,3 +385,19 @@ def test_float32_output_is_float32_accurate(fmt, scales, nq, hq, hkv):
         got, want = run_case(c, out_dtype=torch.float32, num_splits=splits)
         err = np.abs(got.cpu().numpy() - want).max()
         assert err <= 1e-4 * np.abs(want).max(), f"{fmt} {scales} Q={nq} Hq={hq}: {err:.3e} vs max {np.abs(want).max():.3e}"
+
+
+@pytest.mark.parametrize("fmt,scales", [("fp8", "head"), ("int8", "token")])
+@pytest.mark.parametrize("lengths", [[0, 700, 0, 0, 1500, 33, 0], [2048] * 3 + [0], [1, 0, 5, 31, 32, 33, 0]])
+def test_many_row_segments_head_major_walk(fmt, scales, lengths):
+    """Many-row segments (here 10 and 12 rows) lie head-major on the stream-K line: a workgroup's range runs
+    over the sequences of one KV head, then wraps to the next head's first sequence holding tokens. Empty
+    sequences at the start, the end and in between, and ranges that wrap, must all be walked exactly."""
+    for nq, hq in ((5, 16), (3, 32)):
+        c = make_case(fmt, lengths, nq=nq, hq=hq, hkv=8, scales=scales)
+        for splits in (None, 3):
+            got, want = run_case(c, num_splits=splits)
+            check(got, want, f"{fmt} Q={nq} Hq={hq} {lengths} splits={splits}")
+            for i, t in enumerate(lengths):
+                if t == 0:
+                    assert got[i].float().abs().sum().item() == 0
