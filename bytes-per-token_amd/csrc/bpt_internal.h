@@ -63,6 +63,16 @@ constexpr int decode_groups_per_cu(bool int8, int rows_per_group, bool page_unif
   return int8 && (rows_per_group == 1 || (rows_per_group == 2 && page_uniform && !q_split)) ? kDecodeGroupsPerCuInt8
                                                                                             : kDecodeGroupsPerCu;
 }
+// Fewest chunks the auto plan gives a workgroup (it launches fewer workgroups for small batches rather than
+// thinner ones): many-row matrix-core segments kDecodeMinChunksManyRows, other matrix-core segments one per
+// wave, INT8 on the vector kernel two per wave, everything else one. Measured on one sequence of the
+// 1.7B shape: FP8 (2 rows, 2943 tokens) 15.7 -> 13.0 us, INT8 (8192 tokens) 26.2 -> 19.3 us; BF16's
+// 16-token chunks are best one per workgroup (the 512-token BF16 call: 10.9 us, 11.4 with four).
+constexpr int kDecodeMinChunksMfma = 4;
+constexpr int kDecodeMinChunksInt8 = 8;
+constexpr int decode_min_chunks(bool mfma, int rows, bool int8) {
+  return mfma ? (rows >= kManyRows ? kDecodeMinChunksManyRows : kDecodeMinChunksMfma) : (int8 ? kDecodeMinChunksInt8 : 1);
+}
 // Waves per matrix-core workgroup for segments of `rows` rows, and workgroups per CU.
 constexpr int mfma_waves(int rows) { return rows >= kManyRows ? kMfmaManyRowWaves : kDecodeWaves; }
 constexpr int mfma_groups_per_cu(int rows) { return rows >= kManyRows ? 1 : kDecodeGroupsPerCu; }

@@ -101,6 +101,8 @@ def test_plan_gives_int8_vector_segments_three_groups_per_cu(built_lib):
     assert grid_of(q_dtype=torch.float32) == 512         # 2 rows, f32 q
     assert grid_of(page=4) == 512                        # 2 rows, pages smaller than a load
     assert grid_of(hq=32) == 512                         # 4 rows
+    q, k, v, table, lens, ks, vs = cpu_case("int8", b=1, nb=8192, max_blocks=512)
+    assert decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=8192)[0] == 8 * 256 // 8  # 2 per wave
 
 
 @pytest.mark.parametrize("max_context", [0, 1, 100, 4096, 32768])
@@ -134,13 +136,13 @@ def test_plan_gives_many_row_segments_fuller_workgroups(built_lib):
     grid, chunk, ws, _ = decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=3072)
     assert chunk == 32 and grid == 2 * 8 * 96 // 8 and ws == expected_workspace(2, 8, 16, grid)
     # ... a full batch fills every CU with one 8-wave workgroup, and 2 rows per KV head keep two 4-wave
-    # workgroups per CU and one chunk per workgroup as the floor.
+    # workgroups per CU and one chunk per wave (4 per workgroup) as the floor.
     q, k, v, table, lens, ks, vs = cpu_case("fp8", b=16, nq=5, max_blocks=256, nb=8192)
     assert decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=3072)[0] == 256
     q, k, v, table, lens, ks, vs = cpu_case("fp8", b=16, max_blocks=256, nb=8192)
     assert decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=3072)[0] == 512
     q, k, v, table, lens, ks, vs = cpu_case("fp8", b=1, max_blocks=64, nb=64)
-    assert decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=1024)[0] == 8 * 32
+    assert decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=1024)[0] == 8 * 32 // 4
     q, k, v, table, lens, ks, vs = cpu_case("fp8", b=1, nq=5, max_blocks=64, nb=64)
     assert decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=1024)[0] == 8 * 32 // 8
 
