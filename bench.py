@@ -296,6 +296,49 @@ def measure_kivi(flush, iters: int, warmup: int) -> dict:
     return table
 
 
+def measure_kivi_quantize(flush, iters: int, warmup: int) -> dict:
+    """The KIVI write path (kivi.quantize_kv_into -> bpt_kivi_quantize) at the kernel-2 benchmark's cache
+    shapes: one 32-token key group of new bf16 keys and values per sequence and KV head quantized into the
+    cache (what QuantizedKVCache._append does once every 32 decode steps), and the whole context at once (a
+    prefill). GB/s counts the bf16 read plus the codes and grids written."""
+    import ctypes
+
+    import torch
+
+    from bpt_amd import _lib, kivi, workloads
+
+    table = {}
+    for batch, context in ((1, 32768), (64, 8192)):
+        for bits in (4, 8):
+            cache = workloads.make_kivi(batch, context, bits, device="cuda:0", seed=batch + context)
+            for tokens in (32, context):
+                gen = torch.Generator(device="cuda:0").manual_seed(tokens)
+                k = torch.randn((batch, 8, tokens, workloads.HEAD_DIM), generator=gen, device="cuda:0").to(torch.bfloat16)
+                v = torch.randn_like(k)
+                args = kivi.quantize_args(k, v, cache, context - tokens)
+                stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+                def call():  # the launch alone: the checks in quantize_kv_into cost tens of microseconds of host time
+                    _lib.check(_lib.lib().bpt_kivi_quantize(ctypes.byref(args), stream))
+
+                total, _ = timed_calls(call, flush, iters, warmup)
+                ms = statistics.fmean(total)
+                d = workloads.HEAD_DIM
+                moved = batch * 8 * tokens * (2 * d * 2 + 2 * d * bits // 8) + batch * 8 * (tokens // 32) * d * 4 \
+                    + batch * 8 * tokens * 4  # bf16 in; codes; key grids (scale + zero per channel per group); value grids
+                name = f"kivi-quantize-int{bits}-{batch}x{tokens}"
+                table[name] = {
+                    "us_per_call": round(ms * 1e3, 2),
+                    "gbps": round(moved / (ms * 1e-3) / 1e9, 1),
+                    "bytes_moved": moved,
+                }
+                log(f"{name}: {table[name]['us_per_call']} us, {table[name]['gbps']} GB/s")
+                del k, v
+            del cache
+            torch.cuda.empty_cache()
+    return table
+
+
 def measure_norm_quant(flush, iters: int, warmup: int) -> dict:
     """RMSNorm + per-token INT8 at the shapes of fastserve's kernel-1 benchmark (bf16, d = 1024 / 2048,
     1 .. 32768 rows): cold µs/call and GB/s of the bytes it must move (2d read + d + 4 written per row),
@@ -540,6 +583,7 @@ def main() -> int:
         result["configs"] = table
     if not args.no_kivi:
         result["kivi"] = measure_kivi(flush, iters=20, warmup=5)
+        result["kivi_quantize"] = measure_kivi_quantize(flush, iters=20, warmup=5)
     if not args.no_norm:
         result["norm_quant"] = measure_norm_quant(flush, iters=20, warmup=5)
     if not args.no_cpu_baseline:

@@ -112,6 +112,21 @@ def quantize_kv_into(k: torch.Tensor, v: torch.Tensor, kv: Any, start: int) -> N
         kv.k_codes[:, :, start:start + n].copy_(k)
         kv.v_codes[:, :, start:start + n].copy_(v)
         return
+    a = quantize_args(k, v, kv, start)
+    stream = torch.cuda.current_stream(k.device).cuda_stream
+    _lib.check(_lib.lib().bpt_kivi_quantize(ctypes.byref(a), ctypes.c_void_p(stream)))
+
+
+def quantize_args(k: torch.Tensor, v: torch.Tensor, kv: Any, start: int) -> Any:
+    """The checked bpt_kivi_quantize arguments that quantize_kv_into launches with (bits 4 / 8 caches), for a
+    caller that launches the same write again without the Python checks (a timing loop, a captured graph).
+    The struct holds raw pointers: the tensors must stay alive and in place while it is used."""
+    b, h, n, d = k.shape
+    _require(tuple(v.shape) == (b, h, n, d) and v.dtype == k.dtype and v.stride() == k.stride(),
+             "k and v must be [B, Hkv, n, D] with one dtype and layout")
+    _require(kv.k_codes.shape[0] == b and kv.k_codes.shape[1] == h, "the cache's batch and KV heads must match")
+    _require(start >= 0 and start % kv.group == 0 and start + n <= kv.k_codes.shape[2],
+             f"tokens {start} .. {start + n} must start on a key group and fit the cache")
     _require(kv.bits in (4, 8), f"bits must be 4, 8 or 16, got {kv.bits}")
     _require(n % kv.group == 0, f"{n} tokens are not a whole number of groups of {kv.group}")
     _require(k.dtype in _Q_CODES and k.stride(-1) == 1, "k and v must be bf16, f16 or f32 with contiguous channels")
@@ -141,8 +156,7 @@ def quantize_kv_into(k: torch.Tensor, v: torch.Tensor, kv: Any, start: int) -> N
     a.kgrid_stride_b, a.kgrid_stride_h, a.kgrid_stride_g = ks.stride(0), ks.stride(1), ks.stride(2)
     a.v_scale, a.v_zero = vs.data_ptr(), vz.data_ptr()
     a.vgrid_stride_b, a.vgrid_stride_h = vs.stride(0), vs.stride(1)
-    stream = torch.cuda.current_stream(dev).cuda_stream
-    _lib.check(_lib.lib().bpt_kivi_quantize(ctypes.byref(a), ctypes.c_void_p(stream)))
+    return a
 
 
 def default_split(batch: int, kv_heads: int, tokens: int, group: int = 32, max_programs: int = 16384) -> int:

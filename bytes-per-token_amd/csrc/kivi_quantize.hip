@@ -9,10 +9,17 @@
 // float32 and rounding is half to even, so codes and grids are bit-exact with the reference formulas. 4-bit
 // codes pair channel d (low nibble) with d + D/2 (high nibble).
 //
-// One wave per (sequence, KV head, key group): lane l owns channels l, l + 64, ... (D a power of two up to 256);
-// the key grids are column reductions over the group's tokens within each lane, the value grids wave
-// reductions over each token's channels. Roofline: HBM, 2 * D * esize bytes read and 2 * D * bits / 8 + 4 *
-// (D / group + 1) written per token, a launch-bound kernel at decode sizes.
+// Two kernels, one wave per (sequence, KV head, key group) in both:
+// * kivi_quantize_rows_kernel, for key groups of 32 tokens whose rows start on 16 bytes and span 32 .. 512
+//   bytes (bf16 / f16 D = 16 .. 256, f32 D = 8 .. 128): lane l reads 16-byte pieces, E = 16 / esize channels
+//   (l % L) E .. + E - 1 of tokens l / L + R k (L = D / E lanes per row, R = 64 / L rows per wave-wide load,
+//   k < 32 / R), every key and value piece of the group requested before any arithmetic. Key grids: min / max
+//   over the lane's tokens, then across the R lanes holding the same channels; value grids: over the lane's E
+//   channels, then across the row's L lanes. Codes leave as E bytes per lane (4-bit: the lane holding
+//   channels c .. c + E - 1 takes its partner's codes for c + D / 2 .. with one shuffle and stores the pairs).
+// * kivi_quantize_kernel, any other group, head dim or alignment: lane l owns channels l, l + 64, ... and
+//   walks the group's tokens one row at a time (2- or 4-byte loads and byte stores).
+// Roofline: HBM, 2 * D * esize bytes read and 2 * D * bits / 8 + 4 * (D / group + 1) written per token.
 #include "bpt_device.h"
 #include "bpt_internal.h"
 
@@ -153,10 +160,263 @@ __global__ __launch_bounds__(kQuantWaves * 64) void kivi_quantize_kernel(const K
   }
 }
 
+// ---- rows kernel: 32-token key groups, 16-byte rows ------------------------------------------------------
+
+constexpr int kRowsGroup = 32;
+
+template <int SRC>
+constexpr int src_bytes() {
+  return SRC == kFF32 ? 4 : 2;
+}
+
+// 16 bytes of source elements -> E floats, in channel order.
+template <int SRC, int E>
+__device__ __forceinline__ void unpack16(const U4& u, float (&x)[E]) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if constexpr (SRC == kFF32) {
+      x[i] = __uint_as_float(w[i]);
+    } else if constexpr (SRC == kFBf16) {
+      x[2 * i] = __uint_as_float(w[i] << 16);
+      x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    } else {
+      x[2 * i] = (float)__builtin_bit_cast(_Float16, (uint16_t)w[i]);
+      x[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] >> 16));
+    }
+  }
+}
+
+// rint of the IEEE quotient x / s, given inv = v_rcp_f32(s) (s a positive normal float). q = x * inv is within
+// 2^-22 |x / s| of x / s (rcp: 1 ulp, 2^-23 relative; the product: half an ulp) and the IEEE quotient within
+// 2^-24 |x / s|, so both lie strictly on the same side of every half-integer farther than 2^-21 |q| from q,
+// and then round to the same integer. Quotients closer to a half-integer than 2^-20 |q| (a few in ten
+// thousand at most) take the IEEE division; NaN and infinite q keep q, as the division would give.
+__device__ __forceinline__ float rint_quotient(float x, float s, float inv) {
+  const float q = x * inv;
+  float n = rintf(q);
+  if (0.5f - fabsf(q - n) <= fabsf(q) * 0x1p-20f) n = rintf(__fdiv_rn(x, s));
+  return n;
+}
+
+// E codes of one piece (integer-valued floats in [0, qmax], so the byte conversion is exact) -> E bytes.
+// Grid j of the piece's element j is g[j * g_step], with inv[j * g_step] = v_rcp_f32 of its scale.
+template <int E>
+__device__ __forceinline__ void code_bytes(const float (&x)[E], const Grid* g, const float* inv, int g_step,
+                                           float qmax, uint32_t (&w)[E / 4]) {
+#pragma unroll
+  for (int i = 0; i < E / 4; ++i) {
+    uint32_t a = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = (4 * i + j) * g_step;
+      const float n = rint_quotient(x[4 * i + j], g[e].scale, inv[e]);
+      a = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_amdgcn_fmed3f(n + g[e].zero, 0.0f, qmax), j, a);
+    }
+    w[i] = a;
+  }
+}
+
+// Min and max over aligned groups of N lanes (N a power of two up to 64), every lane left holding them:
+// DPP inside rows of 16, shuffles across rows.
+template <int N>
+__device__ __forceinline__ void group_min_max(float& mn, float& mx) {
+  if constexpr (N >= 2) {
+    mn = fminf(mn, dpp_mov<kDppXor1>(mn));
+    mx = fmaxf(mx, dpp_mov<kDppXor1>(mx));
+  }
+  if constexpr (N >= 4) {
+    mn = fminf(mn, dpp_mov<kDppXor2>(mn));
+    mx = fmaxf(mx, dpp_mov<kDppXor2>(mx));
+  }
+  if constexpr (N >= 8) {
+    mn = fminf(mn, dpp_mov<kDppHalfMirror>(mn));
+    mx = fmaxf(mx, dpp_mov<kDppHalfMirror>(mx));
+  }
+  if constexpr (N >= 16) {
+    mn = fminf(mn, dpp_mov<kDppRowMirror>(mn));
+    mx = fmaxf(mx, dpp_mov<kDppRowMirror>(mx));
+  }
+#pragma unroll
+  for (int m = 16; m < N; m <<= 1) {
+    mn = fminf(mn, shfl_xor_f(mn, m));
+    mx = fmaxf(mx, shfl_xor_f(mx, m));
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void store_words(void* dst, const uint32_t (&w)[N]) {
+  if constexpr (N == 1) {
+    *(uint32_t*)dst = w[0];
+  } else if constexpr (N == 2) {
+    *(uint2*)dst = make_uint2(w[0], w[1]);
+  } else {
+    static_assert(N == 4, "1, 2 or 4 words");
+    *(uint4*)dst = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// One piece's codes to its row: 8 bits as they are; 4 bits paired with the partner lane L / 2 away, which
+// holds the channels D / 2 higher, and stored by the lower lane (byte c = channel c | channel c + D / 2 << 4).
+template <int BITS, int L, int NW>
+__device__ __forceinline__ void store_piece(uint8_t* dst, uint32_t (&w)[NW], int cp) {
+  if constexpr (BITS == 4) {
+#pragma unroll
+    for (int i = 0; i < NW; ++i) w[i] |= (uint32_t)__shfl_xor((int)w[i], L / 2, 64) << 4;
+    if (cp < L / 2) store_words(dst, w);
+  } else {
+    store_words(dst, w);
+  }
+}
+
+template <int BITS, int SRC, int D>
+__global__ __launch_bounds__(kQuantWaves * 64) void kivi_quantize_rows_kernel(const KiviQuantParams p) {
+  constexpr int ES = src_bytes<SRC>();
+  constexpr int E = 16 / ES;
+  constexpr int L = D / E;
+  constexpr int R = 64 / L;
+  constexpr int NV = kRowsGroup / R;
+  constexpr float kQmax = BITS == 4 ? 15.0f : 255.0f;
+  static_assert(L >= 2 && L <= 32 && NV * R == kRowsGroup, "rows of 32 .. 512 bytes");
+  const int lane = threadIdx.x & 63;
+  const int64_t item = (int64_t)blockIdx.x * kQuantWaves + (threadIdx.x >> 6);  // (b, h, key group)
+  const int groups = p.T / kRowsGroup;
+  if (item >= (int64_t)p.B * p.Hkv * groups) return;
+  const int g = (int)(item % groups);
+  const int bh = (int)(item / groups);
+  const int h = bh % p.Hkv, b = bh / p.Hkv;
+  const int cp = lane % L, r0 = lane / L;
+  const int t = g * kRowsGroup + r0;  // this lane's first token; then every R-th
+  const int64_t src = ((int64_t)b * p.x_sb + (int64_t)h * p.x_sh + (int64_t)t * p.x_st) * ES + cp * 16;
+  const int64_t src_step = (int64_t)R * p.x_st * ES;
+  U4 kr[NV], vr[NV];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) kr[k] = load16((const uint8_t*)p.k + src + k * src_step);
+#pragma unroll
+  for (int k = 0; k < NV; ++k) vr[k] = load16((const uint8_t*)p.v + src + k * src_step);
+  const int64_t code = (int64_t)b * p.c_sb + (int64_t)h * p.c_sh + (int64_t)t * p.c_st + cp * E;
+  const int64_t code_step = (int64_t)R * p.c_st;
+
+  // ---- keys: per channel over the group's 32 tokens ----------------------------------------------------
+  {
+    float mn[E], mx[E];
+    {
+      float x[E];
+      unpack16<SRC>(kr[0], x);
+#pragma unroll
+      for (int e = 0; e < E; ++e) mn[e] = mx[e] = x[e];
+    }
+#pragma unroll
+    for (int k = 1; k < NV; ++k) {
+      float x[E];
+      unpack16<SRC>(kr[k], x);
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        mn[e] = fminf(mn[e], x[e]);
+        mx[e] = fmaxf(mx[e], x[e]);
+      }
+    }
+#pragma unroll
+    for (int m = L; m < 64; m <<= 1) {
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        mn[e] = fminf(mn[e], shfl_xor_f(mn[e], m));
+        mx[e] = fmaxf(mx[e], shfl_xor_f(mx[e], m));
+      }
+    }
+    Grid gr[E];
+    float inv[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      gr[e] = make_grid(mn[e], mx[e], kQmax);
+      inv[e] = __builtin_amdgcn_rcpf(gr[e].scale);
+    }
+    if (r0 == 0) {
+      uint32_t sw[E / 2], zw[E / 2];
+#pragma unroll
+      for (int i = 0; i < E / 2; ++i) {
+        sw[i] = f16_bits(gr[2 * i].scale) | (uint32_t)f16_bits(gr[2 * i + 1].scale) << 16;
+        zw[i] = f16_bits(gr[2 * i].zero) | (uint32_t)f16_bits(gr[2 * i + 1].zero) << 16;
+      }
+      const int64_t go = (int64_t)b * p.g_sb + (int64_t)h * p.g_sh + (int64_t)g * p.g_sg + cp * E;
+      store_words(p.ks + go, sw);
+      store_words(p.kz + go, zw);
+    }
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      float x[E];
+      unpack16<SRC>(kr[k], x);
+      uint32_t w[E / 4];
+      code_bytes(x, gr, inv, 1, kQmax, w);
+      store_piece<BITS, L>(p.kc + code + k * code_step, w, cp);
+    }
+  }
+
+  // ---- values: per token over its D channels ------------------------------------------------------------
+  const int64_t vo = (int64_t)b * p.t_sb + (int64_t)h * p.t_sh + t;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    float x[E];
+    unpack16<SRC>(vr[k], x);
+    float mn = x[0], mx = x[0];
+#pragma unroll
+    for (int e = 1; e < E; ++e) {
+      mn = fminf(mn, x[e]);
+      mx = fmaxf(mx, x[e]);
+    }
+    group_min_max<L>(mn, mx);
+    const Grid gr = make_grid(mn, mx, kQmax);
+    const float inv = __builtin_amdgcn_rcpf(gr.scale);
+    if (cp == 0) {
+      p.vs[vo + k * R] = f16_bits(gr.scale);
+      p.vz[vo + k * R] = f16_bits(gr.zero);
+    }
+    uint32_t w[E / 4];
+    code_bytes(x, &gr, &inv, 0, kQmax, w);
+    store_piece<BITS, L>(p.vc + code + k * code_step, w, cp);
+  }
+}
+
+// The rows kernel's layout conditions: 32-token groups; rows of 32 .. 512 bytes; sources, codes (E bytes per
+// lane) and key grids (E halves per lane) aligned for the lanes' vector accesses at every (b, h, token).
+static bool rows_kernel_fits(const KiviQuantParams& p) {
+  const int es = p.src_dtype == kFF32 ? 4 : 2;
+  const int e = 16 / es;
+  const int64_t rb = (int64_t)p.D * es;
+  auto al = [](const void* ptr, int n) { return (uintptr_t)ptr % n == 0; };
+  return p.group == kRowsGroup && rb >= 32 && rb <= 512 && al(p.k, 16) && al(p.v, 16) &&
+         (p.x_sb * es) % 16 == 0 && (p.x_sh * es) % 16 == 0 && (p.x_st * es) % 16 == 0 && al(p.kc, e) &&
+         al(p.vc, e) && p.c_sb % e == 0 && p.c_sh % e == 0 && p.c_st % e == 0 && al(p.ks, 2 * e) &&
+         al(p.kz, 2 * e) && p.g_sb % e == 0 && p.g_sh % e == 0 && p.g_sg % e == 0;
+}
+
+template <int BITS, int SRC>
+static hipError_t launch_rows(const KiviQuantParams& p, dim3 grid, dim3 block, hipStream_t stream) {
+  constexpr int ES = src_bytes<SRC>();
+  switch (p.D * ES) {
+    case 32: hipLaunchKernelGGL((kivi_quantize_rows_kernel<BITS, SRC, 32 / ES>), grid, block, 0, stream, p); break;
+    case 64: hipLaunchKernelGGL((kivi_quantize_rows_kernel<BITS, SRC, 64 / ES>), grid, block, 0, stream, p); break;
+    case 128: hipLaunchKernelGGL((kivi_quantize_rows_kernel<BITS, SRC, 128 / ES>), grid, block, 0, stream, p); break;
+    case 256: hipLaunchKernelGGL((kivi_quantize_rows_kernel<BITS, SRC, 256 / ES>), grid, block, 0, stream, p); break;
+    case 512: hipLaunchKernelGGL((kivi_quantize_rows_kernel<BITS, SRC, 512 / ES>), grid, block, 0, stream, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <int BITS>
+static hipError_t launch_rows_bits(const KiviQuantParams& p, dim3 grid, dim3 block, hipStream_t stream) {
+  if (p.src_dtype == kFBf16) return launch_rows<BITS, kFBf16>(p, grid, block, stream);
+  if (p.src_dtype == kFF16) return launch_rows<BITS, kFF16>(p, grid, block, stream);
+  return launch_rows<BITS, kFF32>(p, grid, block, stream);
+}
+
 hipError_t launch_kivi_quantize(const KiviQuantParams& p, hipStream_t stream) {
   const int64_t items = (int64_t)p.B * p.Hkv * (p.T / p.group);
   if (items == 0) return hipSuccess;
   dim3 grid((unsigned)((items + kQuantWaves - 1) / kQuantWaves)), block(kQuantWaves * 64);
+  if (rows_kernel_fits(p))
+    return p.bits == 4 ? launch_rows_bits<4>(p, grid, block, stream) : launch_rows_bits<8>(p, grid, block, stream);
   if (p.bits == 4) hipLaunchKernelGGL(kivi_quantize_kernel<4>, grid, block, 0, stream, p);
   else hipLaunchKernelGGL(kivi_quantize_kernel<8>, grid, block, 0, stream, p);
   return hipGetLastError();

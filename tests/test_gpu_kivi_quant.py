@@ -106,6 +106,83 @@ def test_append_into_a_cache_then_decode(bits):
     np.testing.assert_allclose(got.cpu().numpy(), want, rtol=2e-4, atol=2e-4 * float(np.abs(want).max()))
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+def test_half_way_quotients_round_to_even(bits):
+    """Every x / scale is exactly n + 1/2: ranges [0, qmax / 16] give scale 1/16 and zero point 0, and each
+    other value is (n + 1/2) / 16 (n < 127, so bf16 holds it exactly). Codes must be n rounded half to even,
+    the closed form torch.round gives, for keys (per channel) and values (per token)."""
+    from bpt_amd import kivi
+
+    qmax = (1 << bits) - 1
+    n = (np.arange(32)[:, None] * 3 + np.arange(128)[None, :]) % min(qmax, 127)  # [token, channel]
+    x = (n + 0.5) / 16.0
+    k, v = x.copy(), x.copy()
+    k[5] = qmax / 16.0  # each key channel's range reaches qmax / 16 at token 5
+    v[:, 7] = qmax / 16.0  # each token's value range reaches it at channel 7
+    want = np.where(n % 2 == 0, n, n + 1)
+    for dtype in (torch.float32, torch.bfloat16):
+        kt = torch.from_numpy(np.stack([k, k[::-1]])[None].astype(np.float32)).to(dtype).cuda()
+        vt = torch.from_numpy(np.stack([v, v[::-1]])[None].astype(np.float32)).to(dtype).cuda()
+        got = kivi.quantize_kv(kt, vt, bits)
+        ref = okivi.quantize_kv(kt.float().cpu().numpy(), vt.float().cpu().numpy(), bits)
+        check_quant(got, ref, f"{bits} bits {dtype} half-way")
+        kc, vc = got.k_codes[0, 0].cpu().numpy().astype(np.int64), got.v_codes[0, 0].cpu().numpy().astype(np.int64)
+        if bits == 4:  # byte c = channel c | channel c + 64 << 4
+            kc = np.concatenate([kc & 15, kc >> 4], 1)
+            vc = np.concatenate([vc & 15, vc >> 4], 1)
+        rows = np.arange(32) != 5
+        assert np.array_equal(kc[rows], want[rows]) and (kc[5] == qmax).all()
+        cols = np.arange(128) != 7
+        assert np.array_equal(vc[:, cols], want[:, cols]) and (vc[:, 7] == qmax).all()
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_quotients_within_ulps_of_half_way(bits):
+    """float32 values 0 .. 3 ulps either side of (n + 1/2) * s for a scale s = 41/64 (not a power of two):
+    x / s then rounds to n + 1/2 or to a neighbour depending on the last bits, and x times the correctly
+    rounded 1 / s rounds hundreds of these codes the wrong way. Keys and values, bit-exact with the oracle."""
+    from bpt_amd import kivi
+
+    qmax = (1 << bits) - 1
+    s = 41 / 64
+    t, c = np.meshgrid(np.arange(64), np.arange(128), indexing="ij")
+    n = (t * 7 + c) % qmax
+    x0 = ((n + 0.5) * s).astype(np.float32)
+    x = (x0.view(np.int32) + ((t + 3 * c) % 7 - 3).astype(np.int32)).view(np.float32)
+    k, v = x.copy(), x.copy()
+    k[[5, 40]] = np.float32(qmax * s)  # every key channel's range: [0, qmax s], so its scale is s
+    v[:, 9] = np.float32(qmax * s)  # every token's value range too
+    q = x / np.float32(s)
+    assert (np.abs(q - np.floor(q) - 0.5) < np.abs(q) * 2.0**-20).mean() > 0.5  # most sit in the fallback band
+    assert (np.rint(x * (np.float32(1) / np.float32(s))) != np.rint(q)).sum() > 300
+    kt = torch.from_numpy(np.stack([k, k[::-1]])[None].copy()).cuda()
+    vt = torch.from_numpy(np.stack([v, v[::-1]])[None].copy()).cuda()
+    got = kivi.quantize_kv(kt, vt, bits)
+    ref = okivi.quantize_kv(kt.cpu().numpy(), vt.cpu().numpy(), bits)
+    assert (ref.k_scale == np.float16(s)).all() and (ref.v_scale == np.float16(s)).all()
+    check_quant(got, ref, f"{bits} bits near half-way")
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_unaligned_rows_take_the_general_kernel(bits):
+    """Sources that do not start on 16 bytes (a channel offset of one element, rows of D + 1 elements) and
+    codes at an odd byte offset go through the row-at-a-time kernel; same bit-exact result."""
+    from bpt_amd import kivi
+
+    b, h, n, d = 2, 4, 64, 128
+    for dtype in (torch.bfloat16, torch.float32):
+        k, v, kn, vn = inputs(b, h, n, d + 1, seed=11, dtype=dtype)
+        k, v = k[..., 1:], v[..., 1:]
+        ks = torch.full((b, h, 2, d), 7, dtype=torch.float16, device="cuda")
+        width = d // 2 if bits == 4 else d
+        raw = torch.zeros((2, b, h, n, width + 1), dtype=torch.uint8, device="cuda")
+        cache = kivi.QuantKV(bits, 32, raw[0, ..., 1:], raw[1, ..., 1:], ks, ks.clone(),
+                             torch.zeros((b, h, n), dtype=torch.float16, device="cuda"),
+                             torch.zeros((b, h, n), dtype=torch.float16, device="cuda"))
+        kivi.quantize_kv_into(k, v, cache, 0)
+        check_quant(cache, okivi.quantize_kv(kn[..., 1:], vn[..., 1:], bits), f"{bits} bits {dtype} unaligned")
+
+
 def test_bad_arguments_raise_value_error():
     from bpt_amd import kivi
 
