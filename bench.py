@@ -98,6 +98,21 @@ def profile_pass(args) -> int:
             flush.run()
             rms_norm_int8(x, weight, 1e-6, out=out)
         nbytes = rows * (3 * d + 4)
+    elif args.workload.startswith("kivi-quantize-"):  # kivi-quantize-<int4|int8>-<batch>x<tokens>
+        from bpt_amd import kivi
+
+        fmt, shape = args.workload.split("-")[2:]
+        batch, tokens = (int(x) for x in shape.split("x"))
+        bits = {"int4": 4, "int8": 8}[fmt]
+        cache = workloads.make_kivi(batch, tokens, bits, device="cuda:0", seed=batch + tokens)
+        gen = torch.Generator(device="cuda:0").manual_seed(tokens)
+        k = torch.randn((batch, 8, tokens, workloads.HEAD_DIM), generator=gen, device="cuda:0").to(torch.bfloat16)
+        v = torch.randn_like(k)
+        for _ in range(args.warmup + args.steps):
+            flush.run()
+            kivi.quantize_kv_into(k, v, cache, 0)
+        d = workloads.HEAD_DIM
+        nbytes = batch * 8 * tokens * (2 * d * 2 + 2 * d * bits // 8 + 4) + batch * 8 * (tokens // 32) * d * 4
     elif args.workload.startswith("kivi-"):  # kivi-<int4|int8|bf16>-<batch>x<context>
         from bpt_amd import kivi
 

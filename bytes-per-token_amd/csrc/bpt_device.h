@@ -115,6 +115,19 @@ __device__ __forceinline__ float wave_max(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// rint of the IEEE quotient x / s (torch's round(x / s)), given inv = v_rcp_f32(s), s a positive normal float.
+// q = x * inv is within 2^-22 |x / s| of x / s (rcp: 1 ulp, 2^-23 relative; the product: half an ulp) and the
+// IEEE quotient within 2^-24 |x / s|, so both lie strictly on the same side of every half-integer farther
+// than 2^-21 |q| from q, and then round to the same integer. Quotients closer to a half-integer than
+// 2^-20 |q| (a few in ten thousand of random values) take the IEEE division; NaN and infinite q keep q, as
+// the division would give.
+__device__ __forceinline__ float rint_quotient(float x, float s, float inv) {
+  const float q = x * inv;
+  float n = rintf(q);
+  if (0.5f - fabsf(q - n) <= fabsf(q) * 0x1p-20f) n = rintf(__fdiv_rn(x, s));
+  return n;
+}
+
 // ---- memory ------------------------------------------------------------------------------------------
 
 struct alignas(16) U4 {

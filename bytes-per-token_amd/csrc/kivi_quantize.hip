@@ -187,15 +187,17 @@ __device__ __forceinline__ void unpack16(const U4& u, float (&x)[E]) {
   }
 }
 
-// rint of the IEEE quotient x / s, given inv = v_rcp_f32(s) (s a positive normal float). q = x * inv is within
-// 2^-22 |x / s| of x / s (rcp: 1 ulp, 2^-23 relative; the product: half an ulp) and the IEEE quotient within
-// 2^-24 |x / s|, so both lie strictly on the same side of every half-integer farther than 2^-21 |q| from q,
-// and then round to the same integer. Quotients closer to a half-integer than 2^-20 |q| (a few in ten
-// thousand at most) take the IEEE division; NaN and infinite q keep q, as the division would give.
-__device__ __forceinline__ float rint_quotient(float x, float s, float inv) {
-  const float q = x * inv;
+// rint(x / s) + z with x / s the IEEE quotient (the reference's round(x / scale) + zero), given
+// inv = v_rcp_f32(s) and the integer zero point z. q = fma(x, inv, z) is within 2^-23 |x / s| (rcp: 1 ulp)
+// plus half an ulp of |q| of x / s + z. A scale is the float16 rounding of (hi - lo) / qmax (1 if that is 0),
+// never below 2/3 of it, so |x / s| <= 1.5 qmax and |q| < 1024: q is within 7.7e-5 of x / s + z, and the IEEE
+// quotient within 3.1e-5 of x / s. Farther than 2^-12 from every half-integer, q and the IEEE quotient
+// (shifted by the integer z) lie in the same unit interval around an integer and round to it; nearer (about
+// one value in two thousand), the IEEE division decides. NaN and infinite q keep q, as the division would give.
+__device__ __forceinline__ float rint_code(float x, float s, float inv, float z) {
+  const float q = fmaf(x, inv, z);
   float n = rintf(q);
-  if (0.5f - fabsf(q - n) <= fabsf(q) * 0x1p-20f) n = rintf(__fdiv_rn(x, s));
+  if (fabsf(q - n) >= 0.5f - 0x1p-12f) n = rintf(__fdiv_rn(x, s)) + z;
   return n;
 }
 
@@ -210,8 +212,8 @@ __device__ __forceinline__ void code_bytes(const float (&x)[E], const Grid* g, c
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int e = (4 * i + j) * g_step;
-      const float n = rint_quotient(x[4 * i + j], g[e].scale, inv[e]);
-      a = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_amdgcn_fmed3f(n + g[e].zero, 0.0f, qmax), j, a);
+      const float n = rint_code(x[4 * i + j], g[e].scale, inv[e], g[e].zero);
+      a = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_amdgcn_fmed3f(n, 0.0f, qmax), j, a);
     }
     w[i] = a;
   }
@@ -324,11 +326,29 @@ __global__ __launch_bounds__(kQuantWaves * 64) void kivi_quantize_rows_kernel(co
         mx[e] = fmaxf(mx[e], shfl_xor_f(mx[e], m));
       }
     }
+    // The R lanes of a channel column now hold the same E ranges: lane r0 makes the grids of channels
+    // r0 % RE + RE j only, and every lane takes the E grids from their makers.
+    constexpr int RE = R < E ? R : E;
+    constexpr int KG = E / RE;
+    const int sub = r0 % RE;
+    Grid own[KG];
+#pragma unroll
+    for (int j = 0; j < KG; ++j) {
+      float lo = mn[j * RE], hi = mx[j * RE];
+#pragma unroll
+      for (int u = 1; u < RE; ++u) {
+        lo = sub == u ? mn[j * RE + u] : lo;
+        hi = sub == u ? mx[j * RE + u] : hi;
+      }
+      own[j] = make_grid(lo, hi, kQmax);
+    }
     Grid gr[E];
     float inv[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-      gr[e] = make_grid(mn[e], mx[e], kQmax);
+      const int maker = (e % RE) * L + cp;
+      gr[e].scale = __shfl(own[e / RE].scale, maker, 64);
+      gr[e].zero = __shfl(own[e / RE].zero, maker, 64);
       inv[e] = __builtin_amdgcn_rcpf(gr[e].scale);
     }
     if (r0 == 0) {
@@ -353,7 +373,10 @@ __global__ __launch_bounds__(kQuantWaves * 64) void kivi_quantize_rows_kernel(co
   }
 
   // ---- values: per token over its D channels ------------------------------------------------------------
-  const int64_t vo = (int64_t)b * p.t_sb + (int64_t)h * p.t_sh + t;
+  // Ranges of the lane's NV rows first; the row's L lanes then hold the same NV ranges, and lane cp makes
+  // the grid of row cp % NV only (NV = L / 2: two makers per row), stores it, and every lane takes its NV
+  // rows' grids from their makers.
+  float vmn[NV], vmx[NV];
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     float x[E];
@@ -365,12 +388,35 @@ __global__ __launch_bounds__(kQuantWaves * 64) void kivi_quantize_rows_kernel(co
       mx = fmaxf(mx, x[e]);
     }
     group_min_max<L>(mn, mx);
-    const Grid gr = make_grid(mn, mx, kQmax);
-    const float inv = __builtin_amdgcn_rcpf(gr.scale);
-    if (cp == 0) {
-      p.vs[vo + k * R] = f16_bits(gr.scale);
-      p.vz[vo + k * R] = f16_bits(gr.zero);
+    vmn[k] = mn;
+    vmx[k] = mx;
+  }
+  static_assert(2 * NV == L, "two makers per row");
+  const int vsub = cp % NV;
+  Grid vown;
+  {
+    float lo = vmn[0], hi = vmx[0];
+#pragma unroll
+    for (int u = 1; u < NV; ++u) {
+      lo = vsub == u ? vmn[u] : lo;
+      hi = vsub == u ? vmx[u] : hi;
     }
+    vown = make_grid(lo, hi, kQmax);
+  }
+  if (cp < NV) {
+    const int64_t vo = (int64_t)b * p.t_sb + (int64_t)h * p.t_sh + t + (int64_t)cp * R;
+    p.vs[vo] = f16_bits(vown.scale);
+    p.vz[vo] = f16_bits(vown.zero);
+  }
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int maker = r0 * L + k;
+    Grid gr;
+    gr.scale = __shfl(vown.scale, maker, 64);
+    gr.zero = __shfl(vown.zero, maker, 64);
+    const float inv = __builtin_amdgcn_rcpf(gr.scale);
+    float x[E];
+    unpack16<SRC>(vr[k], x);
     uint32_t w[E / 4];
     code_bytes(x, &gr, &inv, 0, kQmax, w);
     store_piece<BITS, L>(p.vc + code + k * code_step, w, cp);

@@ -51,13 +51,14 @@ __device__ __forceinline__ void load_vec(const void* base, int64_t idx, int dtyp
   }
 }
 
-// Codes of VEC elements of one row, written at element e.
+// Codes of VEC elements of one row, written at element e; inv = v_rcp_f32(scale).
 template <int VEC>
-__device__ __forceinline__ void store_codes(int8_t* row, int e, int d, const float (&y)[VEC], float scale) {
+__device__ __forceinline__ void store_codes(int8_t* row, int e, int d, const float (&y)[VEC], float scale,
+                                            float inv) {
   uint32_t c[VEC];
 #pragma unroll
   for (int j = 0; j < VEC; ++j) {
-    float q = rintf(__fdiv_rn(y[j], scale));  // IEEE division, as torch's y / scale
+    float q = rint_quotient(y[j], scale, inv);  // rint of the IEEE quotient, as torch's round(y / scale)
     q = q > 127.0f ? 127.0f : (q < -128.0f ? -128.0f : q);
     c[j] = (uint32_t)(int)q & 0xffu;
   }
@@ -114,10 +115,11 @@ __global__ __launch_bounds__(kRowsPerGroup * 64) void rms_norm_int8_kernel(const
     }
     amax = wave_max(amax);
     const float scale = fmaxf(__fdiv_rn(amax, 127.0f), 1e-12f);
+    const float inv = __builtin_amdgcn_rcpf(scale);
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
       const int e = it * STEP + lane * VEC;
-      if (VEC == 1 || e < d) store_codes<VEC>(crow, e, d, v[it], scale);
+      if (VEC == 1 || e < d) store_codes<VEC>(crow, e, d, v[it], scale, inv);
     }
     if (lane == 0) p.scale[row] = scale;
   } else {
@@ -140,13 +142,14 @@ __global__ __launch_bounds__(kRowsPerGroup * 64) void rms_norm_int8_kernel(const
     }
     amax = wave_max(amax);
     const float scale = fmaxf(__fdiv_rn(amax, 127.0f), 1e-12f);
+    const float inv = __builtin_amdgcn_rcpf(scale);
     for (int e = lane * VEC; e < d; e += STEP) {
       float v[VEC], w[VEC];
       load_vec<VEC>(p.x, xr + e, p.x_dtype, e, d, v);
       load_vec<VEC>(p.w, e, p.w_dtype, e, d, w);
 #pragma unroll
       for (int j = 0; j < VEC; ++j) v[j] = (v[j] * r) * w[j];
-      store_codes<VEC>(crow, e, d, v, scale);
+      store_codes<VEC>(crow, e, d, v, scale, inv);
     }
     if (lane == 0) p.scale[row] = scale;
   }
