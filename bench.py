@@ -354,6 +354,66 @@ def measure_kivi_quantize(flush, iters: int, warmup: int) -> dict:
     return table
 
 
+def measure_decode_step(iters: int, warmup: int, layers: int = 28) -> dict:
+    """One decode step of a 28-layer Qwen3-1.7B through the paged cache object (engine/kv_cache.py's role):
+    `PagedQuantKVCache.prepare` from device positions (block tables, write slots and lengths built on the
+    device), then per layer `attend` = the new token's quantize-on-write plus the decode call. FP8 codes with
+    per-head scales and the headline workload's 32 ragged lengths; the pools hold random codes (the step reads
+    them, not their values). Timed eager (host-bound: 57 launches from Python) and replayed from a HIP graph;
+    GB/s counts the KV bytes the step's decode calls read. The step's 4.8 GB exceeds every cache, so no
+    flush is needed between steps."""
+    import torch
+
+    from bpt_amd import measure, workloads
+    from bpt_amd.kv_cache import PagedQuantKVCache
+
+    lens = workloads.make("qwen3-1.7b-fp8", device="cuda:0", seed=0).context_lens.cpu().tolist()
+    torch.cuda.empty_cache()
+    b, hq, hkv, d, page = len(lens), 16, 8, workloads.HEAD_DIM, 16
+    gen = torch.Generator(device="cuda:0").manual_seed(3)
+    scales = [torch.rand((layers, hkv), generator=gen, device="cuda:0").cpu() * 4 / 448 + 1 / 448 for _ in range(2)]
+    cache = PagedQuantKVCache(num_layers=layers, num_kv_heads=hkv, head_dim=d, block_size=page,
+                              num_blocks=sum(-(-n // page) for n in lens) + 8, kv_dtype=torch.float8_e4m3fn,
+                              device="cuda:0", k_scale=scales[0], v_scale=scales[1], max_seqs=b)
+    rows = list(range(b))
+    for r, n in zip(rows, lens):
+        cache.reserve(r, n)
+    for pool in cache.k + cache.v:  # finite e4m3fn codes: 0x00 .. 0x7e with either sign
+        codes = torch.randint(0, 0x7F, pool.shape, generator=gen, device="cuda:0", dtype=torch.uint8)
+        codes |= torch.randint(0, 2, pool.shape, generator=gen, device="cuda:0", dtype=torch.uint8) << 7
+        pool.view(torch.uint8).copy_(codes)
+        del codes
+    positions = torch.tensor([[n - 1] for n in lens], dtype=torch.int64, device="cuda:0")
+    q = torch.randn((b, hq, 1, d), generator=gen, device="cuda:0").to(torch.bfloat16)
+    k = torch.randn((b, hkv, 1, d), generator=gen, device="cuda:0").to(torch.bfloat16)
+    v = torch.randn((b, hkv, 1, d), generator=gen, device="cuda:0").to(torch.bfloat16)
+
+    def step():
+        meta = cache.prepare(rows, positions)
+        for layer in range(layers):
+            cache.attend(layer, q, k, v, meta, scale=d**-0.5)
+
+    eager = measure.event_times_ms(step, warmup=warmup, iters=iters)
+    graph = measure.graph_time_ms(step, calls=4, warmup=2, iters=iters)
+    kv = layers * sum(lens) * hkv * d * 2
+    us_eager, us_graph = statistics.median(eager) * 1e3, statistics.median(graph) * 1e3
+    row = {
+        "layers": layers,
+        "batch": b,
+        "kv_format": "fp8 e4m3fn, per-head scales",
+        "kv_bytes_per_step": kv,
+        "us_per_step_eager": round(us_eager, 1),
+        "us_per_step_graph": round(us_graph, 1),
+        "gbps_graph": round(kv / (us_graph * 1e-6) / 1e9, 1),
+        "launches_per_step": 1 + 2 * layers,
+    }
+    log(f"decode-step {layers} layers: {row['us_per_step_eager']} us eager, {row['us_per_step_graph']} us in a graph, "
+        f"{row['gbps_graph']} GB/s")
+    del cache
+    torch.cuda.empty_cache()
+    return row
+
+
 def measure_norm_quant(flush, iters: int, warmup: int) -> dict:
     """RMSNorm + per-token INT8 at the shapes of fastserve's kernel-1 benchmark (bf16, d = 1024 / 2048,
     1 .. 32768 rows): cold µs/call and GB/s of the bytes it must move (2d read + d + 4 written per row),
@@ -481,6 +541,7 @@ def main() -> int:
     ap.add_argument("--no-configs", action="store_true", help="skip the five-shape table")
     ap.add_argument("--no-kivi", action="store_true", help="skip the KIVI (contiguous 4/8/16-bit cache) table")
     ap.add_argument("--no-norm", action="store_true", help="skip the RMSNorm + INT8 table")
+    ap.add_argument("--no-step", action="store_true", help="skip the 28-layer decode step through the paged cache")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--profile", action="store_true", help="short run for rocprofv3 (no JSON line)")
@@ -599,6 +660,8 @@ def main() -> int:
     if not args.no_kivi:
         result["kivi"] = measure_kivi(flush, iters=20, warmup=5)
         result["kivi_quantize"] = measure_kivi_quantize(flush, iters=20, warmup=5)
+    if not args.no_step:
+        result["decode_step"] = measure_decode_step(iters=10, warmup=3)
     if not args.no_norm:
         result["norm_quant"] = measure_norm_quant(flush, iters=20, warmup=5)
     if not args.no_cpu_baseline:
