@@ -248,8 +248,9 @@ def to_oracle(w: Workload) -> dict:
 # ---- KIVI caches (contiguous, fastserve's kernel-2 format) ------------------------------------------------
 
 # The shapes of fastserve's kernel-2 benchmark (experiments/m7.py:210-290, one Qwen3-1.7B attention layer:
-# 16 query / 8 KV heads, head dim 128), as (batch, context).
-KIVI_SHAPES = ((1, 32768), (4, 32768), (16, 2048), (64, 8192))
+# 16 query / 8 KV heads, head dim 128), as (batch, context): every batch of 1, 4, 16, 64 with every context
+# of 512 .. 32768 tokens up to 524288 tokens in all (benchmarks/configs/m7_kernels.yaml:26-31).
+KIVI_SHAPES = tuple((b, t) for b in (1, 4, 16, 64) for t in (512, 2048, 8192, 32768) if b * t <= 524288)
 KIVI_BITS = (4, 8, 16)
 
 

@@ -73,6 +73,15 @@ constexpr int kDecodeMinChunksInt8 = 8;
 constexpr int decode_min_chunks(bool mfma, int rows, bool int8) {
   return mfma ? (rows >= kManyRows ? kDecodeMinChunksManyRows : kDecodeMinChunksMfma) : (int8 ? kDecodeMinChunksInt8 : 1);
 }
+// The KIVI kernel's fewest chunks per workgroup: one per wave while the call's chunks number no more than the
+// largest grid, two per wave beyond. Measured on INT8 caches: 1 x 2048 tokens 21.0 -> 14.0 us and 4 x 512
+// 16.1 -> 13.2 (4 instead of 1); 1 x 8192 22.8 -> 18.5, 4 x 2048 18.2 -> 16.0 and 16 x 512 16.3 -> 15.5 (8
+// instead of 4, which costs 1 us on the 512-chunk shapes); 16 or 32 were no better anywhere.
+constexpr int kKiviMinChunksSmall = 4;
+constexpr int kKiviMinChunks = 8;
+constexpr int64_t kivi_min_chunks(int64_t chunks, int64_t max_grid) {
+  return chunks <= max_grid ? kKiviMinChunksSmall : kKiviMinChunks;
+}
 // Waves per matrix-core workgroup for segments of `rows` rows, and workgroups per CU.
 constexpr int mfma_waves(int rows) { return rows >= kManyRows ? kMfmaManyRowWaves : kDecodeWaves; }
 constexpr int mfma_groups_per_cu(int rows) { return rows >= kManyRows ? 1 : kDecodeGroupsPerCu; }

@@ -211,7 +211,9 @@ int make_kivi_plan(const bpt_kivi_args* a, KiviPlan* pl) {
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: batch x tokens x heads too large", fn);
   int64_t grid = (int64_t)bpt::kComputeUnits * bpt::kDecodeGroupsPerCu;
   const int64_t bound_c = seq_chunks * a->num_kv_heads;
-  if (bound_c < grid) grid = bound_c;
+  const int64_t min_chunks = bpt::kivi_min_chunks(bound_c, grid);
+  const int64_t by_chunks = (bound_c + min_chunks - 1) / min_chunks;
+  if (by_chunks < grid) grid = by_chunks;
   pl->grid = (int)(grid < 1 ? 1 : grid);
   const size_t slots = 2 * (size_t)pl->grid;
   pl->ws_out_floats = slots * pl->G * a->head_dim;

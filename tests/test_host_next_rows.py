@@ -34,11 +34,15 @@ def test_kivi_plan_sizes(built_lib):
     rc, ws, cnt = plan(a)
     assert rc == 0
     grid = a.grid_groups
-    assert grid == 512  # 2 x 8 heads x 128 chunks = 2048 chunks: the full launch of 2 groups per CU
+    assert grid == 256  # 2 x 8 heads x 128 chunks = 2048 chunks, more than one launch of 512: 8 per workgroup
     assert ws == (2 * grid * 2 * (128 + 1) * 4 + 255) // 256 * 256  # two slots per workgroup, 2 rows each
     assert cnt == (2 * 8 * 32 * 4 + 255) // 256 * 256  # one counter per (sequence, KV head, split)
+    big = kivi_args(batch=8, tokens=4096, num_splits=32)
+    assert plan(big)[0] == 0 and big.grid_groups == 512  # 8192 chunks: the full launch of 2 groups per CU
+    mid = kivi_args(batch=1, tokens=2048, num_groups=64, split=128, num_splits=16)
+    assert plan(mid)[0] == 0 and mid.grid_groups == 128  # 512 chunks, no more than one launch: 4 per workgroup
     small = kivi_args(batch=1, tokens=64, num_groups=2, split=64, num_splits=1)
-    assert plan(small)[0] == 0 and small.grid_groups == 8 * 2  # never more workgroups than chunks
+    assert plan(small)[0] == 0 and small.grid_groups == 4  # 16 chunks: one per wave of 4 workgroups
 
 
 def test_kivi_plan_other_head_dims_and_float32_take_the_float32_kernel(built_lib):
