@@ -70,8 +70,16 @@ constexpr int decode_groups_per_cu(bool int8, int rows_per_group, bool page_unif
 // 16-token chunks are best one per workgroup (the 512-token BF16 call: 10.9 us, 11.4 with four).
 constexpr int kDecodeMinChunksMfma = 4;
 constexpr int kDecodeMinChunksInt8 = 8;
-constexpr int decode_min_chunks(bool mfma, int rows, bool int8) {
-  return mfma ? (rows >= kManyRows ? kDecodeMinChunksManyRows : kDecodeMinChunksMfma) : (int8 ? kDecodeMinChunksInt8 : 1);
+// Matrix-core segments of fewer than kManyRows rows take two chunks per wave instead while that still
+// launches at least one workgroup per two CUs: FP8 (2 rows) batches of 2, 3 and 4 sequences 15.2 -> 13.5,
+// 15.4 -> 14.0 and 15.0 -> 14.5 us; one sequence keeps one chunk per wave (12.9 us with 184 workgroups, 13.7
+// with 92), and INT8's vector kernel and many-row segments were slower with twice their minimum.
+constexpr int kDecodeMinChunksMfmaWide = 8;
+constexpr int64_t decode_min_chunks(bool mfma, int rows, bool int8, int64_t chunks) {
+  return mfma ? (rows >= kManyRows ? kDecodeMinChunksManyRows
+                                   : (chunks / kDecodeMinChunksMfmaWide >= kComputeUnits / 2 ? kDecodeMinChunksMfmaWide
+                                                                                             : kDecodeMinChunksMfma))
+              : (int8 ? kDecodeMinChunksInt8 : 1);
 }
 // The KIVI kernel's fewest chunks per workgroup: one per wave while the call's chunks number no more than the
 // largest grid, two per wave beyond. Measured on INT8 caches: 1 x 2048 tokens 21.0 -> 14.0 us and 4 x 512

@@ -126,7 +126,7 @@ int make_plan(const bpt_decode_args* a, Plan* pl) {
   } else {
     pl->per_forced = 0;
     int64_t grid = (int64_t)bpt::kComputeUnits * groups_per_cu;
-    const int64_t min_chunks = bpt::decode_min_chunks(pl->mfma, pl->rows, a->kv_dtype == BPT_KV_INT8);
+    const int64_t min_chunks = bpt::decode_min_chunks(pl->mfma, pl->rows, a->kv_dtype == BPT_KV_INT8, bound_c);
     const int64_t fill = (bound_c + min_chunks - 1) / min_chunks;
     if (fill < grid) grid = fill;
     pl->grid = (int)(grid < 1 ? 1 : grid);

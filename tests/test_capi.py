@@ -143,6 +143,12 @@ def test_plan_gives_many_row_segments_fuller_workgroups(built_lib):
     assert decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=3072)[0] == 512
     q, k, v, table, lens, ks, vs = cpu_case("fp8", b=1, max_blocks=64, nb=64)
     assert decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=1024)[0] == 8 * 32 // 4
+    # Two chunks per wave (8 per workgroup) once that still launches a workgroup per two CUs: 2 x 8 heads x
+    # 128 chunks -> 256 workgroups; one sequence of 2944 tokens (736 chunks) keeps 4 per workgroup (184).
+    q, k, v, table, lens, ks, vs = cpu_case("fp8", b=2, max_blocks=256, nb=8192)
+    assert decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=4096)[0] == 2 * 8 * 128 // 8
+    q, k, v, table, lens, ks, vs = cpu_case("fp8", b=1, max_blocks=256, nb=8192)
+    assert decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=2944)[0] == 8 * 92 // 4
     q, k, v, table, lens, ks, vs = cpu_case("fp8", b=1, nq=5, max_blocks=64, nb=64)
     assert decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=1024)[0] == 8 * 32 // 8
 
