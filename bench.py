@@ -12,8 +12,10 @@ exactly the call's KV bytes (read_floor_us) and a read of exactly the call's pag
 with no attention math (page_read_floor_us); the CPU baseline, the PyTorch float32 restatement of
 fastserve's CPU path (padded gather + attention, torch.set_num_threads) on the host cores over a bounded
 sample of every workload; µs/call + GB/s for all five measured shapes; the KIVI (contiguous 4/8/16-bit
-cache) decode at the shapes of fastserve's kernel-2 benchmark, and the fused RMSNorm + INT8 quantizer at
-the shapes of its kernel-1 benchmark. Prints ONE JSON line.
+cache) decode over fastserve's whole kernel-2 sweep and its quantize-on-write at that benchmark's cache
+shapes; one 28-layer decode step through the paged cache object (device prepare, then write + decode per
+layer), eager and replayed from a graph; and the fused RMSNorm + INT8 quantizer at the shapes of the
+kernel-1 benchmark. Prints ONE JSON line.
 """
 
 from __future__ import annotations
