@@ -5,9 +5,10 @@
 // Per grid (keys: one channel over `group` tokens; values: one token over its D channels):
 //   lo = min(min x, 0), hi = max(max x, 0), scale = f16((hi - lo) / (2^bits - 1)) (1 where that is not > 0),
 //   zero = clamp(round(-lo / scale), 0, 2^bits - 1), code = clamp(round(x / scale) + zero, 0, 2^bits - 1),
-// the scale rounded to float16 before the zero point and codes are computed from it; divisions are IEEE
-// float32 and rounding is half to even, so codes and grids are bit-exact with the reference formulas. 4-bit
-// codes pair channel d (low nibble) with d + D/2 (high nibble).
+// the scale rounded to float16 before the zero point and codes are computed from it; every quotient rounds as
+// IEEE float32 division does (the rows kernel takes x times the scale's reciprocal and divides only where
+// that lands near a half-way point, see rint_code) and rounding is half to even, so codes and grids are
+// bit-exact with the reference formulas. 4-bit codes pair channel d (low nibble) with d + D/2 (high nibble).
 //
 // Two kernels, one wave per (sequence, KV head, key group) in both:
 // * kivi_quantize_rows_kernel, for key groups of 32 tokens whose rows start on 16 bytes and span 32 .. 512
@@ -15,8 +16,9 @@
 //   (l % L) E .. + E - 1 of tokens l / L + R k (L = D / E lanes per row, R = 64 / L rows per wave-wide load,
 //   k < 32 / R), every key and value piece of the group requested before any arithmetic. Key grids: min / max
 //   over the lane's tokens, then across the R lanes holding the same channels; value grids: over the lane's E
-//   channels, then across the row's L lanes. Codes leave as E bytes per lane (4-bit: the lane holding
-//   channels c .. c + E - 1 takes its partner's codes for c + D / 2 .. with one shuffle and stores the pairs).
+//   channels, then across the row's L lanes; each grid is then made by one lane of each share and shuffled to
+//   the others. Codes leave as E bytes per lane in nontemporal stores (4-bit: the lane holding channels
+//   c .. c + E - 1 takes its partner's codes for c + D / 2 .. with one shuffle and stores the pairs).
 // * kivi_quantize_kernel, any other group, head dim or alignment: lane l owns channels l, l + 64, ... and
 //   walks the group's tokens one row at a time (2- or 4-byte loads and byte stores).
 // Roofline: HBM, 2 * D * esize bytes read and 2 * D * bits / 8 + 4 * (D / group + 1) written per token.
