@@ -107,6 +107,36 @@ __device__ __forceinline__ float group_sum(float x) {
 
 __device__ __forceinline__ float shfl_xor_f(float x, int mask) { return __shfl_xor(x, mask, 64); }
 
+// Lane l's value and lane (l ^ 16)'s (XOR16) or (l ^ 32)'s (XOR32), in some order, in every lane: gfx950's
+// v_permlane16_swap / v_permlane32_swap, VALU instructions with no LDS round trip (unlike __shfl_xor's
+// ds_bpermute). Both lanes of a pair get the same two values, so max and sum agree between them.
+template <int XOR>
+__device__ __forceinline__ void lane_pair(float x, float& a, float& b) {
+  static_assert(XOR == 16 || XOR == 32, "rows of 16 or halves of 32");
+  const unsigned u = __float_as_uint(x);
+  if constexpr (XOR == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+  }
+}
+template <int XOR>
+__device__ __forceinline__ float max_xor(float x) {
+  float a, b;
+  lane_pair<XOR>(x, a, b);
+  return fmaxf(a, b);
+}
+template <int XOR>
+__device__ __forceinline__ float sum_xor(float x) {
+  float a, b;
+  lane_pair<XOR>(x, a, b);
+  return a + b;
+}
+
 __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) x = fmaxf(x, shfl_xor_f(x, m));

@@ -241,8 +241,14 @@ __device__ __forceinline__ void fold(const float (&qf)[CPL], const uint32_t (&gs
     x[c] = qf[c] * s;
     mx = fmaxf(mx, fabsf(x[c]));
   }
-#pragma unroll
-  for (int off = 1; off < LPR; off <<= 1) mx = fmaxf(mx, shfl_xor_f(mx, off));
+  // The row's largest |x| over its LPR lanes (an aligned group of 4 .. 32): DPP within rows of 16, then the
+  // row pair through v_permlane16_swap (no LDS round trips on the chunk's path).
+  static_assert(LPR >= 4 && LPR <= 32, "4 .. 32 lanes per fold row");
+  mx = fmaxf(mx, dpp_mov<kDppXor1>(mx));
+  mx = fmaxf(mx, dpp_mov<kDppXor2>(mx));
+  if constexpr (LPR >= 8) mx = fmaxf(mx, dpp_mov<kDppHalfMirror>(mx));
+  if constexpr (LPR >= 16) mx = fmaxf(mx, dpp_mov<kDppRowMirror>(mx));
+  if constexpr (LPR >= 32) mx = max_xor<16>(mx);
   int e = 0;
   if (mx > 0.0f) (void)frexpf(mx, &e);
   e = e < -100 ? -100 : e;
@@ -393,8 +399,7 @@ __device__ __forceinline__ void compute(KChunk<FMT, CPL>& c, int kk, int len, in
 #pragma unroll
   for (int j = 0; j < 8; ++j) mx = fmaxf(mx, sc[j]);
   mx += ev;
-  mx = fmaxf(mx, shfl_xor_f(mx, 16));
-  mx = fmaxf(mx, shfl_xor_f(mx, 32));
+  mx = max_xor<32>(max_xor<16>(mx));
   const bool move = mx > m + kSlack;
   if (__any(move)) {
     const float mn = move ? mx : m;
@@ -711,8 +716,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void kivi_decode_kernel(const
     }
 
     // This wave's state of row n: the four lanes' weight sums added, stored for the workgroup merge.
-    l += shfl_xor_f(l, 16);
-    l += shfl_xor_f(l, 32);
+    l = sum_xor<32>(sum_xor<16>(l));
     if (n < RP) {
       if (kq == 0) {
         s_m[wave][n] = m;

@@ -244,8 +244,7 @@ __device__ __forceinline__ void mfma_compute(MChunk& c, U4 (&sk)[2][16][8], floa
 #pragma unroll
   for (int j = 0; j < 8; ++j)
     mx = fmaxf(mx, SK == kScaleTokenHead ? sc[j] + vscale_bound(vs4[j >> 2][j & 3]) : sc[j]);
-  mx = fmaxf(mx, shfl_xor_f(mx, 16));
-  mx = fmaxf(mx, shfl_xor_f(mx, 32));
+  mx = max_xor<32>(max_xor<16>(mx));
   const bool move = mx > m + kSlack;
   if (__any(move)) {
     const float mn = move ? mx : m;
@@ -495,8 +494,7 @@ __global__ __launch_bounds__(NW * 64, kMfmaWavesPerSimd) void decode_mfma_kernel
     }
 
     // This wave's state of row n: the four lanes' weight sums added, stored for the workgroup merge.
-    l += shfl_xor_f(l, 16);
-    l += shfl_xor_f(l, 32);
+    l = sum_xor<32>(sum_xor<16>(l));
     if (kq == 0) {
       s_m[wave][n] = m;
       s_l[wave][n] = l;
