@@ -123,6 +123,19 @@ int make_plan(const bpt_decode_args* a, Plan* pl) {
     pl->per_forced = per;
     int64_t grid = (bound_c + pl->per_forced - 1) / pl->per_forced;
     pl->grid = (int)(grid < 1 ? 1 : grid);
+  } else if (!pl->mfma && bound_c > 0 &&
+             ((a->kv_dtype == BPT_KV_BF16 && bound_c <= bpt::kAlignedMaxChunksBf16) ||
+              (a->kv_dtype == BPT_KV_INT8 && bound_c <= bpt::kAlignedMaxChunksInt8))) {
+    // Equal partitions of a power-of-two number of chunks, about 4 sqrt(chunks) of them (at most 512).
+    int64_t target = (int64_t)(4.0 * std::sqrt((double)bound_c));
+    target = target < 1 ? 1 : (target > bpt::kAlignedMaxGrid ? bpt::kAlignedMaxGrid : target);
+    int64_t per = 1;
+    while (per * 2 <= bound_c / target) per *= 2;
+    const int64_t parts = (bound_c + per - 1) / per;
+    if (parts > bpt::kAlignedMaxGrid) per *= (parts + bpt::kAlignedMaxGrid - 1) / bpt::kAlignedMaxGrid;
+    pl->per_forced = per;
+    const int64_t grid = (bound_c + per - 1) / per;
+    pl->grid = (int)(grid < 1 ? 1 : grid);
   } else {
     pl->per_forced = 0;
     int64_t grid = (int64_t)bpt::kComputeUnits * groups_per_cu;
