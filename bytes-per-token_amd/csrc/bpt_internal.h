@@ -91,13 +91,15 @@ constexpr int64_t kivi_min_chunks(int64_t chunks, int64_t max_grid) {
   return chunks <= max_grid ? kKiviMinChunksSmall : kKiviMinChunks;
 }
 // Small and mid-size calls on the vector kernel (BF16 caches up to kAlignedMaxChunksBf16 chunks in all, INT8
-// up to kAlignedMaxChunksInt8) are cut into equal partitions of a power-of-two number of chunks per segment,
-// about 4 sqrt(chunks) of them and at most 512, the way a caller's num_splits cuts them: no piece cost, and
-// every KV head of a sequence covers the same tokens at the same time (per-token scale lines, which hold
-// all heads, are read once). Measured against the line cut (auto): BF16 1 x 2048 tokens 17.9 -> 14.6 us,
-// 2 x 512 14.6 -> 12.5, 8 x 8192 55.6 -> 53.2; INT8 1 x 2048 17.9 -> 16.0, 4 x 8192 30.0 -> 27.8,
-// 16 x 2048 29.0 -> 27.8. INT8 at 16 x 8192 and beyond is faster on the line cut with three workgroups per
-// CU (62.6 against 65.4 us).
+// up to kAlignedMaxChunksInt8): when every sequence has the same length (the kernel checks, in LDS, while it
+// builds the segment line), about 4 sqrt(chunks) workgroups (at most 512; the launch holds at least that
+// many) cut equal partitions of a power-of-two number of chunks, the fewest that they cover, as a caller's
+// num_splits would: no piece cost, and every KV head of a sequence covers the same tokens at the same time
+// (per-token scale lines, which hold all heads, are read once). The rest of the launch leaves at once;
+// ragged batches keep the line cut over the whole launch. Measured on equal lengths against the line cut:
+// BF16 1 x 512 tokens 12.9 -> 12.2 us, 1 x 2048 18.0 -> 15.1, 2 x 2048 19.2 -> 17.0; INT8 1 x 2048
+// 17.6 -> 16.3, 4 x 8192 29.6 -> 28.1, 16 x 2048 29.3 -> 28.5; ragged batches within 0.3 us. INT8 at
+// 16 x 8192 and beyond is faster on the line cut with three workgroups per CU (62.6 against 65.4 us).
 constexpr int64_t kAlignedMaxChunksBf16 = 32768;
 constexpr int64_t kAlignedMaxChunksInt8 = 16384;
 constexpr int64_t kAlignedMaxGrid = 512;
@@ -150,6 +152,8 @@ struct DecodeParams {
   int grid;          // workgroups launched
   int64_t per_forced;  // chunks per workgroup when the caller fixed the split count, else 0
   int piece_cost;      // line units charged per segment start (0 with a fixed split count)
+  int equal_grid;      // > 0: if every sequence has the same length, the first equal_grid workgroups cut
+                       // equal power-of-two partitions instead and the others leave
   float qscale;      // sm_scale * log2(e)
   int q_dtype, out_dtype, table_i64;
   int noncausal;        // every query sees all of its sequence's tokens

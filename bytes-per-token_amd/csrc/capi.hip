@@ -47,6 +47,7 @@ struct Plan {
   bool mfma;  // the matrix-core kernel (all rows of a KV head in one 16-row group)
   int rows, rows_per_group, n_rg, HR, chunk, grid, len_cap;
   int64_t per_forced;
+  int equal_grid;  // workgroups that take equal partitions when all lengths are equal (0: none)
   size_t ws_out_floats, ws_lse_floats, workspace, counters;
 };
 
@@ -110,6 +111,7 @@ int make_plan(const bpt_decode_args* a, Plan* pl) {
                : bpt::decode_groups_per_cu(a->kv_dtype == BPT_KV_INT8, pl->rows_per_group,
                                            a->page_size >= bpt::decode_rows_per_load(a->kv_dtype),
                                            a->q_dtype != BPT_F_BF16);
+  pl->equal_grid = 0;
   if (a->num_splits > 0) {
     // num_splits partitions for a max_context sequence. When that gives more partitions than resident
     // workgroups, each workgroup takes several consecutive ones whole: inside a workgroup the online
@@ -123,25 +125,27 @@ int make_plan(const bpt_decode_args* a, Plan* pl) {
     pl->per_forced = per;
     int64_t grid = (bound_c + pl->per_forced - 1) / pl->per_forced;
     pl->grid = (int)(grid < 1 ? 1 : grid);
-  } else if (!pl->mfma && bound_c > 0 &&
-             ((a->kv_dtype == BPT_KV_BF16 && bound_c <= bpt::kAlignedMaxChunksBf16) ||
-              (a->kv_dtype == BPT_KV_INT8 && bound_c <= bpt::kAlignedMaxChunksInt8))) {
-    // Equal partitions of a power-of-two number of chunks, about 4 sqrt(chunks) of them (at most 512).
-    int64_t target = (int64_t)(4.0 * std::sqrt((double)bound_c));
-    target = target < 1 ? 1 : (target > bpt::kAlignedMaxGrid ? bpt::kAlignedMaxGrid : target);
-    int64_t per = 1;
-    while (per * 2 <= bound_c / target) per *= 2;
-    const int64_t parts = (bound_c + per - 1) / per;
-    if (parts > bpt::kAlignedMaxGrid) per *= (parts + bpt::kAlignedMaxGrid - 1) / bpt::kAlignedMaxGrid;
-    pl->per_forced = per;
-    const int64_t grid = (bound_c + per - 1) / per;
-    pl->grid = (int)(grid < 1 ? 1 : grid);
   } else {
     pl->per_forced = 0;
     int64_t grid = (int64_t)bpt::kComputeUnits * groups_per_cu;
     const int64_t min_chunks = bpt::decode_min_chunks(pl->mfma, pl->rows, a->kv_dtype == BPT_KV_INT8, bound_c);
     const int64_t fill = (bound_c + min_chunks - 1) / min_chunks;
     if (fill < grid) grid = fill;
+    if (!pl->mfma && bound_c > 0 &&
+        ((a->kv_dtype == BPT_KV_BF16 && bound_c <= bpt::kAlignedMaxChunksBf16) ||
+         (a->kv_dtype == BPT_KV_INT8 && bound_c <= bpt::kAlignedMaxChunksInt8))) {
+      // About 4 sqrt(chunks) workgroups (at most 512) take equal partitions of a power-of-two number of
+      // chunks when every sequence has the same length (the kernel checks); the launch keeps the line
+      // cut's workgroups for ragged batches, the rest of them leaving at once otherwise.
+      int64_t target = (int64_t)(4.0 * std::sqrt((double)bound_c));
+      target = target < 1 ? 1 : (target > bpt::kAlignedMaxGrid ? bpt::kAlignedMaxGrid : target);
+      int64_t per = 1;
+      while (per * 2 <= bound_c / target) per *= 2;
+      const int64_t parts = (bound_c + per - 1) / per;
+      if (parts > bpt::kAlignedMaxGrid) per *= (parts + bpt::kAlignedMaxGrid - 1) / bpt::kAlignedMaxGrid;
+      pl->equal_grid = (int)((bound_c + per - 1) / per);
+      if (pl->equal_grid > grid) grid = pl->equal_grid;
+    }
     pl->grid = (int)(grid < 1 ? 1 : grid);
   }
   const size_t slots = (size_t)a->batch * pl->HR + pl->grid;
@@ -345,6 +349,7 @@ int paged_decode(const bpt_decode_args* a, void* stream, const bpt::LaunchEvents
   p.HR = pl.HR;
   p.grid = pl.grid;
   p.per_forced = pl.per_forced;
+  p.equal_grid = pl.equal_grid;
   p.piece_cost = pl.per_forced > 0                         ? 0
                  : pl.mfma && pl.rows >= bpt::kManyRows ? bpt::kManyRowPieceCost
                                                         : bpt::kDecodePieceCost;

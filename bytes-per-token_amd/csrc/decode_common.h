@@ -125,11 +125,17 @@ __device__ __forceinline__ void load_q(const DecodeParams& p, int64_t base, floa
 // over the batch (the segment line: sequence b's segments start at HR * prefix[b]), computed by the whole
 // workgroup into LDS: s_prefix[B + 1], s_len[B]; s_wsum holds one int per wave. A segment of a non-empty
 // sequence costs its chunks plus piece_cost units, which stand for the merge of one more piece and sit
-// at the segment's start, ahead of its chunks. Params: any parameter block with B, lens (NULL: every
-// sequence is len_cap long), len_offset and len_cap.
+// at the segment's start, ahead of its chunks. With check_uniform set, a batch whose sequences all have
+// the same length gets no piece cost. Returns the piece cost the line was built with and whether the
+// lengths were found equal (the same in every thread). Params: any parameter block with B, lens (NULL:
+// every sequence is len_cap long), len_offset and len_cap.
+struct SegmentLine {
+  int piece_cost;
+  bool uniform;
+};
 template <int NW, int CH, typename Params>
-__device__ __forceinline__ void build_segment_line(const Params& p, int* s_prefix, int* s_len, int* s_wsum,
-                                                   int piece_cost = 0) {
+__device__ __forceinline__ SegmentLine build_segment_line(const Params& p, int* s_prefix, int* s_len, int* s_wsum,
+                                                          int piece_cost = 0, bool check_uniform = false) {
   constexpr int NT = NW * 64;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -150,21 +156,35 @@ __device__ __forceinline__ void build_segment_line(const Params& p, int* s_prefi
     const int y = __shfl_up(x, off, 64);
     if (lane >= off) x += y;
   }
+  __shared__ int s_uniform;  // cleared by any thread that sees a length other than the first
   if (lane == 63) s_wsum[tid >> 6] = x;
+  if (check_uniform && tid == 0) s_uniform = 1;
   __syncthreads();
   int run = 0;
   for (int w = 0; w < (tid >> 6); ++w) run += s_wsum[w];
   run += x - sum;
+  const int len0 = s_len[0];
+  int same = 1;
   for (int b = lo; b < hi; ++b) {
     s_prefix[b] = run;
     run += s_len[b] > 0 ? (s_len[b] + CH - 1) / CH + piece_cost : 0;
+    same &= s_len[b] == len0;
   }
   if (tid == 0) {
     int total = 0;
     for (int w = 0; w < NW; ++w) total += s_wsum[w];
     s_prefix[B] = total;
   }
+  if (check_uniform && !same) s_uniform = 0;
   __syncthreads();
+  if (!check_uniform || !s_uniform) return {piece_cost, false};
+  if (piece_cost == 0) return {0, true};
+  // Equal lengths: every segment is the same number of chunks, with no piece cost.
+  const int nb = len0 > 0 ? (len0 + CH - 1) / CH : 0;
+  for (int b = lo; b < hi; ++b) s_prefix[b] = b * nb;
+  if (tid == 0) s_prefix[B] = B * nb;
+  __syncthreads();
+  return {0, true};
 }
 
 constexpr float kLn2 = 0.69314718055994531f;
@@ -192,8 +212,9 @@ __device__ __forceinline__ void write_out(const DecodeParams& p, int b, int qi, 
 // runs on XCD x % 8, each XCD with its own L2), and the line is numbered XCD-major: XCD k takes one
 // contiguous stretch of it. Neighbouring ranges then meet in one L2: the KV heads of a sequence (one page
 // holds all of them, and per-token scales share cache lines across them) and the ranges of one segment.
-__device__ __forceinline__ int64_t line_index() {
-  const int x = blockIdx.x, n = gridDim.x;
+// n: the workgroups that share the line (the first n of the launch).
+__device__ __forceinline__ int64_t line_index(int n) {
+  const int x = blockIdx.x;
   const int q = n >> 3, r = n & 7, k = x & 7;
   return (int64_t)k * q + min(k, r) + (x >> 3);
 }

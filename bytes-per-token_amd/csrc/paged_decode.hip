@@ -426,15 +426,27 @@ void decode_kernel(const DecodeParams p) {
   const int wave = sread(tid >> 6);
   const int B = p.B;
 
-  build_segment_line<NW, CH>(p, s_prefix, s_len, s_wsum, p.piece_cost);
+  // Equal partitions when the plan asked for them and every sequence has the same length: no piece cost, the
+  // first equal_grid workgroups each take the smallest power-of-two number of chunks that they cover between
+  // them, and the rest of the launch leaves. Otherwise the whole launch shares the line cut.
+  const SegmentLine line = build_segment_line<NW, CH>(p, s_prefix, s_len, s_wsum, p.piece_cost, p.equal_grid > 0);
+  const int X = sread(line.piece_cost);
+  const bool equal = sread(line.uniform ? 1 : 0) != 0;
   zero_empty_sequences<NT>(p, s_prefix);
 
   // ---- this workgroup's range of chunks -----------------------------------------------------------
   const int HR = p.HR;
   const int64_t C = (int64_t)HR * s_prefix[B];
   if (C == 0) return;
-  const int64_t per = p.per_forced > 0 ? p.per_forced : (C + gridDim.x - 1) / gridDim.x;
-  const int64_t g = line_index();
+  const int n_line = equal ? p.equal_grid : (int)gridDim.x;
+  if ((int)blockIdx.x >= n_line) return;
+  int64_t per = p.per_forced > 0 ? p.per_forced : (C + n_line - 1) / n_line;
+  if (equal) {
+    int64_t pw = 1;
+    while (pw < per) pw *= 2;
+    per = pw;
+  }
+  const int64_t g = line_index(n_line);
   const int64_t c_begin = g * per;
   if (c_begin >= C) return;
   const int64_t c_end = min(c_begin + per, C);
@@ -451,7 +463,6 @@ void decode_kernel(const DecodeParams p) {
   }
   // A segment spans X line units, then its nb chunks; a range that starts among the X units starts with
   // the segment's first chunk.
-  const int X = p.piece_cost;
   int span = sread(s_prefix[b + 1] - s_prefix[b]);
   int nb = span - X;
   int hr, k;

@@ -379,7 +379,7 @@ __global__ __launch_bounds__(NW * 64, kMfmaWavesPerSimd) void decode_mfma_kernel
   const int64_t C = (int64_t)HR * SB;
   if (C == 0) return;
   const int64_t per = p.per_forced > 0 ? p.per_forced : (C + gridDim.x - 1) / gridDim.x;
-  const int64_t g = line_index();
+  const int64_t g = line_index(gridDim.x);
   const int64_t c_begin = g * per;
   if (c_begin >= C) return;
   const int64_t c_end = min(c_begin + per, C);

@@ -233,6 +233,38 @@ def test_measured_shapes_at_full_size(name):
     check(got, oracle_out(w), name)
 
 
+@pytest.mark.parametrize("fmt,scales", [("bf16", None), ("int8", "token"), ("int8", "head")])
+@pytest.mark.parametrize("lengths,max_context", [([2048], None), ([513] * 3, None), ([17] * 8, None),
+                                                 ([1] * 64, None), ([4096] * 2, 8192), ([700] * 5, 3000),
+                                                 ([0] * 4, 512), ([300] * 6 + [299], None)])
+def test_equal_lengths_take_equal_partitions(fmt, scales, lengths, max_context):
+    """Small BF16 / INT8 calls on the vector kernel whose sequences all have one length are cut into equal
+    power-of-two partitions by part of the launch (the rest leaves at once), ranges crossing sequence
+    boundaries; lengths below max_context use fewer of those workgroups. The last case differs in one
+    length and keeps the line cut."""
+    c = make_case(fmt, lengths, scales=scales)
+    got, want = run_case(c, max_context=max_context)
+    check(got, want, f"{fmt}/{scales} {len(lengths)} x {lengths[0]}")
+    if lengths[0] == 0:
+        assert got.float().abs().sum().item() == 0
+
+
+def test_equal_lengths_beyond_max_context_are_cut_to_it():
+    """Lengths that differ but all exceed max_context are equal once cut to it."""
+    c = make_case("bf16", [600, 900, 556])
+    from bpt_amd import paged_decode_attention
+
+    got = paged_decode_attention(c["q"], c["k"], c["v"], c["table"], c["lens"], c["ks"], c["vs"], scale=0.1,
+                                 max_context=256)
+    lens = torch.full((3,), 256, dtype=torch.int32, device=DEV)
+    want = paged_decode_attention(c["q"], c["k"], c["v"], c["table"], lens, c["ks"], c["vs"], scale=0.1,
+                                  max_context=256)
+    assert torch.equal(got, want)
+    c["lens"] = lens
+    got, want = run_case(c, scale=0.1, max_context=256)
+    check(got, want, "three lengths cut to 256")
+
+
 def test_many_short_sequences_share_workgroups():
     """More segments than workgroups: a workgroup's range walks many (sequence, head) segments, with
     empty sequences at the start, middle and end of the batch."""
