@@ -136,7 +136,8 @@ int make_plan(const bpt_decode_args* a, Plan* pl) {
          (a->kv_dtype == BPT_KV_INT8 && bound_c <= bpt::kAlignedMaxChunksInt8))) {
       // About 4 sqrt(chunks) workgroups (at most 512) take equal partitions of a power-of-two number of
       // chunks when every sequence has the same length (the kernel checks); the launch keeps the line
-      // cut's workgroups for ragged batches, the rest of them leaving at once otherwise.
+      // cut's workgroups for ragged batches, the rest of them leaving at once otherwise. One sequence
+      // is never ragged: it launches the equal count alone.
       int64_t target = (int64_t)(4.0 * std::sqrt((double)bound_c));
       target = target < 1 ? 1 : (target > bpt::kAlignedMaxGrid ? bpt::kAlignedMaxGrid : target);
       int64_t per = 1;
@@ -144,7 +145,7 @@ int make_plan(const bpt_decode_args* a, Plan* pl) {
       const int64_t parts = (bound_c + per - 1) / per;
       if (parts > bpt::kAlignedMaxGrid) per *= (parts + bpt::kAlignedMaxGrid - 1) / bpt::kAlignedMaxGrid;
       pl->equal_grid = (int)((bound_c + per - 1) / per);
-      if (pl->equal_grid > grid) grid = pl->equal_grid;
+      if (a->batch == 1 || pl->equal_grid > grid) grid = pl->equal_grid;
     }
     pl->grid = (int)(grid < 1 ? 1 : grid);
   }
@@ -350,9 +351,11 @@ int paged_decode(const bpt_decode_args* a, void* stream, const bpt::LaunchEvents
   p.grid = pl.grid;
   p.per_forced = pl.per_forced;
   p.equal_grid = pl.equal_grid;
-  p.piece_cost = pl.per_forced > 0                         ? 0
-                 : pl.mfma && pl.rows >= bpt::kManyRows ? bpt::kManyRowPieceCost
-                                                        : bpt::kDecodePieceCost;
+  // No piece cost with a fixed split count, nor for one sequence cut into equal partitions (the kernel then
+  // has no line to rebuild).
+  p.piece_cost = pl.per_forced > 0 || (pl.equal_grid > 0 && a->batch == 1) ? 0
+                 : pl.mfma && pl.rows >= bpt::kManyRows                    ? bpt::kManyRowPieceCost
+                                                                           : bpt::kDecodePieceCost;
   p.len_cap = pl.len_cap;
   p.qscale = a->sm_scale * bpt::kLog2e;
   p.q_dtype = a->q_dtype;

@@ -108,18 +108,20 @@ def test_plan_gives_int8_vector_segments_three_groups_per_cu(built_lib):
 def test_plan_launches_enough_workgroups_for_equal_partitions(built_lib):
     """BF16 and INT8 calls on the vector kernel up to 32768 / 16384 chunks may be cut into partitions of a
     power-of-two number of chunks, about 4 sqrt(chunks) of them and at most 512 (when the kernel finds
-    all lengths equal): the launch is the larger of that count and the line cut's."""
+    all lengths equal): the launch is the larger of that count and the line cut's, or that count alone for
+    one sequence."""
     def plan(fmt, b, ctx, hq=16):
         nb = max(b * ctx // 16, 64)
         q, k, v, table, lens, ks, vs = cpu_case(fmt, b=b, hq=hq, nb=nb, max_blocks=max(ctx // 16, 1))
         grid, chunk, ws, _ = decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=ctx)
         return grid, chunk, ws
 
-    grid, chunk, ws = plan("bf16", 1, 512)  # 8 heads x 32 chunks of 16 tokens = 256: the line cut's 256
-    assert (grid, chunk) == (256, 16) and ws == expected_workspace(1, 8, 2, 256)
+    grid, chunk, ws = plan("bf16", 1, 512)  # 8 heads x 32 chunks of 16 tokens = 256: 64 partitions of 4
+    assert (grid, chunk) == (64, 16) and ws == expected_workspace(1, 8, 2, 64)
     assert plan("bf16", 2, 2048)[0] == 512   # 2048 chunks: 256 partitions of 8, the line cut 512
     assert plan("bf16", 8, 8192)[0] == 512   # 32768 chunks: target 512 (724 capped), partitions of 64
-    assert plan("int8", 1, 2048)[0] == 128   # 512 chunks of 32 tokens: 128 partitions of 4 (line cut: 64)
+    assert plan("int8", 1, 2048)[0] == 128   # 512 chunks of 32 tokens: 128 partitions of 4
+    assert plan("bf16", 1, 8192)[0] == 256   # 4096 chunks: 256 partitions of 16 (line cut: 512)
     assert plan("int8", 4, 8192)[0] == 768   # 8192 chunks: 512 partitions of 16, line cut 3 per CU
     assert plan("int8", 16, 8192)[0] == 768  # 32768 chunks: the line cut only, three workgroups per CU
 
