@@ -137,15 +137,21 @@ int make_plan(const bpt_decode_args* a, Plan* pl) {
       // About 4 sqrt(chunks) workgroups (at most 512) take equal partitions of a power-of-two number of
       // chunks when every sequence has the same length (the kernel checks); the launch keeps the line
       // cut's workgroups for ragged batches, the rest of them leaving at once otherwise. One sequence
-      // is never ragged: it launches the equal count alone.
+      // is never ragged: its partitions are fixed here (no piece cost, no check in the kernel).
       int64_t target = (int64_t)(4.0 * std::sqrt((double)bound_c));
       target = target < 1 ? 1 : (target > bpt::kAlignedMaxGrid ? bpt::kAlignedMaxGrid : target);
       int64_t per = 1;
       while (per * 2 <= bound_c / target) per *= 2;
       const int64_t parts = (bound_c + per - 1) / per;
       if (parts > bpt::kAlignedMaxGrid) per *= (parts + bpt::kAlignedMaxGrid - 1) / bpt::kAlignedMaxGrid;
-      pl->equal_grid = (int)((bound_c + per - 1) / per);
-      if (a->batch == 1 || pl->equal_grid > grid) grid = pl->equal_grid;
+      const int64_t equal = (bound_c + per - 1) / per;
+      if (a->batch == 1) {
+        pl->per_forced = per;
+        grid = equal;
+      } else {
+        pl->equal_grid = (int)equal;
+        if (equal > grid) grid = equal;
+      }
     }
     pl->grid = (int)(grid < 1 ? 1 : grid);
   }
@@ -351,11 +357,9 @@ int paged_decode(const bpt_decode_args* a, void* stream, const bpt::LaunchEvents
   p.grid = pl.grid;
   p.per_forced = pl.per_forced;
   p.equal_grid = pl.equal_grid;
-  // No piece cost with a fixed split count, nor for one sequence cut into equal partitions (the kernel then
-  // has no line to rebuild).
-  p.piece_cost = pl.per_forced > 0 || (pl.equal_grid > 0 && a->batch == 1) ? 0
-                 : pl.mfma && pl.rows >= bpt::kManyRows                    ? bpt::kManyRowPieceCost
-                                                                           : bpt::kDecodePieceCost;
+  p.piece_cost = pl.per_forced > 0                         ? 0
+                 : pl.mfma && pl.rows >= bpt::kManyRows ? bpt::kManyRowPieceCost
+                                                        : bpt::kDecodePieceCost;
   p.len_cap = pl.len_cap;
   p.qscale = a->sm_scale * bpt::kLog2e;
   p.q_dtype = a->q_dtype;

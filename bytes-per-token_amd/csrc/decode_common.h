@@ -163,12 +163,14 @@ __device__ __forceinline__ SegmentLine build_segment_line(const Params& p, int* 
   int run = 0;
   for (int w = 0; w < (tid >> 6); ++w) run += s_wsum[w];
   run += x - sum;
-  const int len0 = s_len[0];
   int same = 1;
+  if (check_uniform) {
+    const int len0 = s_len[0];
+    for (int b = lo; b < hi; ++b) same &= s_len[b] == len0;
+  }
   for (int b = lo; b < hi; ++b) {
     s_prefix[b] = run;
     run += s_len[b] > 0 ? (s_len[b] + CH - 1) / CH + piece_cost : 0;
-    same &= s_len[b] == len0;
   }
   if (tid == 0) {
     int total = 0;
@@ -180,6 +182,7 @@ __device__ __forceinline__ SegmentLine build_segment_line(const Params& p, int* 
   if (!check_uniform || !s_uniform) return {piece_cost, false};
   if (piece_cost == 0) return {0, true};
   // Equal lengths: every segment is the same number of chunks, with no piece cost.
+  const int len0 = s_len[0];
   const int nb = len0 > 0 ? (len0 + CH - 1) / CH : 0;
   for (int b = lo; b < hi; ++b) s_prefix[b] = b * nb;
   if (tid == 0) s_prefix[B] = B * nb;
