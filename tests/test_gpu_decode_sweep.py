@@ -6,6 +6,8 @@ counts, queries per sequence, page size, cache format and scale granularity, q d
 one seed, so both kernels, the stream-K line walk (pieces, split segments, ranges that hold no chunk) and
 the split-K combine meet many combinations that the targeted tests in test_gpu_decode.py do not spell out.
 Sizes stay small enough for the oracle to finish in well under a second per case.
+A second sweep keeps every sequence of a call at one length, the case the vector kernel cuts into equal
+partitions.
 """
 
 import numpy as np
@@ -49,3 +51,25 @@ def test_random_configuration(seed):
     for i, t in enumerate(cfg["lengths"]):
         if t == 0:
             assert got[i].float().abs().sum().item() == 0, f"seed {seed}: row {i} has no tokens"
+
+
+def draw_equal(seed: int) -> dict:
+    """Vector-kernel calls (BF16, or INT8 with 1..4 rows per KV head) whose sequences share one length: the
+    equal power-of-two partitions, with max_context at or above that length and a batch of one now and then."""
+    g = np.random.default_rng(5000 + seed)
+    fmt, scales = [("bf16", None), ("int8", "token"), ("int8", "head")][int(g.integers(3))]
+    hq, hkv = [(8, 8), (16, 8), (32, 8), (12, 4)][int(g.integers(4))]
+    b = int(g.choice([1, 1, 2, 3, 7, 16]))
+    t = int(g.choice([1, 15, 16, 17, 100, 513, 1024, 2047, 3000]))
+    return dict(fmt=fmt, scales=scales, hq=hq, hkv=hkv, lengths=[t] * b, page=int(g.choice([8, 16, 32])),
+                max_context=t + int(g.choice([0, 0, 1, 500])),
+                q_dtype=[torch.bfloat16, torch.float16, torch.float32][int(g.integers(3))])
+
+
+@pytest.mark.parametrize("seed", range(48))
+def test_random_equal_lengths(seed):
+    cfg = draw_equal(seed)
+    c = make_case(cfg["fmt"], cfg["lengths"], hq=cfg["hq"], hkv=cfg["hkv"], page=cfg["page"],
+                  scales=cfg["scales"] or "head", seed=seed)
+    got, want = run_case(c, q=c["q"].to(cfg["q_dtype"]), max_context=cfg["max_context"])
+    check(got, want, f"seed {seed}: {cfg}")
