@@ -359,9 +359,10 @@ def measure_kivi_quantize(flush, iters: int, warmup: int) -> dict:
 def measure_decode_step(iters: int, warmup: int, layers: int = 28) -> dict:
     """One decode step of a 28-layer Qwen3-1.7B through the paged cache object (engine/kv_cache.py's role):
     `PagedQuantKVCache.prepare` from device positions (block tables, write slots and lengths built on the
-    device), then per layer `attend` = the new token's quantize-on-write plus the decode call. FP8 codes with
+    device), then per layer `attend` = the new token's quantize-on-write and the decode call, one launch
+    (paged_append_decode: the matrix-core kernel stores the token's codes and uses them in place). FP8 codes with
     per-head scales and the headline workload's 32 ragged lengths; the pools hold random codes (the step reads
-    them, not their values). Timed eager (host-bound: 57 launches from Python) and replayed from a HIP graph;
+    them, not their values). Timed eager (29 launches from Python) and replayed from a HIP graph;
     GB/s counts the KV bytes the step's decode calls read. The step's 4.8 GB exceeds every cache, so no
     flush is needed between steps."""
     import torch
@@ -407,7 +408,7 @@ def measure_decode_step(iters: int, warmup: int, layers: int = 28) -> dict:
         "us_per_step_eager": round(us_eager, 1),
         "us_per_step_graph": round(us_graph, 1),
         "gbps_graph": round(kv / (us_graph * 1e-6) / 1e9, 1),
-        "launches_per_step": 1 + 2 * layers,
+        "launches_per_step": 1 + layers,
     }
     log(f"decode-step {layers} layers: {row['us_per_step_eager']} us eager, {row['us_per_step_graph']} us in a graph, "
         f"{row['gbps_graph']} GB/s")

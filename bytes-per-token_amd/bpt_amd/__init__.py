@@ -16,6 +16,7 @@ from .paged_attention import (
     decode_kernel_name,
     decode_plan,
     kv_read_bytes,
+    paged_append_decode,
     paged_decode_attention,
     paged_prepare,
     quantize_append,
@@ -30,6 +31,7 @@ __all__ = [
     "decode_plan",
     "kivi",
     "kv_read_bytes",
+    "paged_append_decode",
     "paged_decode_attention",
     "paged_prepare",
     "quantize_append",

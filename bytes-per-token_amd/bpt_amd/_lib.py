@@ -271,6 +271,7 @@ SIGNATURES = {
     "bpt_paged_decode_noalloc": (_i32, [ctypes.POINTER(DecodeArgs), _vp]),
     "bpt_paged_decode_timed": (_i32, [ctypes.POINTER(DecodeArgs), _vp, _vp, _vp]),
     "bpt_quant_append": (_i32, [ctypes.POINTER(AppendArgs), _vp]),
+    "bpt_paged_append_decode": (_i32, [ctypes.POINTER(AppendArgs), ctypes.POINTER(DecodeArgs), _vp]),
     "bpt_kivi_plan": (
         _i32,
         [ctypes.POINTER(KiviArgs), ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)],
@@ -290,7 +291,7 @@ SIGNATURES = {
     "bpt_copy_probe": (_i32, [_vp, _vp, ctypes.c_uint64, _vp]),
 }
 
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 
 class BptError(RuntimeError):

@@ -32,7 +32,7 @@ from typing import Any
 
 import torch
 
-from .paged_attention import paged_decode_attention, paged_prepare, quantize_append
+from .paged_attention import paged_append_decode, paged_prepare
 
 _FORMATS = {torch.float8_e4m3fn: "fp8", torch.int8: "int8", torch.bfloat16: "bf16"}
 HEAD_DIM = 128  # the one head size the paged decode kernels are built for
@@ -233,12 +233,10 @@ class PagedQuantKVCache:
             raise ValueError(f"k and v must be [{b}, {self.num_kv_heads}, {nq}, {d}]")
         if tuple(meta.write_blocks.shape) != (b, nq):
             raise ValueError(f"meta was prepared for {tuple(meta.write_blocks.shape)} tokens, not {(b, nq)}")
-        quantize_append(
-            k.transpose(1, 2), v.transpose(1, 2), self.k[layer], self.v[layer], self.k_scale[layer],
-            self.v_scale[layer], meta.write_blocks, meta.write_offsets,
-        )
-        out = paged_decode_attention(
-            q.transpose(1, 2), self.k[layer], self.v[layer], meta.block_table, meta.context_lens,
-            self.k_scale[layer], self.v_scale[layer], scale=scale, max_context=meta.kv_len, out_dtype=q.dtype,
+        # Store, then attend; one launch where the decode kernel can store the rows itself (paged_append_decode).
+        out = paged_append_decode(
+            q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), self.k[layer], self.v[layer], meta.block_table,
+            meta.context_lens, self.k_scale[layer], self.v_scale[layer], meta.write_blocks, meta.write_offsets,
+            scale=scale, max_context=meta.kv_len, out_dtype=q.dtype,
         )  # [B, Q, Hq, D] in q's dtype: the kernel rounds once, from float32 (integration/kv_cache.py:177-181)
         return out.transpose(1, 2)

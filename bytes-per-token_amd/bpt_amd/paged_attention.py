@@ -199,6 +199,7 @@ def paged_decode_attention(
     lse: torch.Tensor | None = None,
     _cascade: dict | None = None,
     _events: tuple | None = None,
+    _append: object | None = None,
 ) -> torch.Tensor:
     """softmax(q kᵀ · scale) v over each sequence's paged cache, dequantized in registers.
 
@@ -265,7 +266,9 @@ def paged_decode_attention(
         _require(t.device == dev and t.is_contiguous(), f"{name} must be a contiguous tensor on q's device")
     a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     a.counters, a.counters_bytes = counters.data_ptr(), counters.numel() * counters.element_size()
-    if _events is None:
+    if _append is not None:  # paged_append_decode: store the new rows, then attend (one launch where it can)
+        _lib.check(lib.bpt_paged_append_decode(ctypes.byref(_append), ctypes.byref(a), ctypes.c_void_p(stream)))
+    elif _events is None:
         _lib.check(lib.bpt_paged_decode(ctypes.byref(a), ctypes.c_void_p(stream)))
     else:  # measurement: two raw hipEvent_t handles recorded around the kernel itself
         _lib.check(lib.bpt_paged_decode_timed(ctypes.byref(a), ctypes.c_void_p(stream), ctypes.c_void_p(_events[0]),
@@ -291,6 +294,12 @@ def quantize_append(
     max(amax / 127, 1e-12) (448 for FP8) is computed and stored next to the codes (quant/w8a8.py:55-74).
     BF16: the rows are copied. Rows whose page is negative or outside the pool are skipped.
     """
+    a, dev = _append_args(k, v, k_cache, v_cache, k_scale, v_scale, write_blocks, write_offsets)
+    _lib.check(_lib.lib().bpt_quant_append(ctypes.byref(a), ctypes.c_void_p(_stream(dev))))
+
+
+def _append_args(k, v, k_cache, v_cache, k_scale, v_scale, write_blocks, write_offsets):
+    """The checked bpt_append_args of quantize_append's arguments, and their device."""
     _require(k.dim() == 4 and k.shape == v.shape, "k and v must be [B, Q, Hkv, D]")
     _require(k.dtype == v.dtype and k.dtype in _FLOAT_CODES, "k and v must share a bf16/f16/f32 dtype")
     _require(k.stride() == v.stride() and k.stride(-1) == 1, "k and v must share strides, channels contiguous")
@@ -325,7 +334,39 @@ def quantize_append(
     a.kv_stride_block, a.kv_stride_token, a.kv_stride_head = k_cache.stride(0), k_cache.stride(1), k_cache.stride(2)
     a.k_scale, a.v_scale = _ptr(k_scale), _ptr(v_scale)
     a.scale_stride_block, a.scale_stride_token, a.scale_stride_head = sc_strides
-    _lib.check(_lib.lib().bpt_quant_append(ctypes.byref(a), ctypes.c_void_p(_stream(dev))))
+    return a, dev
+
+
+def paged_append_decode(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    context_lens: torch.Tensor,
+    k_scale: torch.Tensor | None,
+    v_scale: torch.Tensor | None,
+    write_blocks: torch.Tensor,
+    write_offsets: torch.Tensor,
+    *,
+    scale: float,
+    max_context: int,
+    out: torch.Tensor | None = None,
+    out_dtype: torch.dtype = torch.bfloat16,
+) -> torch.Tensor:
+    """Store the new rows k, v [B, Q, Hkv, D] (as quantize_append), then attend (as paged_decode_attention):
+    the cache's store-then-attend (integration/kv_cache.py:160-192).
+
+    One launch when the decode runs on the matrix-core kernel with per-head scales and the rows are the last
+    Q <= 8 tokens of every sequence (write slots = the block table's pages for positions context_len - Q ..
+    context_len - 1, as paged_prepare produces them), bf16, head dim 128: the kernel stores the codes and uses
+    them for those tokens directly. Otherwise the two calls, in order.
+    """
+    a, dev = _append_args(k, v, k_cache, v_cache, k_scale, v_scale, write_blocks, write_offsets)
+    _require(q.device == dev, f"q is on {q.device}, the new rows on {dev}")
+    return paged_decode_attention(q, k_cache, v_cache, block_table, context_lens, k_scale, v_scale, scale=scale,
+                                  max_context=max_context, out=out, out_dtype=out_dtype, _append=a)
 
 
 def paged_prepare(

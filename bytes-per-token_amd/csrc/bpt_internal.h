@@ -162,6 +162,17 @@ struct DecodeParams {
   float* lse_out;       // optional [B, Q, Hq]: each row's log-sum-exp (natural log)
   const float* merge_out;  // optional [B, Q, Hq, D]: another token range's normalized partial, merged into out
   const float* merge_lse;  // its log-sum-exp [B, Q, Hq] (natural log, -inf when empty)
+  // Quantize-on-write in the same launch (fuse_q > 0, matrix-core kernel, per-head scales): the bf16 rows
+  // [B, fuse_q, Hkv, D] of the last fuse_q tokens of every sequence, stored to their slots and used for
+  // those tokens in place of what the pool held.
+  int fuse_q;
+  const uint16_t* nk;
+  const uint16_t* nv;
+  int64_t n_sb, n_sq, n_sh;  // elements
+  const void* w_blocks;
+  const void* w_offsets;
+  int64_t w_sb, w_sq;
+  int w_i64;
 };
 
 struct AppendParams {

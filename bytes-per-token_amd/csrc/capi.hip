@@ -284,7 +284,7 @@ struct Buffers {
 };
 
 int paged_decode(const bpt_decode_args* a, void* stream, const bpt::LaunchEvents& ev, const char* fn,
-                 const Buffers* own = nullptr) {
+                 const Buffers* own = nullptr, const bpt::AppendParams* fuse = nullptr) {
   Plan pl;
   int rc = make_plan(a, &pl);
   if (rc) return rc;
@@ -318,7 +318,7 @@ int paged_decode(const bpt_decode_args* a, void* stream, const bpt::LaunchEvents
   if (!aligned_to(a->q, a->q_stride_b, a->q_stride_q, a->q_stride_h, float_bytes(a->q_dtype)))
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: q rows must be 16-byte aligned (pointer and strides)", fn);
 
-  bpt::DecodeParams p;
+  bpt::DecodeParams p{};
   p.q = a->q;
   p.q_sb = a->q_stride_b;
   p.q_sq = a->q_stride_q;
@@ -370,6 +370,19 @@ int paged_decode(const bpt_decode_args* a, void* stream, const bpt::LaunchEvents
   p.lse_out = a->lse_out;
   p.merge_out = a->merge_out;
   p.merge_lse = a->merge_lse;
+  if (fuse) {
+    p.fuse_q = fuse->Q;
+    p.nk = (const uint16_t*)fuse->k;
+    p.nv = (const uint16_t*)fuse->v;
+    p.n_sb = fuse->n_sb;
+    p.n_sq = fuse->n_sq;
+    p.n_sh = fuse->n_sh;
+    p.w_blocks = fuse->blocks;
+    p.w_offsets = fuse->offsets;
+    p.w_sb = fuse->s_sb;
+    p.w_sq = fuse->s_sq;
+    p.w_i64 = fuse->slot_i64;
+  }
   hipError_t e = pl.mfma ? bpt::launch_decode_mfma(p, a->kv_dtype, a->scale_kind, (hipStream_t)stream, ev)
                          : bpt::launch_decode(p, a->kv_dtype, a->scale_kind, pl.rows_per_group, (hipStream_t)stream, ev);
   if (e != hipSuccess) return hip_fail(fn, e);
@@ -695,8 +708,11 @@ int bpt_rms_norm_int8(const bpt_norm_quant_args* a, void* stream) {
   return BPT_OK;
 }
 
-int bpt_quant_append(const bpt_append_args* a, void* stream) {
-  const char* fn = "bpt_quant_append";
+namespace {
+
+// Checks bpt_append_args and fills p; *empty: nothing to write.
+int append_params(const bpt_append_args* a, bpt::AppendParams* out, bool* empty, const char* fn) {
+  *empty = false;
   if (!a) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: args is NULL", fn);
   if (a->struct_size != sizeof(bpt_append_args))
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: struct_size %u != %zu (stale binding)", fn, a->struct_size,
@@ -715,7 +731,10 @@ int bpt_quant_append(const bpt_append_args* a, void* stream) {
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: bad sizes", fn);
   if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256)
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: head_dim %d not supported (64, 128, 256)", fn, a->head_dim);
-  if ((int64_t)a->batch * a->num_queries * a->num_kv_heads == 0) return BPT_OK;
+  if ((int64_t)a->batch * a->num_queries * a->num_kv_heads == 0) {
+    *empty = true;
+    return BPT_OK;
+  }
   if (!a->k || !a->v || !a->write_blocks || !a->write_offsets || !a->k_cache || !a->v_cache)
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: rows, slots and caches must be non-NULL", fn);
   if (a->kv_dtype != BPT_KV_BF16 && (!a->k_scale || !a->v_scale))
@@ -751,9 +770,54 @@ int bpt_quant_append(const bpt_append_args* a, void* stream) {
   p.num_blocks = a->num_blocks;
   p.src_dtype = a->src_dtype;
   p.slot_i64 = a->slot_dtype == BPT_IDX_I64;
+  *out = p;
+  return BPT_OK;
+}
+
+// Whether the matrix-core decode of d can store a's rows itself: the same caches and shapes, per-head scales,
+// bf16 rows (16-byte aligned) for the last Q <= 8 tokens of every sequence, lengths given and not offset,
+// head dim 128, no caller partial to merge.
+bool fusable(const bpt_append_args* a, const bpt_decode_args* d) {
+  Plan pl;
+  if (make_plan(d, &pl) != BPT_OK) return false;
+  const bool rows_aligned = aligned16(a->k) && aligned16(a->v) && (a->new_stride_b * 2) % 16 == 0 &&
+                            (a->new_stride_q * 2) % 16 == 0 && (a->new_stride_h * 2) % 16 == 0;
+  return pl.mfma && a->kv_dtype == d->kv_dtype && a->kv_dtype != BPT_KV_BF16 && a->scale_kind == BPT_SCALE_PER_HEAD &&
+         d->scale_kind == BPT_SCALE_PER_HEAD && a->k_cache == d->k_cache && a->v_cache == d->v_cache &&
+         a->k_scale == d->k_scale && a->v_scale == d->v_scale && a->kv_stride_block == d->kv_stride_block &&
+         a->kv_stride_token == d->kv_stride_token && a->kv_stride_head == d->kv_stride_head &&
+         a->num_blocks == d->num_blocks && a->page_size == d->page_size && a->num_kv_heads == d->num_kv_heads &&
+         a->head_dim == 128 && d->head_dim == 128 && a->batch == d->batch && a->num_queries == d->num_queries &&
+         a->num_queries >= 1 && a->num_queries <= 8 && a->src_dtype == BPT_F_BF16 && rows_aligned &&
+         d->context_lens != nullptr && d->len_offset == 0 && d->merge_out == nullptr;
+}
+
+}  // namespace
+
+int bpt_quant_append(const bpt_append_args* a, void* stream) {
+  const char* fn = "bpt_quant_append";
+  bpt::AppendParams p;
+  bool empty;
+  int rc = append_params(a, &p, &empty, fn);
+  if (rc || empty) return rc;
   hipError_t e = bpt::launch_append(p, a->kv_dtype, a->scale_kind, a->head_dim, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(fn, e);
   return BPT_OK;
+}
+
+int bpt_paged_append_decode(const bpt_append_args* append, const bpt_decode_args* decode, void* stream) {
+  const char* fn = "bpt_paged_append_decode";
+  bpt::AppendParams p;
+  bool empty;
+  int rc = append_params(append, &p, &empty, fn);
+  if (rc) return rc;
+  if (!decode) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: decode args is NULL", fn);
+  if (!empty && fusable(append, decode)) return paged_decode(decode, stream, {}, fn, nullptr, &p);
+  if (!empty) {
+    hipError_t e = bpt::launch_append(p, append->kv_dtype, append->scale_kind, append->head_dim, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(fn, e);
+  }
+  return paged_decode(decode, stream, {}, fn);
 }
 
 int bpt_fp8_decode_table(float* out256, void* stream) {

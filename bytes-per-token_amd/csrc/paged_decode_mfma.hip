@@ -46,7 +46,109 @@ struct MChunk {
   U4 k[2][2];          // tile t, load j: token 16 t + 8 j + l / 8, bytes 16 (l % 8) .. 16 (l % 8) + 15
   U4 v[2][2];          // tile t, load j: V of token 16 t + 8 j + l / 8, bytes 16 (l % 8) .. + 15 (as k)
   float sc1;           // per-token scales: lane l holds tile l / 32's token l % 16, K (l / 16 even) or V
+  // Fused writes: the bf16 channels 16 (l % 8) .. + 15 of a new token among this lane's four load rows
+  // (at most one when fuse_q <= 8), and which load (2 t + j) it replaces, or -1.
+  U4 nk[2], nv[2];
+  int nsel_k, nsel_v;
 };
+
+// The new token among this lane's four rows of chunk kk (first_new: the sequence's first new token), as
+// 2 t + j with its index among the new rows, or -1.
+__device__ __forceinline__ int new_row(int kk, int len, int first_new, int lane, int& qi) {
+  const int T0 = kk * kMChunk;
+  int sel = -1;
+  qi = 0;
+  if (T0 + kMChunk > first_new) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int tok = T0 + 16 * t + 8 * j + (lane >> 3);
+        if (tok >= first_new && tok < len) {
+          sel = 2 * t + j;
+          qi = tok - first_new;
+        }
+      }
+    }
+  }
+  return sel;
+}
+
+// 16 new channels (bf16, in order) -> their codes under scale s, as quant_append_kernel computes them
+// (IEEE quotient; FP8: clamp to +-448 and round to nearest even; INT8: rint and clamp).
+template <int KV>
+__device__ __forceinline__ U4 quantize16(const U4 (&x)[2], float s) {
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const U4& h = x[i >> 3];
+    const uint32_t word = ((i >> 1) & 3) == 0 ? h.x : ((i >> 1) & 3) == 1 ? h.y : ((i >> 1) & 3) == 2 ? h.z : h.w;
+    const float f = __uint_as_float((i & 1) ? (word & 0xffff0000u) : (word << 16));
+    const float y = __fdiv_rn(f, s);
+    uint32_t code;
+    if constexpr (KV == kKvFp8) {
+      code = f32_to_fp8(clamp_fp8_range(y));
+    } else {
+      float r = rintf(y);
+      r = r > 127.0f ? 127.0f : (r < -128.0f ? -128.0f : r);
+      code = (uint32_t)(int32_t)r & 0xffu;
+    }
+    w[i >> 2] |= code << (8 * (i & 3));
+  }
+  return U4{w[0], w[1], w[2], w[3]};
+}
+
+template <int KV>
+__device__ __forceinline__ void substitute(U4 (&rows)[2][2], const U4 (&x)[2], int sel, float s) {
+  if (sel < 0) return;
+  const U4 c = quantize16<KV>(x, s);
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      if (sel == 2 * t + j) rows[t][j] = c;
+    }
+  }
+}
+
+// This launch's share of the new rows' writes: B x fuse_q x Hkv rows of K and of V, one per half-wave,
+// 32 lanes x 4 channels, to the caller's (block, offset) slots: the bytes quant_append_kernel stores.
+template <int KV, int NT>
+__device__ __forceinline__ void fused_append(const DecodeParams& p) {
+  const int lane = threadIdx.x & 31;
+  const int64_t ntask = (int64_t)p.B * p.fuse_q * p.Hkv * 2;
+  for (int64_t task = (int64_t)blockIdx.x * (NT / 32) + (threadIdx.x >> 5); task < ntask;
+       task += (int64_t)gridDim.x * (NT / 32)) {
+    const int which = (int)(task & 1);
+    const int64_t row = task >> 1;
+    const int h = (int)(row % p.Hkv);
+    const int64_t bq = row / p.Hkv;
+    const int qi = (int)(bq % p.fuse_q);
+    const int b = (int)(bq / p.fuse_q);
+    const int64_t si = (int64_t)b * p.w_sb + (int64_t)qi * p.w_sq;
+    const int64_t blk = load_index(p.w_blocks, si, p.w_i64 != 0);
+    const int64_t off = load_index(p.w_offsets, si, p.w_i64 != 0);
+    if (blk < 0 || blk >= p.num_blocks || off < 0 || off >= p.P) continue;
+    const uint16_t* src = (which ? p.nv : p.nk) + (int64_t)b * p.n_sb + (int64_t)qi * p.n_sq + (int64_t)h * p.n_sh + 4 * lane;
+    const float s = (which ? p.vs : p.ks)[h];
+    uint32_t w = 0u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float y = __fdiv_rn(__uint_as_float((uint32_t)src[i] << 16), s);
+      uint32_t code;
+      if constexpr (KV == kKvFp8) {
+        code = f32_to_fp8(clamp_fp8_range(y));
+      } else {
+        float r = rintf(y);
+        r = r > 127.0f ? 127.0f : (r < -128.0f ? -128.0f : r);
+        code = (uint32_t)(int32_t)r & 0xffu;
+      }
+      w |= code << (8 * i);
+    }
+    uint8_t* dst = (uint8_t*)(which ? p.v : p.k) + blk * p.kv_sblk + off * p.kv_stok + (int64_t)h * p.kv_shead + 4 * lane;
+    *(uint32_t*)dst = w;
+  }
+}
 
 __device__ __forceinline__ int clamp_page(const DecodeParams& p, int e) {
   return e < 0 ? 0 : (e >= p.num_blocks ? p.num_blocks - 1 : e);
@@ -66,8 +168,9 @@ __device__ __forceinline__ int mfma_page(const DecodeParams& p, int b, int tile_
 // K rows are loaded whole: each load instruction covers eight tokens' 128-byte rows (lane l: token
 // l / 8, 16 bytes at 16 (l % 8)), which the memory pipeline serves faster than the operand layout's half
 // rows of sixteen tokens; mfma_k_operand then rearranges them through LDS.
-template <bool PU>
-__device__ __forceinline__ void mfma_issue_k(const DecodeParams& p, int b, int h, int kk, int len, int lane, MChunk& c) {
+template <bool PU, bool FUSE>
+__device__ __forceinline__ void mfma_issue_k(const DecodeParams& p, int b, int h, int kk, int len, int lane, int first_new,
+                                             MChunk& c) {
   const int T0 = kk * kMChunk;
   const int r = lane >> 3, sg = lane & 7;
   const int64_t head_off = (int64_t)h * p.kv_shead + 16 * sg;
@@ -78,6 +181,15 @@ __device__ __forceinline__ void mfma_issue_k(const DecodeParams& p, int b, int h
       const int tok = min(T0 + 16 * t + 8 * j + r, len - 1);
       const int e = mfma_page<PU>(p, b, T0 + 16 * t, tok, len);
       c.k[t][j] = load16(p.k + (int64_t)e * p.kv_sblk + (int64_t)(tok & (p.P - 1)) * p.kv_stok + head_off);
+    }
+  }
+  if constexpr (FUSE) {
+    int qi;
+    c.nsel_k = new_row(kk, len, first_new, lane, qi);
+    if (c.nsel_k >= 0) {
+      const uint16_t* src = p.nk + (int64_t)b * p.n_sb + (int64_t)qi * p.n_sq + (int64_t)h * p.n_sh + 16 * sg;
+      c.nk[0] = load16((const uint8_t*)src);
+      c.nk[1] = load16((const uint8_t*)(src + 8));
     }
   }
 }
@@ -102,8 +214,9 @@ __device__ __forceinline__ void mfma_k_operand(const MChunk& c, U4 (&sk)[2][16][
   }
 }
 
-template <int SK, bool PU>
-__device__ __forceinline__ void mfma_issue_v(const DecodeParams& p, int b, int h, int kk, int len, int lane, MChunk& c) {
+template <int SK, bool PU, bool FUSE>
+__device__ __forceinline__ void mfma_issue_v(const DecodeParams& p, int b, int h, int kk, int len, int lane, int first_new,
+                                             MChunk& c) {
   const int T0 = kk * kMChunk;
   {
     const int r = lane >> 3, sg = lane & 7;
@@ -126,12 +239,22 @@ __device__ __forceinline__ void mfma_issue_v(const DecodeParams& p, int b, int h
     const int64_t so = (int64_t)e * p.sc_sblk + (int64_t)(tok & (p.P - 1)) * p.sc_stok + (int64_t)h * p.sc_shead;
     c.sc1 = ((lane >> 4) & 1 ? p.vs : p.ks)[so];
   }
+  if constexpr (FUSE) {
+    int qi;
+    c.nsel_v = new_row(kk, len, first_new, lane, qi);
+    if (c.nsel_v >= 0) {
+      const uint16_t* src = p.nv + (int64_t)b * p.n_sb + (int64_t)qi * p.n_sq + (int64_t)h * p.n_sh + 16 * (lane & 7);
+      c.nv[0] = load16((const uint8_t*)src);
+      c.nv[1] = load16((const uint8_t*)(src + 8));
+    }
+  }
 }
 
-template <int SK, bool PU>
-__device__ __forceinline__ void mfma_issue(const DecodeParams& p, int b, int h, int kk, int len, int lane, MChunk& c) {
-  mfma_issue_k<PU>(p, b, h, kk, len, lane, c);
-  mfma_issue_v<SK, PU>(p, b, h, kk, len, lane, c);
+template <int SK, bool PU, bool FUSE>
+__device__ __forceinline__ void mfma_issue(const DecodeParams& p, int b, int h, int kk, int len, int lane, int first_new,
+                                           MChunk& c) {
+  mfma_issue_k<PU, FUSE>(p, b, h, kk, len, lane, first_new, c);
+  mfma_issue_v<SK, PU, FUSE>(p, b, h, kk, len, lane, first_new, c);
 }
 
 // 4 x 4 byte transpose: w[i] byte j -> out[j] byte i.
@@ -191,12 +314,14 @@ struct MQ {
 // l (this lane's partial weight sum) and o[mu] (row n, channels 32 kq + 8 i + mu).
 // `after_scores` runs once the chunk's K registers are consumed (the caller issues the next chunk's K loads
 // there, so they fly during this chunk's softmax and value products).
-template <int KV, int SK, bool QS, typename AfterScores>
+template <int KV, int SK, bool QS, bool FUSE, typename AfterScores>
 __device__ __forceinline__ void mfma_compute(MChunk& c, U4 (&sk)[2][16][8], float (&ssc)[64], int kk, int lane,
                                              const typename MQ<KV, QS>::T (&qb)[MQ<KV, QS>::kOps], float qscale,
-                                             int rlen, float& m, float& l, f32x4 (&o)[8], AfterScores after_scores) {
+                                             int rlen, float& m, float& l, f32x4 (&o)[8], float ks_new, float vs_new,
+                                             AfterScores after_scores) {
   const int T0 = kk * kMChunk;
   const int kq = lane >> 4;
+  if constexpr (FUSE) substitute<KV>(c.k, c.nk, c.nsel_k, ks_new);
   U4 kr[2][2];
   mfma_k_operand(c, sk, lane, kr);
   // Per-token scales of this lane's score tokens 16 t + 4 kq + i: ks4[t][i] (K), vs4[t][i] (V).
@@ -270,6 +395,7 @@ __device__ __forceinline__ void mfma_compute(MChunk& c, U4 (&sk)[2][16][8], floa
   // V rows through the wave's LDS tile (the K operand's reads are done): lane (n', kq) reads channels
   // 8 n' .. 8 n' + 7 of its score tokens 16 t + 4 kq + i, with the K tile's segment swizzle.
   u32x2 vw[2][4];
+  if constexpr (FUSE) substitute<KV>(c.v, c.nv, c.nsel_v, vs_new);
   {
     const int r = lane >> 3, sg = lane & 7;
 #pragma unroll
@@ -340,7 +466,7 @@ __device__ __forceinline__ void mfma_load_q(const DecodeParams& p, int b, int h,
   }
 }
 
-template <int KV, int SK, bool PU, bool QS, int NW>
+template <int KV, int SK, bool PU, bool QS, int NW, bool FUSE>
 __global__ __launch_bounds__(NW * 64, kMfmaWavesPerSimd) void decode_mfma_kernel(const DecodeParams p) {
   constexpr int NT = NW * 64;
   constexpr int D = kHeadDim;
@@ -363,6 +489,7 @@ __global__ __launch_bounds__(NW * 64, kMfmaWavesPerSimd) void decode_mfma_kernel
   const int kq = lane >> 4, n = lane & 15;
   const int B = p.B;
 
+  if constexpr (FUSE) fused_append<KV, NT>(p);
   build_segment_line<NW, kMChunk>(p, s_prefix, s_len, s_wsum, p.piece_cost);
   zero_empty_sequences<NT>(p, s_prefix);
 
@@ -423,12 +550,16 @@ __global__ __launch_bounds__(NW * 64, kMfmaWavesPerSimd) void decode_mfma_kernel
   int rlen;
   MChunk cr;
   int len = sread(s_len[b]);
+  // Fused writes: the sequence's first new token (its new rows are the last fuse_q of its length) and the
+  // head's scales, which quantize them.
+  int first_new = FUSE ? load_uniform(p.lens + b) - p.fuse_q : 0;
+  float ks_new = FUSE ? load_uniform(p.ks + h) : 1.0f, vs_new = FUSE ? load_uniform(p.vs + h) : 1.0f;
   float qscale = p.qscale * (SK == kScaleHead ? load_uniform(p.ks + h) : 1.0f);
   mfma_load_q<KV, QS>(p, b, h, rows, len, lane, qb, rlen);
   {
     const int64_t seg_c0 = seg_start(b, h, span);
     const int k_end = (int)(min(c_end, seg_c0 + span) - seg_c0 - X);
-    if (k + wave < k_end) mfma_issue<SK, PU>(p, b, h, k + wave, len, lane, cr);
+    if (k + wave < k_end) mfma_issue<SK, PU, FUSE>(p, b, h, k + wave, len, lane, first_new, cr);
   }
 
   for (;;) {
@@ -445,10 +576,11 @@ __global__ __launch_bounds__(NW * 64, kMfmaWavesPerSimd) void decode_mfma_kernel
     // the next chunk's K loads are issued as soon as kk's scores are done, its V loads after kk's values.
     for (int kk = k + wave; kk < k_end;) {
       const int kn = kk + NW;
-      mfma_compute<KV, SK, QS>(cr, s_k[wave], s_sc[wave], kk, lane, qb, qscale, rlen, m, l, o, [&]() {
-        if (kn < k_end) mfma_issue_k<PU>(p, b, h, kn, len, lane, cr);
-      });
-      if (kn < k_end) mfma_issue_v<SK, PU>(p, b, h, kn, len, lane, cr);
+      mfma_compute<KV, SK, QS, FUSE>(cr, s_k[wave], s_sc[wave], kk, lane, qb, qscale, rlen, m, l, o, ks_new, vs_new,
+                                     [&]() {
+                                       if (kn < k_end) mfma_issue_k<PU, FUSE>(p, b, h, kn, len, lane, first_new, cr);
+                                     });
+      if (kn < k_end) mfma_issue_v<SK, PU, FUSE>(p, b, h, kn, len, lane, first_new, cr);
       kk = kn;
     }
 
@@ -487,9 +619,14 @@ __global__ __launch_bounds__(NW * 64, kMfmaWavesPerSimd) void decode_mfma_kernel
       more = kn_end > 0;
       if (more) {
         len = sread(s_len[b]);
+        if constexpr (FUSE) {
+          first_new = load_uniform(p.lens + b) - p.fuse_q;
+          ks_new = load_uniform(p.ks + h);
+          vs_new = load_uniform(p.vs + h);
+        }
         qscale = p.qscale * (SK == kScaleHead ? load_uniform(p.ks + h) : 1.0f);
         mfma_load_q<KV, QS>(p, b, h, rows, len, lane, qb, rlen);
-        if (wave < kn_end) mfma_issue<SK, PU>(p, b, h, wave, len, lane, cr);
+        if (wave < kn_end) mfma_issue<SK, PU, FUSE>(p, b, h, wave, len, lane, first_new, cr);
       }
     }
 
@@ -558,21 +695,30 @@ __global__ __launch_bounds__(NW * 64, kMfmaWavesPerSimd) void decode_mfma_kernel
   }
 }
 
-template <int KV, int SK, int NW>
+template <int KV, int SK, int NW, bool FUSE>
 static hipError_t launch_mfma_nw(const DecodeParams& p, bool pu, bool qs, hipStream_t stream, const LaunchEvents& ev) {
   dim3 grid(p.grid), block(NW * 64);
   const size_t lds = (size_t)(2 * p.B + 1) * sizeof(int);
-  if (pu && !qs) launch_kernel(decode_mfma_kernel<KV, SK, true, false, NW>, grid, block, lds, stream, ev, p);
-  else if (pu) launch_kernel(decode_mfma_kernel<KV, SK, true, true, NW>, grid, block, lds, stream, ev, p);
-  else if (!qs) launch_kernel(decode_mfma_kernel<KV, SK, false, false, NW>, grid, block, lds, stream, ev, p);
-  else launch_kernel(decode_mfma_kernel<KV, SK, false, true, NW>, grid, block, lds, stream, ev, p);
+  if (pu && !qs) launch_kernel(decode_mfma_kernel<KV, SK, true, false, NW, FUSE>, grid, block, lds, stream, ev, p);
+  else if (pu) launch_kernel(decode_mfma_kernel<KV, SK, true, true, NW, FUSE>, grid, block, lds, stream, ev, p);
+  else if (!qs) launch_kernel(decode_mfma_kernel<KV, SK, false, false, NW, FUSE>, grid, block, lds, stream, ev, p);
+  else launch_kernel(decode_mfma_kernel<KV, SK, false, true, NW, FUSE>, grid, block, lds, stream, ev, p);
   return hipGetLastError();
 }
 
 template <int KV, int SK>
 static hipError_t launch_mfma_sk(const DecodeParams& p, bool pu, bool qs, hipStream_t stream, const LaunchEvents& ev) {
-  if (mfma_waves(p.Q * p.G) == kMfmaManyRowWaves) return launch_mfma_nw<KV, SK, kMfmaManyRowWaves>(p, pu, qs, stream, ev);
-  return launch_mfma_nw<KV, SK, kDecodeWaves>(p, pu, qs, stream, ev);
+  const bool many = mfma_waves(p.Q * p.G) == kMfmaManyRowWaves;
+  if constexpr (SK == kScaleHead) {
+    if (p.fuse_q > 0) {
+      if (many) return launch_mfma_nw<KV, SK, kMfmaManyRowWaves, true>(p, pu, qs, stream, ev);
+      return launch_mfma_nw<KV, SK, kDecodeWaves, true>(p, pu, qs, stream, ev);
+    }
+  } else {
+    if (p.fuse_q > 0) return hipErrorInvalidValue;  // fused writes take per-head scales
+  }
+  if (many) return launch_mfma_nw<KV, SK, kMfmaManyRowWaves, false>(p, pu, qs, stream, ev);
+  return launch_mfma_nw<KV, SK, kDecodeWaves, false>(p, pu, qs, stream, ev);
 }
 
 hipError_t launch_decode_mfma(const DecodeParams& p, int kv_dtype, int scale_kind, hipStream_t stream,

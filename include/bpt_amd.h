@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define BPT_ABI_VERSION 11
+#define BPT_ABI_VERSION 12
 
 /* return codes */
 #define BPT_OK 0
@@ -350,6 +350,15 @@ int bpt_paged_prepare(const bpt_prepare_args* args, void* stream);
 
 /* Quantize-on-write of new K/V rows into their (page, slot). */
 int bpt_quant_append(const bpt_append_args* args, void* stream);
+
+/* Store, then attend (replaces integration/kv_cache.py:160-192, the cache's attend: _append then the decode
+ * call): the rows of `append` are written as bpt_quant_append writes them and `decode` attends the pools with
+ * them in place. When the decode runs on the matrix-core kernel with per-head scales over the same pools, the
+ * rows are bf16 (16-byte aligned) and are the last Q <= 8 tokens of every sequence (their write slots are the
+ * block table's pages for positions context_len - Q .. context_len - 1), head dim 128, context lengths given,
+ * no len_offset and no merge partial, one launch does both: it stores the rows and uses their codes for those
+ * tokens directly. Otherwise bpt_quant_append then bpt_paged_decode (two launches). Errors as theirs. */
+int bpt_paged_append_decode(const bpt_append_args* append, const bpt_decode_args* decode, void* stream);
 
 /* Host-only: validate a KIVI call, fill grid_groups, report workspace and counter sizes in bytes. */
 int bpt_kivi_plan(bpt_kivi_args* args, size_t* workspace_bytes, size_t* counters_bytes);

@@ -1,0 +1,101 @@
+"""GPU: store-then-attend in one call (bpt_amd.paged_append_decode -> bpt_paged_append_decode) against the two
+calls it replaces, quantize_append then paged_decode_attention, on copies of the same pools.
+
+Where the matrix-core kernel stores the new rows itself (per-head scales, bf16 rows of the last Q <= 8 tokens),
+the pools must come out byte for byte the same and the outputs bit for bit the same (the same codes go through
+the same kernel arithmetic). The other layouts (per-token scales, BF16 caches, the vector kernel) take the two
+launches inside the call and must match too. The codes themselves are pinned to the oracle's quantizers by
+test_gpu_quant.py, and the attention by test_gpu_decode.py.
+"""
+
+import pytest
+import torch
+
+from test_gpu_decode import DEV, make_case
+
+pytestmark = pytest.mark.gpu
+
+
+def new_rows(c, nq, seed):
+    """New bf16 rows [B, Q, Hkv, D] and their slots: the table's pages for the last Q positions of each length."""
+    b = len(c["lens"])
+    hkv, d = c["k"].shape[2], c["k"].shape[3]
+    page = c["k"].shape[1]
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    k = (torch.randn((b, nq, hkv, d), generator=g, device=DEV) * 2).to(torch.bfloat16)
+    v = (torch.randn((b, nq, hkv, d), generator=g, device=DEV) * 2).to(torch.bfloat16)
+    lens = c["lens"].long()
+    pos = (lens[:, None] - nq + torch.arange(nq, device=DEV)[None]).clamp(min=0)
+    blocks = torch.gather(c["table"].long(), 1, pos // page).to(torch.int32)
+    offsets = (pos % page).to(torch.int32)
+    return k, v, blocks, offsets
+
+
+def both_ways(c, k, v, blocks, offsets, max_context, scale=0.09):
+    from bpt_amd import paged_append_decode, paged_decode_attention, quantize_append
+
+    pools = []
+    outs = []
+    for fused in (False, True):
+        kc, vc = c["k"].clone(), c["v"].clone()
+        ks = None if c["ks"] is None else c["ks"].clone()
+        vs = None if c["vs"] is None else c["vs"].clone()
+        if fused:
+            out = paged_append_decode(c["q"], k, v, kc, vc, c["table"], c["lens"], ks, vs, blocks, offsets,
+                                      scale=scale, max_context=max_context)
+        else:
+            quantize_append(k, v, kc, vc, ks, vs, blocks, offsets)
+            out = paged_decode_attention(c["q"], kc, vc, c["table"], c["lens"], ks, vs, scale=scale,
+                                         max_context=max_context)
+        torch.cuda.synchronize()
+        pools.append([t.view(torch.uint8) if t.dtype != torch.float32 else t for t in (kc, vc, ks, vs) if t is not None])
+        outs.append(out)
+    for a, b in zip(*pools):
+        assert torch.equal(a, b), "the pools differ after the store"
+    assert torch.equal(outs[0], outs[1]), f"outputs differ: max {(outs[0].float() - outs[1].float()).abs().max()}"
+
+
+@pytest.mark.parametrize("fmt,nq,hq,hkv", [("fp8", 1, 16, 8), ("fp8", 5, 16, 8), ("fp8", 1, 32, 8), ("fp8", 8, 16, 8),
+                                           ("int8", 3, 16, 8), ("int8", 5, 16, 8)])
+@pytest.mark.parametrize("page", [8, 16, 32])
+def test_fused_store_matches_store_then_decode(fmt, nq, hq, hkv, page):
+    """Matrix-core cases (2 .. 16 rows per KV head): the kernel stores the rows and uses them in place."""
+    lengths = [max(t, nq) for t in (1 + nq, 47, 300, 1024, 33, 2000, 64, 95)]
+    c = make_case(fmt, lengths, hq=hq, hkv=hkv, nq=nq, page=page, scales="head", seed=nq + page)
+    k, v, blocks, offsets = new_rows(c, nq, seed=7)
+    both_ways(c, k, v, blocks, offsets, max_context=max(lengths))
+    both_ways(c, k, v, blocks, offsets, max_context=max(lengths) + 700)
+
+
+def test_fused_store_with_lengths_beyond_max_context():
+    """Sequences longer than max_context: their new rows are stored but not attended, as the two calls do."""
+    lengths = [900, 300, 1500, 64]
+    c = make_case("fp8", lengths, nq=1, scales="head", seed=3)
+    k, v, blocks, offsets = new_rows(c, 1, seed=8)
+    both_ways(c, k, v, blocks, offsets, max_context=512)
+
+
+def test_fused_store_of_single_token_sequences():
+    lengths = [1, 1, 2, 1]
+    c = make_case("fp8", lengths, nq=1, scales="head", seed=4)
+    k, v, blocks, offsets = new_rows(c, 1, seed=9)
+    both_ways(c, k, v, blocks, offsets, max_context=2)
+
+
+@pytest.mark.parametrize("fmt,scales,nq,hq", [("int8", "token", 1, 16), ("fp8", "token", 2, 16), ("bf16", None, 1, 16),
+                                              ("fp8", "head", 1, 8), ("int8", "head", 1, 16)])
+def test_other_layouts_take_the_two_launches(fmt, scales, nq, hq):
+    """Per-token scales, BF16 caches and vector-kernel shapes (one FP8 row per KV head, INT8 with 2 rows):
+    the call stores, then attends, with the same results."""
+    lengths = [70, 1, 513, 256]
+    c = make_case(fmt, lengths, hq=hq, nq=nq, scales=scales or "head", seed=5)
+    k, v, blocks, offsets = new_rows(c, nq, seed=10)
+    both_ways(c, k, v, blocks, offsets, max_context=600)
+
+
+def test_f32_rows_take_the_two_launches():
+    """Rows in f32 do not fuse (the kernel reads bf16 rows); the call still stores them and attends."""
+    lengths = [200, 40]
+    c = make_case("fp8", lengths, nq=1, scales="head", seed=6)
+    k, v, blocks, offsets = new_rows(c, 1, seed=11)
+    both_ways(c, k.float(), v.float(), blocks, offsets, max_context=200)
