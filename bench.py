@@ -76,6 +76,28 @@ def append_call(w):
     return write, {"read": b * hkv * 128 * 2 * 2, "written": b * hkv * (128 + scale_bytes) * 2}
 
 
+def fused_call(w, out):
+    """The workload's decode call as the cache's store-then-attend (paged_append_decode): new bf16 rows for
+    the last token of every sequence, written to its slot and attended in the same launch."""
+    import torch
+
+    from bpt_amd import paged_append_decode
+
+    b, hkv, page = w.shape.batch, w.shape.kv_heads, w.k_cache.shape[1]
+    g = torch.Generator(device="cuda:0").manual_seed(6)
+    k_new = torch.randn((b, 1, hkv, 128), generator=g, device="cuda:0").to(torch.bfloat16)
+    v_new = torch.randn((b, 1, hkv, 128), generator=g, device="cuda:0").to(torch.bfloat16)
+    pos = w.context_lens.long()[:, None] - 1
+    blocks = torch.gather(w.block_table.long(), 1, pos // page).to(torch.int32)
+    offsets = (pos % page).to(torch.int32)
+    pargs, kw = w.args(), w.kwargs()
+
+    def call():
+        paged_append_decode(pargs[0], k_new, v_new, *pargs[1:7], blocks, offsets, out=out, **kw)
+
+    return call
+
+
 def profile_pass(args) -> int:
     """A short run for rocprofv3: cold decode calls on the workload, then three 256 MiB copies.
 
@@ -134,7 +156,7 @@ def profile_pass(args) -> int:
             from bpt_amd import cascade_decode_attention
 
             kw = {**kw, "prefix_pages": w.shape.shared_prefix_pages}
-        write = append_call(w)[0] if args.append else None
+        write = append_call(w)[0] if args.append else (fused_call(w, out) if args.fused else None)
         for _ in range(args.warmup + args.steps):
             flush.run()
             if write is not None:
@@ -550,6 +572,8 @@ def main() -> int:
     ap.add_argument("--profile", action="store_true", help="short run for rocprofv3 (no JSON line)")
     ap.add_argument("--cascade", action="store_true", help="with --profile: the shared-prefix cascade call")
     ap.add_argument("--append", action="store_true", help="with --profile: the step's quantize-on-write call")
+    ap.add_argument("--fused", action="store_true",
+                    help="with --profile: the decode call with the last token's store in the same launch")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))

@@ -352,6 +352,7 @@ def paged_append_decode(
     *,
     scale: float,
     max_context: int,
+    num_splits: int | None = None,
     out: torch.Tensor | None = None,
     out_dtype: torch.dtype = torch.bfloat16,
 ) -> torch.Tensor:
@@ -366,7 +367,8 @@ def paged_append_decode(
     a, dev = _append_args(k, v, k_cache, v_cache, k_scale, v_scale, write_blocks, write_offsets)
     _require(q.device == dev, f"q is on {q.device}, the new rows on {dev}")
     return paged_decode_attention(q, k_cache, v_cache, block_table, context_lens, k_scale, v_scale, scale=scale,
-                                  max_context=max_context, out=out, out_dtype=out_dtype, _append=a)
+                                  max_context=max_context, num_splits=num_splits, out=out, out_dtype=out_dtype,
+                                  _append=a)
 
 
 def paged_prepare(

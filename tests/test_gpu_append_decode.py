@@ -87,7 +87,7 @@ def test_fused_store_of_single_token_sequences():
 def test_other_layouts_take_the_two_launches(fmt, scales, nq, hq):
     """Per-token scales, BF16 caches and vector-kernel shapes (one FP8 row per KV head, INT8 with 2 rows):
     the call stores, then attends, with the same results."""
-    lengths = [70, 1, 513, 256]
+    lengths = [max(t, nq) for t in (70, 1, 513, 256)]  # every new row has a slot of its own
     c = make_case(fmt, lengths, hq=hq, nq=nq, scales=scales or "head", seed=5)
     k, v, blocks, offsets = new_rows(c, nq, seed=10)
     both_ways(c, k, v, blocks, offsets, max_context=600)
