@@ -31,7 +31,7 @@ def new_rows(c, nq, seed):
     return k, v, blocks, offsets
 
 
-def both_ways(c, k, v, blocks, offsets, max_context, scale=0.09):
+def both_ways(c, k, v, blocks, offsets, max_context, scale=0.09, num_splits=None):
     from bpt_amd import paged_append_decode, paged_decode_attention, quantize_append
 
     pools = []
@@ -42,11 +42,11 @@ def both_ways(c, k, v, blocks, offsets, max_context, scale=0.09):
         vs = None if c["vs"] is None else c["vs"].clone()
         if fused:
             out = paged_append_decode(c["q"], k, v, kc, vc, c["table"], c["lens"], ks, vs, blocks, offsets,
-                                      scale=scale, max_context=max_context)
+                                      scale=scale, max_context=max_context, num_splits=num_splits)
         else:
             quantize_append(k, v, kc, vc, ks, vs, blocks, offsets)
             out = paged_decode_attention(c["q"], kc, vc, c["table"], c["lens"], ks, vs, scale=scale,
-                                         max_context=max_context)
+                                         max_context=max_context, num_splits=num_splits)
         torch.cuda.synchronize()
         pools.append([t.view(torch.uint8) if t.dtype != torch.float32 else t for t in (kc, vc, ks, vs) if t is not None])
         outs.append(out)
@@ -65,6 +65,15 @@ def test_fused_store_matches_store_then_decode(fmt, nq, hq, hkv, page):
     k, v, blocks, offsets = new_rows(c, nq, seed=7)
     both_ways(c, k, v, blocks, offsets, max_context=max(lengths))
     both_ways(c, k, v, blocks, offsets, max_context=max(lengths) + 700)
+
+
+@pytest.mark.parametrize("num_splits", [1, 7, 64])
+def test_fused_store_with_fixed_split_counts(num_splits):
+    """A caller's split count (the partitions that hold a sequence's last chunk change with it)."""
+    lengths = [1500, 2, 700, 4096, 31, 333]
+    c = make_case("fp8", lengths, nq=2, scales="head", seed=12)
+    k, v, blocks, offsets = new_rows(c, 2, seed=13)
+    both_ways(c, k, v, blocks, offsets, max_context=4096, num_splits=num_splits)
 
 
 def test_fused_store_with_lengths_beyond_max_context():
