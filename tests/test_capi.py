@@ -233,3 +233,24 @@ def test_quantize_append_rejects_bad_tensors(built_lib):
         quantize_append(rows, rows, k_cache, v_cache, ks, vs, slots, slots)
     with pytest.raises(ValueError, match="per-token-head scales"):
         quantize_append(rows, rows, k_cache, v_cache, ks[:3], vs[:3], slots, slots)
+
+
+def test_append_decode_checks_both_argument_blocks_before_any_gpu_call(built_lib):
+    """bpt_paged_append_decode refuses a stale or missing argument block on the host."""
+    stale = _lib.AppendArgs()
+    stale.struct_size = 12
+    with pytest.raises(ValueError, match="stale binding"):
+        _lib.check(built_lib.bpt_paged_append_decode(ctypes.byref(stale), None, None))
+    empty = _lib.AppendArgs()  # no rows to store: only the decode block is left to check
+    empty.struct_size = ctypes.sizeof(_lib.AppendArgs)
+    empty.kv_dtype, empty.scale_kind, empty.src_dtype, empty.slot_dtype = 1, 1, 0, 0
+    empty.num_kv_heads, empty.head_dim, empty.num_blocks, empty.page_size = 8, 128, 4, 16
+    with pytest.raises(ValueError, match="decode args is NULL"):
+        _lib.check(built_lib.bpt_paged_append_decode(ctypes.byref(empty), None, None))
+    from bpt_amd import paged_append_decode
+
+    q, k, v, table, lens, ks, vs = cpu_case()
+    rows = torch.zeros((q.shape[0], 1, 8, 128), dtype=torch.bfloat16)
+    slots = torch.zeros((q.shape[0], 1), dtype=torch.int32)
+    with pytest.raises(ValueError, match="on a GPU"):
+        paged_append_decode(q, rows, rows, k, v, table, lens, ks, vs, slots, slots, scale=0.1, max_context=16)
