@@ -631,15 +631,36 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void kivi_decode_kernel(const
     return k0 + (min(c_end, seg_c0 + split_end) - c0);
   };
 
+  // Chunks in flight per wave. A 4-bit chunk is 4 KiB: with one in flight, the chip's waves hold too few bytes
+  // in flight to cover the memory latency, so each wave keeps two chunks going (a second register set; there
+  // is room for it at up to 2 rows, 255 VGPRs).
+  constexpr int DEPTH = (FMT == kKivi4 && RP <= 2) ? 2 : 1;
   float qf[CPL];
-  KChunk<FMT, CPL> cr;
+  KChunk<FMT, CPL> cr, cr2;
   const LaneOffsets lo = lane_offsets<FMT, RP, CPL>(p, lane);
   Head hd = head_of(p, b, h);
   int len = sread(s_len[b]);
   load_q_fold<RP, CPL>(p, b, h, lane, qf);
+  // Two sets: the piece's first chunks of this wave go in flight, k0 + wave into cr, k0 + wave + NW into cr2.
+  // Every load is issued (a wave without the chunk loads chunk k0 again) and in the loop's order (the grids
+  // and K, then V; cr, then cr2): the compiler sizes the loop's waits for the loads on every path into it,
+  // so a skipped or reordered load here would make every chunk of the loop wait for more of the loads behind.
+  auto prime2 = [&](int k0, int k_end0) __attribute__((always_inline)) {
+    const int c0 = k0 + wave < k_end0 ? k0 + wave : k0;
+    const int c1 = k0 + wave + NW < k_end0 ? k0 + wave + NW : k0;
+    issue_k<FMT, CPL>(p, hd, lo, c0, cr);
+    __builtin_amdgcn_sched_barrier(0);
+    issue_v<FMT, CPL>(p, hd, lo, c0, cr);
+    __builtin_amdgcn_sched_barrier(0);
+    issue_k<FMT, CPL>(p, hd, lo, c1, cr2);
+    __builtin_amdgcn_sched_barrier(0);
+    issue_v<FMT, CPL>(p, hd, lo, c1, cr2);
+  };
   {
     const int k_end = piece_end(k, c);
-    if (k + wave < k_end) {
+    if constexpr (DEPTH == 2) {
+      prime2(k, k_end);
+    } else if (k + wave < k_end) {
       issue_k<FMT, CPL>(p, hd, lo, k + wave, cr);
       issue_v<FMT, CPL>(p, hd, lo, k + wave, cr);
     }
@@ -667,23 +688,50 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void kivi_decode_kernel(const
       read_fold<FMT, RP>(n, kq, G, s_qh[wave], s_ql[wave], s_kz[wave], s_inv[wave], qh, ql, kzp, inv);
     }
 
-    // Chunks k + wave, k + wave + NW, ... of this piece: chunk kk is in flight on entry to its iteration; the
-    // next chunk's grids and K go out once kk's scores are done, its V after kk's value products.
-    for (int kk = k + wave; kk < k_end;) {
-      const int kn = kk + NW;
-      if constexpr (F::kQuant) {
-        fold<FMT, RP, CPL>(qf, cr.gs, cr.gz, p.qscale, lane, s_qh[wave], s_ql[wave], s_kz[wave], s_inv[wave]);
+    if constexpr (DEPTH == 1) {
+      // Chunks k + wave, k + wave + NW, ... of this piece: chunk kk is in flight on entry to its iteration;
+      // the next chunk's grids and K go out once kk's scores are done, its V after kk's value products.
+      for (int kk = k + wave; kk < k_end;) {
+        const int kn = kk + NW;
+        if constexpr (F::kQuant) {
+          fold<FMT, RP, CPL>(qf, cr.gs, cr.gz, p.qscale, lane, s_qh[wave], s_ql[wave], s_kz[wave], s_inv[wave]);
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+          __builtin_amdgcn_wave_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+          read_fold<FMT, RP>(n, kq, G, s_qh[wave], s_ql[wave], s_kz[wave], s_inv[wave], qh, ql, kzp, inv);
+        }
+        compute<FMT, CPL>(cr, kk, len, lane, qh, ql, kzp, inv, m, l, o, [&]() {
+          if (kn < k_end) issue_k<FMT, CPL>(p, hd, lo, kn, cr);
+        });
+        if (kn < k_end) issue_v<FMT, CPL>(p, hd, lo, kn, cr);
+        kk = kn;
+        if constexpr (F::kQuant) __builtin_amdgcn_wave_barrier();  // the LDS fold buffers are rewritten next
+      }
+    } else {
+      // The same with two sets: chunk kk is in flight in set cur on entry to its step, and chunk kk + 2 NW
+      // takes the set over (past the piece, chunk kk again, as in prime2). The sets alternate, cr first on
+      // every piece: pairs, then an odd last chunk. (A loop that may leave between its two steps makes the
+      // compiler assume a path on which cr2's loads were not issued, and wait for them before every pair.)
+      auto step = [&](KChunk<FMT, CPL>& cur, int kk) __attribute__((always_inline)) {
+        const int kn = kk + 2 * NW;
+        const int kl = kn < k_end ? kn : kk;
+        fold<FMT, RP, CPL>(qf, cur.gs, cur.gz, p.qscale, lane, s_qh[wave], s_ql[wave], s_kz[wave], s_inv[wave]);
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         read_fold<FMT, RP>(n, kq, G, s_qh[wave], s_ql[wave], s_kz[wave], s_inv[wave], qh, ql, kzp, inv);
+        compute<FMT, CPL>(cur, kk, len, lane, qh, ql, kzp, inv, m, l, o, [&]() { issue_k<FMT, CPL>(p, hd, lo, kl, cur); });
+        issue_v<FMT, CPL>(p, hd, lo, kl, cur);
+        __builtin_amdgcn_wave_barrier();  // the LDS fold buffers are rewritten next
+      };
+      const int first = k + wave;
+      const int cnt = first < k_end ? (k_end - first + NW - 1) / NW : 0;
+      int kk = first;
+      for (int i = 1; i < cnt; i += 2, kk += 2 * NW) {
+        step(cr, kk);
+        step(cr2, kk + NW);
       }
-      compute<FMT, CPL>(cr, kk, len, lane, qh, ql, kzp, inv, m, l, o, [&]() {
-        if (kn < k_end) issue_k<FMT, CPL>(p, hd, lo, kn, cr);
-      });
-      if (kn < k_end) issue_v<FMT, CPL>(p, hd, lo, kn, cr);
-      kk = kn;
-      if constexpr (F::kQuant) __builtin_amdgcn_wave_barrier();  // the LDS fold buffers are rewritten next
+      if (cnt & 1) step(cr, kk);
     }
 
     // The next piece (if any): its first chunk (and q rows, for a new KV head) go in flight now.
@@ -709,7 +757,9 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void kivi_decode_kernel(const
         load_q_fold<RP, CPL>(p, b, h, lane, qf);
       }
       const int k_next_end = piece_end(k, c_next);
-      if (k + wave < k_next_end) {
+      if constexpr (DEPTH == 2) {
+        prime2(k, k_next_end);
+      } else if (k + wave < k_next_end) {
         issue_k<FMT, CPL>(p, hd, lo, k + wave, cr);
         issue_v<FMT, CPL>(p, hd, lo, k + wave, cr);
       }
