@@ -107,6 +107,20 @@ def test_each_rows_length(bits):
     assert got[3].abs().sum().item() == 0  # no tokens: zeros, not NaN
 
 
+@pytest.mark.parametrize("q_heads", [8, 16])
+def test_four_bit_chunk_pairs(q_heads):
+    """The 4-bit kernel at 1 or 2 query heads per KV head keeps two chunks in flight per wave, walks them in
+    pairs plus an odd last one and reloads a chunk past a piece's end. Ragged rows over ~11 chunks per
+    workgroup give waves 0 .. 3 chunks per piece; the splits of 1, 3, 5 and 32 chunks end pieces between
+    a pair's two steps."""
+    lengths = [4096, 4000, 3100, 2049, 1500, 999, 513, 64, 33, 1, 0, 2047]
+    dev, ref = make_cache(len(lengths), 8, 4096, 4, seed=21)
+    q, qn = make_q(len(lengths), q_heads, 22)
+    check(q, qn, dev, ref, lengths)
+    for split in (32, 96, 160, 1024):
+        check(q, qn, dev, ref, lengths, split=split)
+
+
 @pytest.mark.parametrize("q_heads,kv_heads", [(32, 8), (24, 8), (40, 8), (64, 4)])
 @pytest.mark.parametrize("bits", [4, 8])
 def test_query_heads_per_kv_head(q_heads, kv_heads, bits):
