@@ -26,7 +26,7 @@ FP8 unscaled), INT8 with dynamic per-(token, head) scales amax/127 paged like th
 
 from __future__ import annotations
 
-import math
+import heapq
 from dataclasses import dataclass
 from typing import Any
 
@@ -39,7 +39,7 @@ HEAD_DIM = 128  # the one head size the paged decode kernels are built for
 
 
 class OutOfBlocksError(RuntimeError):
-    """The pool has no free block: the scheduler must wait for sequences to finish (or preempt one)."""
+    """A reservation asked for more blocks (or sequence slots) than are free right now."""
 
 
 @dataclass(frozen=True)
@@ -112,54 +112,66 @@ class PagedQuantKVCache:
             if k_scale is not None or v_scale is not None:
                 raise ValueError("a bfloat16 cache takes no scales")
             self.k_scale = self.v_scale = [None] * self.num_layers
-        self.free_blocks = list(range(num_blocks - 1, -1, -1))  # a stack: pop() hands out block 0 first
-        self.tables: dict[Any, list[int]] = {}  # sequence id -> its block table
-        # The same tables on the device: one row ("slot") per live sequence, and its reserved block count.
+        # Allocation state. Free block ids live in a min-heap: the lowest free id is granted first (block 0 on a
+        # fresh pool) and a released block is granted again before any higher one. `tables` maps each live
+        # sequence to the physical blocks of its logical blocks 0, 1, ...; `free_blocks` is the heap itself
+        # (only its length means anything to a scheduler).
+        self.free_blocks: list[int] = list(range(num_blocks))
+        self.tables: dict[Any, list[int]] = {}
+        # The device mirror of `tables`: row `slot_of[seq]` of table_dev holds the sequence's block ids and
+        # reserved_dev[slot] how many of them are valid. Slots are granted lowest first as well.
         self.max_seqs = max_seqs
         self.max_blocks_per_seq = min(num_blocks, 4096) if max_blocks_per_seq is None else max_blocks_per_seq
         self.table_dev = torch.zeros((max_seqs, self.max_blocks_per_seq), dtype=torch.int32, device=self.device)
         self.reserved_dev = torch.zeros(max_seqs, dtype=torch.int32, device=self.device)
         self.slot_of: dict[Any, int] = {}
-        self.free_slots = list(range(max_seqs - 1, -1, -1))
+        self.free_slots: list[int] = list(range(max_seqs))
         self._rows_key: tuple | None = None  # the rows of the last prepare and their device slots
         self._rows_slots: torch.Tensor | None = None
 
-    # -- memory management (host side) -----------------------------------------------------------------------
+    # -- block allocation ---------------------------------------------------------------------------------------
 
     def blocks_needed(self, num_tokens: int) -> int:
-        return math.ceil(num_tokens / self.block_size)
+        """Blocks that hold positions [0, num_tokens)."""
+        return -(-num_tokens // self.block_size)
+
+    def _shortfall(self, seq_id: Any, num_tokens: int) -> int:
+        """Blocks `seq_id` lacks for num_tokens positions (negative or zero: it has enough)."""
+        return self.blocks_needed(num_tokens) - len(self.tables.get(seq_id, ()))
 
     def can_reserve(self, seq_id: Any, num_tokens: int) -> bool:
-        have = len(self.tables.get(seq_id, []))
-        return self.blocks_needed(num_tokens) - have <= len(self.free_blocks)
+        return self._shortfall(seq_id, num_tokens) <= len(self.free_blocks)
 
     def reserve(self, seq_id: Any, num_tokens: int) -> None:
-        """Make sure `seq_id` owns enough blocks to hold positions [0, num_tokens). New blocks are also written to
-        the sequence's row of the device table (call it outside graph capture: it copies from the host)."""
-        table = self.tables.get(seq_id)
-        missing = self.blocks_needed(num_tokens) - (len(table) if table is not None else 0)
-        if missing > len(self.free_blocks):
-            raise OutOfBlocksError(f"need {missing} blocks, {len(self.free_blocks)} free")
-        if table is None:
-            if not self.free_slots:
-                raise OutOfBlocksError(f"all {self.max_seqs} sequence slots are in use")
-            self.slot_of[seq_id] = self.free_slots.pop()
-            table = self.tables[seq_id] = []
-        if len(table) + max(missing, 0) > self.max_blocks_per_seq:
+        """Grow `seq_id`'s block table until it covers positions [0, num_tokens), granting the lowest free blocks,
+        and mirror the new entries into the sequence's device row (a host-to-device copy: call it outside graph
+        capture). Raises OutOfBlocksError, changing nothing, when the pool or the slots run out."""
+        grow = self._shortfall(seq_id, num_tokens)
+        if grow > len(self.free_blocks):
+            raise OutOfBlocksError(f"sequence {seq_id!r} needs {grow} more blocks, the pool has {len(self.free_blocks)}")
+        owned = self.tables.get(seq_id)
+        if owned is None and not self.free_slots:
+            raise OutOfBlocksError(f"no sequence slot left (all {self.max_seqs} are live)")
+        have = 0 if owned is None else len(owned)
+        if have + max(grow, 0) > self.max_blocks_per_seq:
             raise ValueError(f"sequence {seq_id!r} would need more than {self.max_blocks_per_seq} blocks")
-        start = len(table)
-        table.extend(self.free_blocks.pop() for _ in range(missing))
-        if missing > 0:
-            slot = self.slot_of[seq_id]
-            self.table_dev[slot, start : len(table)] = torch.tensor(table[start:], dtype=torch.int32)
-        self.reserved_dev[self.slot_of[seq_id]] = len(table)
+        if owned is None:
+            owned = self.tables[seq_id] = []
+            self.slot_of[seq_id] = heapq.heappop(self.free_slots)
+        slot = self.slot_of[seq_id]
+        if grow > 0:
+            granted = [heapq.heappop(self.free_blocks) for _ in range(grow)]
+            owned += granted
+            self.table_dev[slot, have : have + grow] = torch.tensor(granted, dtype=torch.int32)
+        self.reserved_dev[slot] = len(owned)
 
     def free(self, seq_id: Any) -> None:
-        """Return a finished sequence's blocks (and its slot) to the pool."""
-        self.free_blocks.extend(reversed(self.tables.pop(seq_id, [])))
+        """Release a finished sequence: its blocks and its device slot become grantable again."""
+        for block in self.tables.pop(seq_id, ()):
+            heapq.heappush(self.free_blocks, block)
         slot = self.slot_of.pop(seq_id, None)
         if slot is not None:
-            self.free_slots.append(slot)
+            heapq.heappush(self.free_slots, slot)
 
     def bytes_per_token(self) -> int:
         """Bytes one token occupies across all layers and KV heads (codes, plus INT8's per-token scales)."""
@@ -174,8 +186,9 @@ class PagedQuantKVCache:
 
         Host positions are checked on the host first, as engine/kv_cache.py:140-146 does (consecutive,
         non-negative, reserved), and give the reference's exact kv_len and table width. Device positions are
-        never read back: kv_len is then the rows' reserved tokens (a bound the launch is sized by), a position
-        outside its row's reserved blocks gets no write slot and lengths are clamped to the reserved tokens.
+        never read back: kv_len is then the rows' reserved tokens (a bound the launch is sized by), lengths are
+        clamped to the reserved tokens, and a row whose positions run past its reserved blocks (or are out of
+        order) gets no write slots: such a step stores nothing for it and attends its reserved tokens.
         On a GPU cache the tables come from one kernel (bpt_paged_prepare); a CPU cache (allocator tests) builds
         the same tables with torch index operations."""
         if positions.dim() != 2 or positions.shape[0] != len(rows):
