@@ -359,10 +359,12 @@ def paged_append_decode(
     """Store the new rows k, v [B, Q, Hkv, D] (as quantize_append), then attend (as paged_decode_attention):
     the cache's store-then-attend (integration/kv_cache.py:160-192).
 
-    One launch when the decode runs on the matrix-core kernel with per-head scales and the rows are the last
-    Q <= 8 tokens of every sequence (write slots = the block table's pages for positions context_len - Q ..
-    context_len - 1, as paged_prepare produces them), bf16, head dim 128: the kernel stores the codes and uses
-    them for those tokens directly. Otherwise the two calls, in order.
+    The rows are the last Q tokens of each sequence (row i of sequence b is token context_lens[b] - Q + i), and a
+    row is stored only where the decode reads that token (its write slot is the block table's page and offset for
+    it, as paged_prepare produces them); a row with no slot (-1) or a slot elsewhere is not stored. One launch when
+    the decode runs on the matrix-core kernel with per-head scales, Q <= 8, bf16 rows, head dim 128: the kernel
+    stores the codes and uses them for those tokens directly. Otherwise the store, then the decode, with the
+    same results.
     """
     a, dev = _append_args(k, v, k_cache, v_cache, k_scale, v_scale, write_blocks, write_offsets)
     _require(q.device == dev, f"q is on {q.device}, the new rows on {dev}")
@@ -385,7 +387,9 @@ def paged_prepare(
     """Per-forward paged metadata on the device (bpt_paged_prepare; engine/kv_cache.py:140-156 without the host
     round trip): from each row's slot of the device table [num_slots, max_blocks] (reserved[slot] blocks held)
     and the positions [B, Q], fill block_table [B, n_blocks] (padded with block 0), write_blocks / write_offsets
-    [B, Q] (-1 outside the reserved blocks) and context_lens [B]. One launch, no host read."""
+    [B, Q] and context_lens [B] (the last position + 1, clamped to the reserved tokens). A position gets a write
+    block only when it is its row's token context_len - Q + i inside the reserved blocks (-1 otherwise: positions
+    past the reservation or out of order store nothing). One launch, no host read."""
     _require(table.dtype == torch.int32 and table.dim() == 2 and table.stride(1) == 1, "table: int32 [slots, blocks]")
     _require(reserved.dtype == torch.int32 and reserved.is_contiguous() and reserved.numel() == table.shape[0],
              "reserved: int32 [slots]")

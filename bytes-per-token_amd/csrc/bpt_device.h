@@ -174,4 +174,16 @@ __device__ __forceinline__ int64_t load_index(const void* base, int64_t idx, boo
   return i64 ? ((const int64_t*)base)[idx] : (int64_t)((const int32_t*)base)[idx];
 }
 
+// Whether pool slot (blk, off) is where the paged decode reads token `tok` of the sequence whose block-table
+// row starts at entry `row_entry`: blk is the token's block-table entry clamped into the pool (as the decode
+// kernels clamp it) and off its offset in the page. A token before the sequence or past the table's width has
+// no slot. Int64 tables are read by their low word, as the decode kernels read them.
+__device__ __forceinline__ bool slot_is_token(const void* table, int64_t row_entry, bool table_i64, int max_blocks,
+                                              int num_blocks, int logP, int64_t tok, int64_t blk, int64_t off) {
+  if (tok < 0 || (tok >> logP) >= max_blocks) return false;
+  int e = ((const int32_t*)table)[(row_entry + (tok >> logP)) << (table_i64 ? 1 : 0)];
+  e = e < 0 ? 0 : (e >= num_blocks ? num_blocks - 1 : e);
+  return blk == e && off == (tok & ((int64_t(1) << logP) - 1));
+}
+
 }  // namespace bpt

@@ -190,6 +190,13 @@ struct AppendParams {
   int64_t sc_sblk, sc_stok, sc_shead;  // elements
   int B, Q, Hkv, P, num_blocks;
   int src_dtype, slot_i64;
+  // in_place: store only the rows whose slot is where the decode reads the sequence's token lens[b] - Q + qi
+  // (slot_is_token), reading the decode's block table and lengths (bpt_paged_append_decode's rule).
+  int in_place;
+  const void* table;
+  int64_t table_sb;
+  int table_i64, max_blocks, logP;
+  const int32_t* lens;
 };
 
 // Launch-ready form of bpt_kivi_args: decode attention over a KIVI cache (asymmetric 4/8-bit codes with

@@ -283,20 +283,16 @@ struct Buffers {
   size_t counters_bytes;
 };
 
-int paged_decode(const bpt_decode_args* a, void* stream, const bpt::LaunchEvents& ev, const char* fn,
-                 const Buffers* own = nullptr, const bpt::AppendParams* fuse = nullptr) {
-  Plan pl;
+// Checks a decode call's arguments and buffers on the host and fills its launch parameters (*p, *pl); nothing
+// is launched. *empty: a batch of zero (nothing to launch).
+int decode_setup(const bpt_decode_args* a, const char* fn, const Buffers* own, bpt::DecodeParams* out, Plan* plan,
+                 bool* empty) {
+  Plan& pl = *plan;
   int rc = make_plan(a, &pl);
   if (rc) return rc;
   const Buffers buf = own ? *own : Buffers{a->workspace, a->workspace_bytes, a->counters, a->counters_bytes};
-  if (a->batch == 0) {
-    if (ev.start) {  // nothing to launch: the interval is empty
-      hipError_t e = hipEventRecord(ev.start, (hipStream_t)stream);
-      if (e == hipSuccess) e = hipEventRecord(ev.stop, (hipStream_t)stream);
-      if (e != hipSuccess) return hip_fail(fn, e);
-    }
-    return BPT_OK;
-  }
+  *empty = a->batch == 0;
+  if (*empty) return BPT_OK;
   if (!a->q || !a->k_cache || !a->v_cache || !a->block_table || !a->out)
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: q, caches, block_table and out must be non-NULL", fn);
   if ((a->merge_out == nullptr) != (a->merge_lse == nullptr))
@@ -370,6 +366,25 @@ int paged_decode(const bpt_decode_args* a, void* stream, const bpt::LaunchEvents
   p.lse_out = a->lse_out;
   p.merge_out = a->merge_out;
   p.merge_lse = a->merge_lse;
+  *out = p;
+  return BPT_OK;
+}
+
+int paged_decode(const bpt_decode_args* a, void* stream, const bpt::LaunchEvents& ev, const char* fn,
+                 const Buffers* own = nullptr, const bpt::AppendParams* fuse = nullptr) {
+  Plan pl;
+  bpt::DecodeParams p;
+  bool empty;
+  int rc = decode_setup(a, fn, own, &p, &pl, &empty);
+  if (rc) return rc;
+  if (empty) {
+    if (ev.start) {  // nothing to launch: the interval is empty
+      hipError_t e = hipEventRecord(ev.start, (hipStream_t)stream);
+      if (e == hipSuccess) e = hipEventRecord(ev.stop, (hipStream_t)stream);
+      if (e != hipSuccess) return hip_fail(fn, e);
+    }
+    return BPT_OK;
+  }
   if (fuse) {
     p.fuse_q = fuse->Q;
     p.nk = (const uint16_t*)fuse->k;
@@ -770,6 +785,11 @@ int append_params(const bpt_append_args* a, bpt::AppendParams* out, bool* empty,
   p.num_blocks = a->num_blocks;
   p.src_dtype = a->src_dtype;
   p.slot_i64 = a->slot_dtype == BPT_IDX_I64;
+  p.in_place = 0;
+  p.table = nullptr;
+  p.table_sb = 0;
+  p.table_i64 = p.max_blocks = p.logP = 0;
+  p.lens = nullptr;
   *out = p;
   return BPT_OK;
 }
@@ -812,7 +832,29 @@ int bpt_paged_append_decode(const bpt_append_args* append, const bpt_decode_args
   int rc = append_params(append, &p, &empty, fn);
   if (rc) return rc;
   if (!decode) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: decode args is NULL", fn);
+  // Every check of the decode half runs before anything is launched: a refused call writes nothing.
+  bpt::DecodeParams dp;
+  Plan pl;
+  bool no_decode;
+  rc = decode_setup(decode, fn, nullptr, &dp, &pl, &no_decode);
+  if (rc) return rc;
+  if (!empty && !no_decode && !decode->context_lens)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: context_lens are required (the new rows are the last tokens)", fn);
   if (!empty && fusable(append, decode)) return paged_decode(decode, stream, {}, fn, nullptr, &p);
+  if (!empty && !no_decode) {
+    if (append->batch != decode->batch || append->num_queries != decode->num_queries)
+      return fail(BPT_ERR_INVALID_ARGUMENT, "%s: the new rows must be [batch, num_queries] of the decode", fn);
+    // The rule of the fused launch: only rows stored where the decode reads token len - Q + qi.
+    p.in_place = 1;
+    p.table = decode->block_table;
+    p.table_sb = decode->table_stride_b;
+    p.table_i64 = decode->table_dtype == BPT_IDX_I64;
+    p.max_blocks = decode->max_blocks_per_seq;
+    p.logP = log2i(decode->page_size);
+    p.lens = decode->context_lens;
+    if (append->page_size != decode->page_size || append->num_blocks != decode->num_blocks)
+      return fail(BPT_ERR_INVALID_ARGUMENT, "%s: append and decode must describe the same pools", fn);
+  }
   if (!empty) {
     hipError_t e = bpt::launch_append(p, append->kv_dtype, append->scale_kind, append->head_dim, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(fn, e);

@@ -53,8 +53,8 @@ struct MChunk {
 };
 
 // The new token among this lane's four rows of chunk kk (first_new: the sequence's first new token), as
-// 2 t + j with its index among the new rows, or -1.
-__device__ __forceinline__ int new_row(int kk, int len, int first_new, int lane, int& qi) {
+// 2 t + j with its index among the new rows, or -1. Only rows stored in place (bit qi of in_place) count.
+__device__ __forceinline__ int new_row(int kk, int len, int first_new, unsigned in_place, int lane, int& qi) {
   const int T0 = kk * kMChunk;
   int sel = -1;
   qi = 0;
@@ -64,7 +64,7 @@ __device__ __forceinline__ int new_row(int kk, int len, int first_new, int lane,
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int tok = T0 + 16 * t + 8 * j + (lane >> 3);
-        if (tok >= first_new && tok < len) {
+        if (tok >= first_new && tok < len && ((in_place >> (tok - first_new)) & 1u)) {
           sel = 2 * t + j;
           qi = tok - first_new;
         }
@@ -129,6 +129,9 @@ __device__ __forceinline__ void fused_append(const DecodeParams& p) {
     const int64_t blk = load_index(p.w_blocks, si, p.w_i64 != 0);
     const int64_t off = load_index(p.w_offsets, si, p.w_i64 != 0);
     if (blk < 0 || blk >= p.num_blocks || off < 0 || off >= p.P) continue;
+    if (!slot_is_token(p.table, (int64_t)b * p.table_sb, p.table_i64 != 0, p.max_blocks, p.num_blocks, p.logP,
+                       (int64_t)p.lens[b] - p.fuse_q + qi, blk, off))
+      continue;
     const uint16_t* src = (which ? p.nv : p.nk) + (int64_t)b * p.n_sb + (int64_t)qi * p.n_sq + (int64_t)h * p.n_sh + 4 * lane;
     const float s = (which ? p.vs : p.ks)[h];
     uint32_t w = 0u;
@@ -153,6 +156,27 @@ __device__ __forceinline__ void fused_append(const DecodeParams& p) {
 __device__ __forceinline__ int clamp_page(const DecodeParams& p, int e) {
   return e < 0 ? 0 : (e >= p.num_blocks ? p.num_blocks - 1 : e);
 }
+__device__ __forceinline__ int clamp_page_u(const DecodeParams& p, int e) { return sread(clamp_page(p, e)); }
+
+// Which of sequence b's new rows (the last fuse_q tokens of its length: row qi is token first_new + qi) are
+// stored where the decode reads that token (slot_is_token): bit qi. Rows aimed anywhere else are neither
+// stored by this launch nor used by it, so no workgroup ever reads a slot another one may be writing. Scalar
+// loads, once per piece.
+__device__ __forceinline__ unsigned fused_in_place(const DecodeParams& p, int b, int first_new) {
+  unsigned mask = 0u;
+  for (int qi = 0; qi < p.fuse_q; ++qi) {
+    const int64_t si = (int64_t)b * p.w_sb + (int64_t)qi * p.w_sq;
+    const int64_t blk = p.w_i64 ? load_uniform((const int64_t*)p.w_blocks + si)
+                                : (int64_t)load_uniform((const int32_t*)p.w_blocks + si);
+    const int64_t off = p.w_i64 ? load_uniform((const int64_t*)p.w_offsets + si)
+                                : (int64_t)load_uniform((const int32_t*)p.w_offsets + si);
+    const int64_t tok = (int64_t)first_new + qi;
+    if (tok < 0 || (tok >> p.logP) >= p.max_blocks || blk < 0 || blk >= p.num_blocks) continue;
+    const int e = clamp_page_u(p, load_uniform((const int32_t*)p.table + table_word(p, b, (int)(tok >> p.logP))));
+    if (blk == e && off == (tok & (p.P - 1))) mask |= 1u << qi;
+  }
+  return mask;
+}
 
 // Issue chunk kk's K loads (mfma_issue_k) or V loads and per-token scales (mfma_issue_v). Tokens at or past
 // len read the sequence's last token instead (valid memory, never weighted). PU: a 16-token tile lies
@@ -170,7 +194,7 @@ __device__ __forceinline__ int mfma_page(const DecodeParams& p, int b, int tile_
 // rows of sixteen tokens; mfma_k_operand then rearranges them through LDS.
 template <bool PU, bool FUSE>
 __device__ __forceinline__ void mfma_issue_k(const DecodeParams& p, int b, int h, int kk, int len, int lane, int first_new,
-                                             MChunk& c) {
+                                             unsigned in_place, MChunk& c) {
   const int T0 = kk * kMChunk;
   const int r = lane >> 3, sg = lane & 7;
   const int64_t head_off = (int64_t)h * p.kv_shead + 16 * sg;
@@ -185,7 +209,7 @@ __device__ __forceinline__ void mfma_issue_k(const DecodeParams& p, int b, int h
   }
   if constexpr (FUSE) {
     int qi;
-    c.nsel_k = new_row(kk, len, first_new, lane, qi);
+    c.nsel_k = new_row(kk, len, first_new, in_place, lane, qi);
     if (c.nsel_k >= 0) {
       const uint16_t* src = p.nk + (int64_t)b * p.n_sb + (int64_t)qi * p.n_sq + (int64_t)h * p.n_sh + 16 * sg;
       c.nk[0] = load16((const uint8_t*)src);
@@ -216,7 +240,7 @@ __device__ __forceinline__ void mfma_k_operand(const MChunk& c, U4 (&sk)[2][16][
 
 template <int SK, bool PU, bool FUSE>
 __device__ __forceinline__ void mfma_issue_v(const DecodeParams& p, int b, int h, int kk, int len, int lane, int first_new,
-                                             MChunk& c) {
+                                             unsigned in_place, MChunk& c) {
   const int T0 = kk * kMChunk;
   {
     const int r = lane >> 3, sg = lane & 7;
@@ -241,7 +265,7 @@ __device__ __forceinline__ void mfma_issue_v(const DecodeParams& p, int b, int h
   }
   if constexpr (FUSE) {
     int qi;
-    c.nsel_v = new_row(kk, len, first_new, lane, qi);
+    c.nsel_v = new_row(kk, len, first_new, in_place, lane, qi);
     if (c.nsel_v >= 0) {
       const uint16_t* src = p.nv + (int64_t)b * p.n_sb + (int64_t)qi * p.n_sq + (int64_t)h * p.n_sh + 16 * (lane & 7);
       c.nv[0] = load16((const uint8_t*)src);
@@ -252,9 +276,9 @@ __device__ __forceinline__ void mfma_issue_v(const DecodeParams& p, int b, int h
 
 template <int SK, bool PU, bool FUSE>
 __device__ __forceinline__ void mfma_issue(const DecodeParams& p, int b, int h, int kk, int len, int lane, int first_new,
-                                           MChunk& c) {
-  mfma_issue_k<PU, FUSE>(p, b, h, kk, len, lane, first_new, c);
-  mfma_issue_v<SK, PU, FUSE>(p, b, h, kk, len, lane, first_new, c);
+                                           unsigned in_place, MChunk& c) {
+  mfma_issue_k<PU, FUSE>(p, b, h, kk, len, lane, first_new, in_place, c);
+  mfma_issue_v<SK, PU, FUSE>(p, b, h, kk, len, lane, first_new, in_place, c);
 }
 
 // 4 x 4 byte transpose: w[i] byte j -> out[j] byte i.
@@ -553,13 +577,14 @@ __global__ __launch_bounds__(NW * 64, kMfmaWavesPerSimd) void decode_mfma_kernel
   // Fused writes: the sequence's first new token (its new rows are the last fuse_q of its length) and the
   // head's scales, which quantize them.
   int first_new = FUSE ? load_uniform(p.lens + b) - p.fuse_q : 0;
+  unsigned in_place = FUSE ? fused_in_place(p, b, first_new) : 0u;
   float ks_new = FUSE ? load_uniform(p.ks + h) : 1.0f, vs_new = FUSE ? load_uniform(p.vs + h) : 1.0f;
   float qscale = p.qscale * (SK == kScaleHead ? load_uniform(p.ks + h) : 1.0f);
   mfma_load_q<KV, QS>(p, b, h, rows, len, lane, qb, rlen);
   {
     const int64_t seg_c0 = seg_start(b, h, span);
     const int k_end = (int)(min(c_end, seg_c0 + span) - seg_c0 - X);
-    if (k + wave < k_end) mfma_issue<SK, PU, FUSE>(p, b, h, k + wave, len, lane, first_new, cr);
+    if (k + wave < k_end) mfma_issue<SK, PU, FUSE>(p, b, h, k + wave, len, lane, first_new, in_place, cr);
   }
 
   for (;;) {
@@ -578,9 +603,10 @@ __global__ __launch_bounds__(NW * 64, kMfmaWavesPerSimd) void decode_mfma_kernel
       const int kn = kk + NW;
       mfma_compute<KV, SK, QS, FUSE>(cr, s_k[wave], s_sc[wave], kk, lane, qb, qscale, rlen, m, l, o, ks_new, vs_new,
                                      [&]() {
-                                       if (kn < k_end) mfma_issue_k<PU, FUSE>(p, b, h, kn, len, lane, first_new, cr);
+                                       if (kn < k_end)
+                                         mfma_issue_k<PU, FUSE>(p, b, h, kn, len, lane, first_new, in_place, cr);
                                      });
-      if (kn < k_end) mfma_issue_v<SK, PU, FUSE>(p, b, h, kn, len, lane, first_new, cr);
+      if (kn < k_end) mfma_issue_v<SK, PU, FUSE>(p, b, h, kn, len, lane, first_new, in_place, cr);
       kk = kn;
     }
 
@@ -621,12 +647,13 @@ __global__ __launch_bounds__(NW * 64, kMfmaWavesPerSimd) void decode_mfma_kernel
         len = sread(s_len[b]);
         if constexpr (FUSE) {
           first_new = load_uniform(p.lens + b) - p.fuse_q;
+          in_place = fused_in_place(p, b, first_new);
           ks_new = load_uniform(p.ks + h);
           vs_new = load_uniform(p.vs + h);
         }
         qscale = p.qscale * (SK == kScaleHead ? load_uniform(p.ks + h) : 1.0f);
         mfma_load_q<KV, QS>(p, b, h, rows, len, lane, qb, rlen);
-        if (wave < kn_end) mfma_issue<SK, PU, FUSE>(p, b, h, wave, len, lane, first_new, cr);
+        if (wave < kn_end) mfma_issue<SK, PU, FUSE>(p, b, h, wave, len, lane, first_new, in_place, cr);
       }
     }
 

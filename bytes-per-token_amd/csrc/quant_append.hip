@@ -31,6 +31,9 @@ __global__ __launch_bounds__(256) void quant_append_kernel(const AppendParams p)
   const int64_t blk = load_index(p.blocks, si, p.slot_i64 != 0);
   const int64_t off = load_index(p.offsets, si, p.slot_i64 != 0);
   if (blk < 0 || blk >= p.num_blocks || off < 0 || off >= p.P) return;
+  if (p.in_place && !slot_is_token(p.table, (int64_t)b * p.table_sb, p.table_i64 != 0, p.max_blocks, p.num_blocks,
+                                   p.logP, (int64_t)p.lens[b] - p.Q + qi, blk, off))
+    return;
 
   const void* src = which ? p.v : p.k;
   const int64_t xi = (int64_t)b * p.n_sb + (int64_t)qi * p.n_sq + (int64_t)h * p.n_sh + lane * PER;

@@ -251,10 +251,13 @@ typedef struct {
  *   slots         [B] int32: the slot of each row of this forward pass (clamped into the table)
  *   positions     [B, Q] int32 / int64 (strides pos_stride_{b,q}): the positions this pass writes and queries
  *   block_table   out [B, n_blocks] int32: the slot's blocks, 0 past the reserved ones (fastserve's padding)
- *   write_blocks  out [B, Q] int32: the block of each position, -1 outside the reserved blocks (such rows are
- *                 skipped by bpt_quant_append)
- *   write_offsets out [B, Q] int32: position % page_size
  *   context_lens  out [B] int32: the last position + 1, clamped to the reserved tokens
+ *   write_blocks  out [B, Q] int32: the block of each position that is token context_len - Q + i of its row
+ *                 (the step's new rows are the row's last Q tokens) inside the reserved blocks, else -1
+ *                 (skipped by bpt_quant_append). Consecutive positions inside the reservation all get their
+ *                 block; positions past it (the length is then clamped) or out of order get none, so a step
+ *                 never stores a row it does not attend as new.
+ *   write_offsets out [B, Q] int32: position % page_size
  * page_size a power of two; max_blocks (<= table_stride) bounds the blocks read per slot. Nothing is read
  * back to the host: the call is one launch and can be captured in a graph.
  */
@@ -352,12 +355,15 @@ int bpt_paged_prepare(const bpt_prepare_args* args, void* stream);
 int bpt_quant_append(const bpt_append_args* args, void* stream);
 
 /* Store, then attend (replaces integration/kv_cache.py:160-192, the cache's attend: _append then the decode
- * call): the rows of `append` are written as bpt_quant_append writes them and `decode` attends the pools with
- * them in place. When the decode runs on the matrix-core kernel with per-head scales over the same pools, the
- * rows are bf16 (16-byte aligned) and are the last Q <= 8 tokens of every sequence (their write slots are the
- * block table's pages for positions context_len - Q .. context_len - 1), head dim 128, context lengths given,
- * no len_offset and no merge partial, one launch does both: it stores the rows and uses their codes for those
- * tokens directly. Otherwise bpt_quant_append then bpt_paged_decode (two launches). Errors as theirs. */
+ * call). The rows of `append` ([batch, num_queries] of the decode) are the last Q tokens of each sequence: row
+ * i of sequence b is token context_lens[b] - Q + i. A row is stored, as bpt_quant_append stores it, when its
+ * slot is where the decode reads that token (the token's block-table page, clamped into the pool as the
+ * decode clamps it, and its offset); rows with no slot or a slot anywhere else are not stored. `decode` then
+ * attends the pools with the stored rows in place. When the decode runs on the matrix-core kernel with
+ * per-head scales over the same pools, the rows are bf16 (16-byte aligned), Q <= 8, head dim 128, no
+ * len_offset and no merge partial, one launch does both: it stores the rows and uses their codes for those
+ * tokens directly. Otherwise two launches (the store, then bpt_paged_decode), with the same results. Every
+ * argument of both halves is checked before anything is launched: a refused call writes nothing. */
 int bpt_paged_append_decode(const bpt_append_args* append, const bpt_decode_args* decode, void* stream);
 
 /* Host-only: validate a KIVI call, fill grid_groups, report workspace and counter sizes in bytes. */

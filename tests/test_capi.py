@@ -254,3 +254,38 @@ def test_append_decode_checks_both_argument_blocks_before_any_gpu_call(built_lib
     slots = torch.zeros((q.shape[0], 1), dtype=torch.int32)
     with pytest.raises(ValueError, match="on a GPU"):
         paged_append_decode(q, rows, rows, k, v, table, lens, ks, vs, slots, slots, scale=0.1, max_context=16)
+
+
+@pytest.mark.parametrize("fmt", ["fp8", "int8"])
+def test_append_decode_refuses_a_bad_decode_block_before_storing(built_lib, fmt):
+    """A valid, non-empty append block with a decode block whose workspace is too small: the call is refused on
+    the host with the decode's own message, before the store is launched (no GPU here, so any launch would
+    surface as a HIP error instead). Per-head FP8 fuses; per-token INT8 takes the two-launch path."""
+    from bpt_amd import paged_attention
+
+    q, k, v, table, lens, ks, vs = cpu_case(fmt)
+    d, _ = paged_attention._decode_args(q, k, v, table, lens, ks, vs, 0.1, 128, None, torch.bfloat16)
+    small = torch.zeros(256, dtype=torch.uint8)
+    counters = torch.zeros(4096, dtype=torch.uint8)
+    d.out = q.data_ptr()
+    d.workspace, d.workspace_bytes = small.data_ptr(), small.numel()
+    d.counters, d.counters_bytes = counters.data_ptr(), counters.numel()
+    rows = torch.zeros((q.shape[0], 1, 8, 128), dtype=torch.bfloat16)
+    slots = torch.zeros((q.shape[0], 1), dtype=torch.int32)
+    a = _lib.AppendArgs()
+    a.struct_size = ctypes.sizeof(_lib.AppendArgs)
+    a.kv_dtype, a.scale_kind = d.kv_dtype, d.scale_kind
+    a.src_dtype, a.slot_dtype = 0, 0
+    a.batch, a.num_queries, a.num_kv_heads, a.head_dim = q.shape[0], 1, 8, 128
+    a.page_size, a.num_blocks = k.shape[1], k.shape[0]
+    a.k = a.v = rows.data_ptr()
+    a.new_stride_b, a.new_stride_q, a.new_stride_h = rows.stride(0), rows.stride(1), rows.stride(2)
+    a.write_blocks = a.write_offsets = slots.data_ptr()
+    a.slot_stride_b, a.slot_stride_q = slots.stride(0), slots.stride(1)
+    a.k_cache, a.v_cache = k.data_ptr(), v.data_ptr()
+    a.kv_stride_block, a.kv_stride_token, a.kv_stride_head = k.stride(0), k.stride(1), k.stride(2)
+    a.k_scale, a.v_scale = d.k_scale, d.v_scale
+    a.scale_stride_block, a.scale_stride_token, a.scale_stride_head = (
+        d.scale_stride_block, d.scale_stride_token, d.scale_stride_head)
+    with pytest.raises(ValueError, match="workspace"):
+        _lib.check(built_lib.bpt_paged_append_decode(ctypes.byref(a), ctypes.byref(d), None))

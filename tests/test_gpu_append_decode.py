@@ -108,3 +108,53 @@ def test_f32_rows_take_the_two_launches():
     c = make_case("fp8", lengths, nq=1, scales="head", seed=6)
     k, v, blocks, offsets = new_rows(c, 1, seed=11)
     both_ways(c, k.float(), v.float(), blocks, offsets, max_context=200)
+
+
+def expected_with_rows_in_place(c, k, v, blocks, offsets, in_place, max_context, scale=0.09):
+    """Pools and output when only the rows marked in_place [B, Q] are stored: quantize_append of those rows
+    (the others' slots set to -1), then paged_decode_attention."""
+    from bpt_amd import paged_decode_attention, quantize_append
+
+    kc, vc = c["k"].clone(), c["v"].clone()
+    ks = None if c["ks"] is None else c["ks"].clone()
+    vs = None if c["vs"] is None else c["vs"].clone()
+    quantize_append(k, v, kc, vc, ks, vs, torch.where(in_place, blocks, torch.full_like(blocks, -1)), offsets)
+    out = paged_decode_attention(c["q"], kc, vc, c["table"], c["lens"], ks, vs, scale=scale, max_context=max_context)
+    return [t for t in (kc, vc, ks, vs) if t is not None], out
+
+
+@pytest.mark.parametrize("fmt,scales,nq", [("fp8", "head", 1), ("fp8", "head", 3), ("int8", "token", 1),
+                                           ("int8", "head", 5), ("bf16", "head", 2)])
+def test_rows_aimed_elsewhere_are_neither_stored_nor_attended(fmt, scales, nq):
+    """bpt_paged_append_decode stores a new row only where the decode reads token len - Q + qi. A row whose
+    slot is another token of its sequence, and a row with no slot (-1), change nothing, in the one-launch path
+    (FP8 and INT8 with per-head scales) and in the two-launch one (per-token scales, BF16) alike."""
+    from bpt_amd import paged_append_decode
+
+    lengths = [max(t, nq + 2) for t in (70, 40, 513, 256, 33)]
+    c = make_case(fmt, lengths, nq=nq, scales=scales, seed=21 + nq)
+    k, v, blocks, offsets = new_rows(c, nq, seed=22)
+    page = c["k"].shape[1]
+    in_place = torch.ones_like(blocks, dtype=torch.bool)
+    # Sequence 0, row 0: the slot of the token two places earlier (a slot the decode reads as another token).
+    pos = int(c["lens"][0]) - nq - 2
+    blocks[0, 0] = c["table"][0, pos // page].to(torch.int32)
+    offsets[0, 0] = pos % page
+    in_place[0, 0] = False
+    # Sequence 2, last row: no slot.
+    blocks[2, nq - 1] = -1
+    in_place[2, nq - 1] = False
+    # Sequence 3, row 0: the right page, the wrong offset.
+    offsets[3, 0] = (offsets[3, 0] + 1) % page
+    in_place[3, 0] = False
+    want_pools, want = expected_with_rows_in_place(c, k, v, blocks, offsets, in_place, max_context=600)
+    kc, vc = c["k"].clone(), c["v"].clone()
+    ks = None if c["ks"] is None else c["ks"].clone()
+    vs = None if c["vs"] is None else c["vs"].clone()
+    got = paged_append_decode(c["q"], k, v, kc, vc, c["table"], c["lens"], ks, vs, blocks, offsets, scale=0.09,
+                              max_context=600)
+    torch.cuda.synchronize()
+    for a, b in zip(want_pools, [t for t in (kc, vc, ks, vs) if t is not None]):
+        assert torch.equal(a.view(torch.uint8) if a.dtype != torch.float32 else a,
+                           b.view(torch.uint8) if b.dtype != torch.float32 else b), "the pools differ"
+    assert torch.equal(got, want), f"outputs differ: max {(got.float() - want.float()).abs().max()}"

@@ -241,3 +241,43 @@ def test_decode_steps_captured_in_a_hip_graph(fmt):
         check_step(meta, outs)
         torch.zeros(1 << 20, device=DEV).sum().item()  # eager work between replays
         set_inputs()
+
+
+@pytest.mark.parametrize("nq", [1, 3])
+def test_positions_past_the_reservation_store_nothing(nq):
+    """Device positions that run past a row's reserved blocks (the host path would refuse them): the row gets no
+    write slot and attends its reserved tokens, and the cache's one-launch attend (FP8, per-head scales) gives
+    exactly what quantize_append then paged_decode_attention give on the same metadata."""
+    from bpt_amd import paged_decode_attention, quantize_append
+
+    cache = PagedQuantKVCache(num_layers=1, num_kv_heads=HKV, head_dim=D, num_blocks=32, block_size=4,
+                              kv_dtype=torch.float8_e4m3fn, device=DEV,
+                              k_scale=torch.full((1, HKV), 4.0 / 448), v_scale=torch.full((1, HKV), 4.0 / 448))
+    g = torch.Generator(device=DEV).manual_seed(31)
+    cache.reserve("a", 8)   # 2 blocks
+    cache.reserve("b", 12)  # 3 blocks
+    for i in range(cache.num_blocks):  # every slot holds codes already
+        cache.k[0][i] = (torch.randn((4, HKV, D), generator=g, device=DEV)).to(torch.float8_e4m3fn)
+        cache.v[0][i] = (torch.randn((4, HKV, D), generator=g, device=DEV)).to(torch.float8_e4m3fn)
+    # "a": positions 7 .. 7 + nq - 1 run past its 8 reserved tokens (for nq > 1); "b": inside its reservation.
+    positions = torch.tensor([[7 + i for i in range(nq)], [5 + i for i in range(nq)]], device=DEV)
+    meta = cache.prepare(["a", "b"], positions)
+    wb = meta.write_blocks.cpu()
+    if nq > 1:
+        assert (wb[0] == -1).all() and int(meta.context_lens[0]) == 8
+    else:
+        assert wb[0, 0] == cache.tables["a"][1] and int(meta.context_lens[0]) == 8
+    assert (wb[1] >= 0).all() and int(meta.context_lens[1]) == 5 + nq
+    q = torch.randn((2, HQ, nq, D), generator=g, device=DEV).to(torch.bfloat16)
+    k = torch.randn((2, HKV, nq, D), generator=g, device=DEV).to(torch.bfloat16)
+    v = torch.randn((2, HKV, nq, D), generator=g, device=DEV).to(torch.bfloat16)
+    kc, vc = cache.k[0].clone(), cache.v[0].clone()
+    quantize_append(k.transpose(1, 2), v.transpose(1, 2), kc, vc, cache.k_scale[0], cache.v_scale[0],
+                    meta.write_blocks, meta.write_offsets)
+    want = paged_decode_attention(q.transpose(1, 2), kc, vc, meta.block_table, meta.context_lens, cache.k_scale[0],
+                                  cache.v_scale[0], scale=SCALE, max_context=meta.kv_len)
+    got = cache.attend(0, q, k, v, meta, scale=SCALE)
+    torch.cuda.synchronize()
+    assert torch.equal(cache.k[0].view(torch.uint8), kc.view(torch.uint8))
+    assert torch.equal(cache.v[0].view(torch.uint8), vc.view(torch.uint8))
+    assert torch.equal(got.transpose(1, 2), want)
