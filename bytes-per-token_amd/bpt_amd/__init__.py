@@ -18,6 +18,7 @@ from .paged_attention import (
     kv_read_bytes,
     paged_append_decode,
     paged_decode_attention,
+    paged_decode_hints,
     paged_prepare,
     quantize_append,
 )
@@ -33,6 +34,7 @@ __all__ = [
     "kv_read_bytes",
     "paged_append_decode",
     "paged_decode_attention",
+    "paged_decode_hints",
     "paged_prepare",
     "quantize_append",
     "rms_norm_int8",

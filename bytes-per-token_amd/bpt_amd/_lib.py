@@ -95,6 +95,8 @@ class DecodeArgs(ctypes.Structure):
         ("lse_out", _vp),
         ("merge_out", _vp),
         ("merge_lse", _vp),
+        ("hints", _vp),
+        ("hints_bytes", ctypes.c_size_t),
     ]
 
 
@@ -212,6 +214,18 @@ class PrepareArgs(ctypes.Structure):
     ]
 
 
+class Tuning(ctypes.Structure):
+    """bpt_tuning: plan constants for sweeps (a field at 0, or -1 for piece_cost, keeps the built-in choice)."""
+
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("groups_per_cu", _i32),
+        ("piece_cost", _i32),
+        ("slot_weight", _i32),
+        ("min_chunks", _i32),
+    ]
+
+
 class KiviQuantArgs(ctypes.Structure):
     _fields_ = [
         ("struct_size", ctypes.c_uint32),
@@ -268,6 +282,8 @@ SIGNATURES = {
         [ctypes.POINTER(DecodeArgs), ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)],
     ),
     "bpt_paged_decode": (_i32, [ctypes.POINTER(DecodeArgs), _vp]),
+    "bpt_decode_hints": (_i32, [ctypes.POINTER(DecodeArgs), _vp, ctypes.POINTER(ctypes.c_size_t), _vp]),
+    "bpt_set_tuning": (_i32, [ctypes.POINTER(Tuning)]),
     "bpt_paged_decode_noalloc": (_i32, [ctypes.POINTER(DecodeArgs), _vp]),
     "bpt_paged_decode_timed": (_i32, [ctypes.POINTER(DecodeArgs), _vp, _vp, _vp]),
     "bpt_quant_append": (_i32, [ctypes.POINTER(AppendArgs), _vp]),
@@ -291,7 +307,7 @@ SIGNATURES = {
     "bpt_copy_probe": (_i32, [_vp, _vp, ctypes.c_uint64, _vp]),
 }
 
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 
 class BptError(RuntimeError):
@@ -333,3 +349,10 @@ def check(rc: int) -> None:
     if rc == BPT_ERR_INVALID_ARGUMENT:
         raise ValueError(msg)
     raise BptError(msg)
+
+
+def set_tuning(groups_per_cu: int = 0, piece_cost: int = -1, slot_weight: int = 0, min_chunks: int = 0) -> None:
+    """Override the decode plan's constants process-wide (bpt_set_tuning), for tuning sweeps; no arguments
+    restores the built-in ones."""
+    t = Tuning(ctypes.sizeof(Tuning), groups_per_cu, piece_cost, slot_weight, min_chunks)
+    check(lib().bpt_set_tuning(ctypes.byref(t)))

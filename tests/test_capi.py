@@ -289,3 +289,18 @@ def test_append_decode_refuses_a_bad_decode_block_before_storing(built_lib, fmt)
         d.scale_stride_block, d.scale_stride_token, d.scale_stride_head)
     with pytest.raises(ValueError, match="workspace"):
         _lib.check(built_lib.bpt_paged_append_decode(ctypes.byref(a), ctypes.byref(d), None))
+
+
+def test_hint_size_query_is_host_only(built_lib):
+    """bpt_decode_hints with no buffer reports the size a call's hints take (one 128-byte record per workgroup of
+    the matrix-core kernel; none for the vector kernel) without launching anything."""
+    from bpt_amd.paged_attention import _plan
+
+    for fmt, hq, want_records in (("fp8", 16, True), ("bf16", 16, False), ("fp8", 8, False)):
+        q, k, v, table, lens, ks, vs = cpu_case(fmt=fmt, b=6, hq=hq, max_blocks=64, nb=512)
+        a, _, _ = _plan(q, k, v, table, lens, ks, vs, 0.1, 1024, None)
+        size = ctypes.c_size_t(123)
+        assert built_lib.bpt_decode_hints(ctypes.byref(a), None, ctypes.byref(size), None) == 0
+        assert size.value == (a.grid_groups * 128 if want_records else 0), (fmt, hq)
+    assert built_lib.bpt_decode_hints(ctypes.byref(a), None, None, None) == _lib.BPT_ERR_INVALID_ARGUMENT
+    assert b"hints_bytes" in built_lib.bpt_last_error()
