@@ -18,7 +18,6 @@ from .paged_attention import (
     kv_read_bytes,
     paged_append_decode,
     paged_decode_attention,
-    paged_decode_hints,
     paged_prepare,
     quantize_append,
 )
@@ -34,7 +33,6 @@ __all__ = [
     "kv_read_bytes",
     "paged_append_decode",
     "paged_decode_attention",
-    "paged_decode_hints",
     "paged_prepare",
     "quantize_append",
     "rms_norm_int8",

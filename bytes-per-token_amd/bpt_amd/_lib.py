@@ -95,8 +95,6 @@ class DecodeArgs(ctypes.Structure):
         ("lse_out", _vp),
         ("merge_out", _vp),
         ("merge_lse", _vp),
-        ("hints", _vp),
-        ("hints_bytes", ctypes.c_size_t),
     ]
 
 
@@ -221,7 +219,6 @@ class Tuning(ctypes.Structure):
         ("struct_size", ctypes.c_uint32),
         ("groups_per_cu", _i32),
         ("piece_cost", _i32),
-        ("slot_weight", _i32),
         ("min_chunks", _i32),
     ]
 
@@ -282,7 +279,6 @@ SIGNATURES = {
         [ctypes.POINTER(DecodeArgs), ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)],
     ),
     "bpt_paged_decode": (_i32, [ctypes.POINTER(DecodeArgs), _vp]),
-    "bpt_decode_hints": (_i32, [ctypes.POINTER(DecodeArgs), _vp, ctypes.POINTER(ctypes.c_size_t), _vp]),
     "bpt_set_tuning": (_i32, [ctypes.POINTER(Tuning)]),
     "bpt_paged_decode_noalloc": (_i32, [ctypes.POINTER(DecodeArgs), _vp]),
     "bpt_paged_decode_timed": (_i32, [ctypes.POINTER(DecodeArgs), _vp, _vp, _vp]),
@@ -351,8 +347,8 @@ def check(rc: int) -> None:
     raise BptError(msg)
 
 
-def set_tuning(groups_per_cu: int = 0, piece_cost: int = -1, slot_weight: int = 0, min_chunks: int = 0) -> None:
+def set_tuning(groups_per_cu: int = 0, piece_cost: int = -1, min_chunks: int = 0) -> None:
     """Override the decode plan's constants process-wide (bpt_set_tuning), for tuning sweeps; no arguments
     restores the built-in ones."""
-    t = Tuning(ctypes.sizeof(Tuning), groups_per_cu, piece_cost, slot_weight, min_chunks)
+    t = Tuning(ctypes.sizeof(Tuning), groups_per_cu, piece_cost, min_chunks)
     check(lib().bpt_set_tuning(ctypes.byref(t)))

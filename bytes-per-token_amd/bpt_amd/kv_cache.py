@@ -27,12 +27,12 @@ FP8 unscaled), INT8 with dynamic per-(token, head) scales amax/127 paged like th
 from __future__ import annotations
 
 import heapq
-from dataclasses import dataclass, field
+from dataclasses import dataclass
 from typing import Any
 
 import torch
 
-from .paged_attention import paged_append_decode, paged_decode_hints, paged_prepare
+from .paged_attention import paged_append_decode, paged_prepare
 
 _FORMATS = {torch.float8_e4m3fn: "fp8", torch.int8: "int8", torch.bfloat16: "bf16"}
 HEAD_DIM = 128  # the one head size the paged decode kernels are built for
@@ -49,9 +49,6 @@ class PagedMeta:
     block_table: torch.Tensor  # [batch, n_blocks] int32: physical blocks of logical blocks 0 .. n_blocks - 1
     context_lens: torch.Tensor  # [batch] int32: tokens in the cache once this step is written
     kv_len: int  # a bound on the longest row's context length, known on the host (its reserved tokens)
-    # Launch hints of the decode over this metadata, per (query heads, queries): built by the first layer's
-    # attend and used by every layer's (the lengths, tables and launch shape are the same for all of them).
-    hints: dict = field(default_factory=dict, compare=False, repr=False)
 
 
 class PagedQuantKVCache:
@@ -250,14 +247,9 @@ class PagedQuantKVCache:
         if tuple(meta.write_blocks.shape) != (b, nq):
             raise ValueError(f"meta was prepared for {tuple(meta.write_blocks.shape)} tokens, not {(b, nq)}")
         # Store, then attend; one launch where the decode kernel can store the rows itself (paged_append_decode).
-        qt = q.transpose(1, 2)
-        cache = (self.k[layer], self.v[layer], meta.block_table, meta.context_lens, self.k_scale[layer],
-                 self.v_scale[layer])
-        key = (hq, nq)
-        if key not in meta.hints:  # once per forward pass: where each layer's decode workgroups start
-            meta.hints[key] = paged_decode_hints(qt, *cache, scale=scale, max_context=meta.kv_len)
         out = paged_append_decode(
-            qt, k.transpose(1, 2), v.transpose(1, 2), *cache[:4], *cache[4:], meta.write_blocks, meta.write_offsets,
-            scale=scale, max_context=meta.kv_len, out_dtype=q.dtype, hints=meta.hints[key],
+            q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), self.k[layer], self.v[layer], meta.block_table,
+            meta.context_lens, self.k_scale[layer], self.v_scale[layer], meta.write_blocks, meta.write_offsets,
+            scale=scale, max_context=meta.kv_len, out_dtype=q.dtype,
         )  # [B, Q, Hq, D] in q's dtype: the kernel rounds once, from float32 (integration/kv_cache.py:177-181)
         return out.transpose(1, 2)

@@ -154,38 +154,6 @@ def decode_plan(
     return a.grid_groups, a.chunk_tokens, ws, cnt
 
 
-def paged_decode_hints(
-    q, k_cache, v_cache, block_table, context_lens, k_scale=None, v_scale=None, *, scale, max_context, num_splits=None,
-    out: torch.Tensor | None = None,
-) -> torch.Tensor | None:
-    """Launch hints for paged_decode_attention over these arguments (bpt_decode_hints): where each workgroup's
-    range of the batch starts and the pages of its waves' first chunks, computed on the device from
-    context_lens and block_table in one small launch, so the decode's first KV loads go out at kernel entry.
-
-    Build them once per forward pass and pass `hints=` to every layer's call with the same lengths, block table
-    and launch shape. The kernel checks each hint against what it computes and ignores any that differ, so a
-    stale hint costs time and never changes a result. Returns the uint8 hint buffer (`out` if given, which must
-    hold enough bytes), or None when the call's kernel takes no hints (nothing is launched then).
-    """
-    a, _, _ = _plan(q, k_cache, v_cache, block_table, context_lens, k_scale, v_scale, scale, max_context, num_splits)
-    lib = _lib.lib()
-    need = ctypes.c_size_t(0)
-    _lib.check(lib.bpt_decode_hints(ctypes.byref(a), None, ctypes.byref(need), None))
-    if need.value == 0:
-        return None
-    dev = q.device
-    _require(dev.type == "cuda", "paged_decode_hints runs on a GPU: q must be a cuda tensor")
-    _require(block_table.device == dev and (context_lens is None or context_lens.device == dev),
-             "block_table and context_lens must be on q's device")
-    if out is None:
-        out = torch.empty(need.value, dtype=torch.uint8, device=dev)
-    _require(out.device == dev and out.is_contiguous(), "hints must be a contiguous tensor on q's device")
-    size = ctypes.c_size_t(out.numel() * out.element_size())
-    _lib.check(lib.bpt_decode_hints(ctypes.byref(a), ctypes.c_void_p(out.data_ptr()), ctypes.byref(size),
-                                    ctypes.c_void_p(_stream(dev))))
-    return out
-
-
 def decode_kernel_name(
     q, k_cache, v_cache, block_table, context_lens, k_scale=None, v_scale=None, *, scale, max_context, num_splits=None
 ) -> str:
@@ -229,7 +197,6 @@ def paged_decode_attention(
     workspace: torch.Tensor | None = None,
     counters: torch.Tensor | None = None,
     lse: torch.Tensor | None = None,
-    hints: torch.Tensor | None = None,
     _cascade: dict | None = None,
     _events: tuple | None = None,
     _append: object | None = None,
@@ -250,8 +217,6 @@ def paged_decode_attention(
     lse           optional contiguous float32 [B, Q, Hq] (or [B, Hq]) receiving each row's log-sum-exp of
                   scale * q.k over the tokens it saw (natural log, -inf for none): with `out` in float32 it is
                   the partial that kernels/reference.py:205-211 merges
-    hints         optional launch hints from paged_decode_hints over the same lengths, block table and shape
-                  (built once per forward pass): the same result, with the first KV loads at kernel entry
 
     Returns out [B, Q, Hq, D] (or [B, Hq, D]) in `out_dtype` (bf16 by default). One kernel launch.
     """
@@ -289,9 +254,6 @@ def paged_decode_attention(
             _require(m_lse.dtype == torch.float32 and m_lse.is_contiguous() and m_lse.numel() == b * nq * hq,
                      "the merged partial's lse must be contiguous float32 [B, Q, Hq]")
             a.merge_out, a.merge_lse = m_out.data_ptr(), m_lse.data_ptr()
-    if hints is not None:
-        _require(hints.device == dev and hints.is_contiguous(), "hints must be a contiguous tensor on q's device")
-        a.hints, a.hints_bytes = hints.data_ptr(), hints.numel() * hints.element_size()
     lib = _lib.lib()
     ws_bytes, cnt_bytes = ctypes.c_size_t(0), ctypes.c_size_t(0)
     _lib.check(lib.bpt_decode_plan(ctypes.byref(a), ctypes.byref(ws_bytes), ctypes.byref(cnt_bytes)))
@@ -393,7 +355,6 @@ def paged_append_decode(
     num_splits: int | None = None,
     out: torch.Tensor | None = None,
     out_dtype: torch.dtype = torch.bfloat16,
-    hints: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Store the new rows k, v [B, Q, Hkv, D] (as quantize_append), then attend (as paged_decode_attention):
     the cache's store-then-attend (integration/kv_cache.py:160-192).
@@ -409,7 +370,7 @@ def paged_append_decode(
     _require(q.device == dev, f"q is on {q.device}, the new rows on {dev}")
     return paged_decode_attention(q, k_cache, v_cache, block_table, context_lens, k_scale, v_scale, scale=scale,
                                   max_context=max_context, num_splits=num_splits, out=out, out_dtype=out_dtype,
-                                  hints=hints, _append=a)
+                                  _append=a)
 
 
 def paged_prepare(

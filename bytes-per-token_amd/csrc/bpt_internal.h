@@ -23,9 +23,6 @@
 #ifndef BPT_DECODE_MFMA_WAVES_PER_SIMD
 #define BPT_DECODE_MFMA_WAVES_PER_SIMD 2
 #endif
-#ifndef BPT_DECODE_SLOT_WEIGHT
-#define BPT_DECODE_SLOT_WEIGHT 1024
-#endif
 #ifndef BPT_DECODE_PIECE_COST
 #define BPT_DECODE_PIECE_COST 8
 #endif
@@ -118,9 +115,6 @@ constexpr int kDecodePieceCost = BPT_DECODE_PIECE_COST;
 // The same for matrix-core segments of kManyRows rows or more (8-wave workgroups; dearer merges).
 constexpr int kManyRowPieceCost = BPT_DECODE_MANY_ROW_PIECE_COST;
 constexpr int kMaxPieceCost = kDecodePieceCost > kManyRowPieceCost ? kDecodePieceCost : kManyRowPieceCost;
-// Matrix-core launches: the first workgroup dispatched to each CU takes a range kSlotWeight / 1024 times the
-// size of the others' (LineCut). Its waves are the older ones on every SIMD and are issued first.
-constexpr int kSlotWeight = BPT_DECODE_SLOT_WEIGHT;
 
 // 16-byte K loads (and V loads) per lane per chunk: fewer for 4-row groups, whose q and accumulators take
 // twice the registers.
@@ -135,9 +129,6 @@ constexpr int kMfmaRows = 16;
 constexpr int kMfmaChunk = 32;
 // Waves per SIMD the matrix-core decode kernel is compiled for (its register budget: 512 / this).
 constexpr int kMfmaWavesPerSimd = BPT_DECODE_MFMA_WAVES_PER_SIMD;
-// Ints per workgroup in a launch-hint record (decode_mfma_hint_kernel): one 128-byte line, room for the pages
-// of up to 8 waves' first chunks.
-constexpr int kHintInts = 32;
 
 // Launch-ready form of bpt_decode_args (cache strides in bytes).
 struct DecodeParams {
@@ -162,8 +153,6 @@ struct DecodeParams {
   int grid;          // workgroups launched
   int64_t per_forced;  // chunks per workgroup when the caller fixed the split count, else 0
   int piece_cost;      // line units charged per segment start (0 with a fixed split count)
-  int slot_groups;     // LineCut: the first slot_groups workgroups (one per CU) take ranges of slot_weight / 1024
-  int slot_weight;     // times the others' size
   int equal_grid;      // > 0: if every sequence has the same length, the first equal_grid workgroups cut
                        // equal power-of-two partitions instead and the others leave
   float qscale;      // sm_scale * log2(e)
@@ -184,8 +173,6 @@ struct DecodeParams {
   const void* w_offsets;
   int64_t w_sb, w_sq;
   int w_i64;
-  // Launch hints (decode_mfma_hint_kernel), kHintInts ints per workgroup, or NULL.
-  const int32_t* hints;
 };
 
 struct AppendParams {
@@ -318,8 +305,6 @@ hipError_t launch_decode(const DecodeParams& p, int kv_dtype, int scale_kind, in
                          const LaunchEvents& ev = {});
 hipError_t launch_decode_mfma(const DecodeParams& p, int kv_dtype, int scale_kind, hipStream_t stream,
                               const LaunchEvents& ev = {});
-// Launch hints for the matrix-core decode of p (page size >= 16): p.grid records of kHintInts ints.
-hipError_t launch_decode_mfma_hints(const DecodeParams& p, int32_t* hints, hipStream_t stream);
 hipError_t launch_kivi(const KiviParams& p, int fmt, hipStream_t stream);
 // Any even head dim up to 256 and float32 bits-16 caches: one workgroup per (sequence, KV head, split).
 hipError_t launch_kivi_any(const KiviParams& p, int fmt, hipStream_t stream);

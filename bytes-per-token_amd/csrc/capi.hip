@@ -49,12 +49,11 @@ struct Plan {
   int64_t per_forced;
   int equal_grid;  // workgroups that take equal partitions when all lengths are equal (0: none)
   int piece_cost;  // line units charged per segment start
-  int slot_groups, slot_weight;  // the line cut's first block (LineCut)
   size_t ws_out_floats, ws_lse_floats, workspace, counters;
 };
 
 // Plan constants set by bpt_set_tuning (sweeps); a field at its neutral value keeps the built-in choice.
-bpt_tuning g_tuning = {sizeof(bpt_tuning), 0, -1, 0, 0};
+bpt_tuning g_tuning = {sizeof(bpt_tuning), 0, -1, 0};
 std::mutex g_tuning_mutex;
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -171,10 +170,6 @@ int make_plan(const bpt_decode_args* a, Plan* pl) {
   pl->piece_cost = pl->per_forced > 0 ? 0
                    : tune.piece_cost >= 0 ? tune.piece_cost
                    : (pl->mfma && pl->rows >= bpt::kManyRows ? bpt::kManyRowPieceCost : bpt::kDecodePieceCost);
-  // The first workgroup on each CU takes a larger range (LineCut): matrix-core launches of more than one
-  // workgroup per CU, auto plan only.
-  pl->slot_groups = bpt::kComputeUnits;
-  pl->slot_weight = pl->mfma && pl->per_forced == 0 ? (tune.slot_weight > 0 ? tune.slot_weight : bpt::kSlotWeight) : 1024;
   const size_t slots = (size_t)a->batch * pl->HR + pl->grid;
   pl->ws_out_floats = slots * pl->rows_per_group * a->head_dim;
   pl->ws_lse_floats = slots * pl->rows_per_group;
@@ -309,14 +304,6 @@ void line_fields(const Plan& pl, bpt::DecodeParams* p) {
   p->per_forced = pl.per_forced;
   p->equal_grid = pl.equal_grid;
   p->piece_cost = pl.piece_cost;
-  p->slot_groups = pl.slot_groups;
-  p->slot_weight = pl.slot_weight;
-}
-
-// Bytes of launch hints the call takes: one record per workgroup for the matrix-core kernel over pages of
-// 16 tokens or more, none otherwise.
-size_t hint_bytes(const bpt_decode_args* a, const Plan& pl) {
-  return pl.mfma && a->page_size >= 16 && a->batch > 0 ? (size_t)pl.grid * bpt::kHintInts * sizeof(int32_t) : 0;
 }
 
 // Checks a decode call's arguments and buffers on the host and fills its launch parameters (*p, *pl); nothing
@@ -397,14 +384,6 @@ int decode_setup(const bpt_decode_args* a, const char* fn, const Buffers* own, b
   p.lse_out = a->lse_out;
   p.merge_out = a->merge_out;
   p.merge_lse = a->merge_lse;
-  p.hints = nullptr;
-  const size_t hints_need = hint_bytes(a, pl);
-  if (a->hints && hints_need > 0) {
-    if (a->hints_bytes < hints_need || !aligned16(a->hints))
-      return fail(BPT_ERR_INVALID_ARGUMENT, "%s: hints must be a 16-byte aligned buffer of %zu bytes (got %zu)", fn,
-                  hints_need, a->hints_bytes);
-    p.hints = (const int32_t*)a->hints;
-  }
   *out = p;
   return BPT_OK;
 }
@@ -448,56 +427,15 @@ int paged_decode(const bpt_decode_args* a, void* stream, const bpt::LaunchEvents
 int bpt_paged_decode(const bpt_decode_args* a, void* stream) { return paged_decode(a, stream, {}, "bpt_paged_decode"); }
 
 int bpt_set_tuning(const bpt_tuning* t) {
-  const bpt_tuning none = {sizeof(bpt_tuning), 0, -1, 0, 0};
+  const bpt_tuning none = {sizeof(bpt_tuning), 0, -1, 0};
   if (t && t->struct_size != sizeof(bpt_tuning))
     return fail(BPT_ERR_INVALID_ARGUMENT, "bpt_set_tuning: struct_size %u != %zu (stale binding)", t->struct_size,
                 sizeof(bpt_tuning));
   if (t && (t->groups_per_cu < 0 || t->groups_per_cu > 16 || t->piece_cost < -1 || t->piece_cost > 1024 ||
-            t->slot_weight < 0 || t->slot_weight > 4096 || t->min_chunks < 0))
+            t->min_chunks < 0))
     return fail(BPT_ERR_INVALID_ARGUMENT, "bpt_set_tuning: a value is out of range");
   std::lock_guard<std::mutex> lock(g_tuning_mutex);
   g_tuning = t ? *t : none;
-  return BPT_OK;
-}
-
-int bpt_decode_hints(const bpt_decode_args* a, void* hints, size_t* hints_bytes, void* stream) {
-  const char* fn = "bpt_decode_hints";
-  if (!hints_bytes) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: hints_bytes is NULL", fn);
-  Plan pl;
-  int rc = make_plan(a, &pl);
-  if (rc) return rc;
-  const size_t need = hint_bytes(a, pl);
-  if (!hints) {
-    *hints_bytes = need;
-    return BPT_OK;
-  }
-  if (need == 0) return BPT_OK;
-  if (*hints_bytes < need || !aligned16(hints))
-    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: hints must be a 16-byte aligned buffer of %zu bytes (got %zu)", fn, need,
-                *hints_bytes);
-  if (!a->block_table) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: block_table must be non-NULL", fn);
-  if (a->len_offset < 0) return fail(BPT_ERR_INVALID_ARGUMENT, "%s: len_offset must be >= 0", fn);
-  bpt::DecodeParams p{};
-  p.table = a->block_table;
-  p.table_sb = a->table_stride_b;
-  p.table_i64 = a->table_dtype == BPT_IDX_I64;
-  p.lens = a->context_lens;
-  p.B = a->batch;
-  p.Q = a->num_queries;
-  p.Hq = a->num_q_heads;
-  p.Hkv = a->num_kv_heads;
-  p.G = a->num_q_heads / a->num_kv_heads;
-  p.P = a->page_size;
-  p.logP = log2i(a->page_size);
-  p.num_blocks = a->num_blocks;
-  p.max_blocks = a->max_blocks_per_seq;
-  p.n_rg = pl.n_rg;
-  p.HR = pl.HR;
-  line_fields(pl, &p);
-  p.len_cap = pl.len_cap;
-  p.len_offset = a->len_offset;
-  hipError_t e = bpt::launch_decode_mfma_hints(p, (int32_t*)hints, (hipStream_t)stream);
-  if (e != hipSuccess) return hip_fail(fn, e);
   return BPT_OK;
 }
 

@@ -9,13 +9,18 @@ namespace bpt {
 __device__ __forceinline__ int sread(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
 // Cross-workgroup exchange of split-K partials. Workgroups run on different XCDs, whose L2 caches are not
-// coherent with each other. Partials are stored and loaded as agent-scope relaxed (monotonic) atomics, which
-// gfx950 performs coherently at the memory side (the sc1 bit): the stores write through the L2, the loads miss
-// it. Publishing a partial waits for this wave's stores to complete (s_waitcnt vmcnt(0)) before the arrival
-// counter is bumped with an agent-scope atomic; the last arriver then loads every partial with agent-scope
-// atomic loads. This is what LLVM's memory model lowers release / acquire to on this target (a release is
-// "buffer_wbl2 sc1; s_waitcnt vmcnt(0)", an acquire "buffer_inv sc1"), minus the L2 writeback and invalidate,
-// which only non-atomic accesses need: every access to the partials here is itself an agent-scope atomic.
+// coherent with each other. Every access to a partial is an agent-scope relaxed (monotonic) atomic, which
+// gfx950 performs coherently at the memory side (the sc1 bit: stores write through the L2, loads miss it), so
+// no access races. The order between a partial's stores and the arrival that announces it is kept at the
+// instruction level, by what LLVM's release / acquire lowering for this target does minus its whole-L2
+// writeback and invalidate (which only non-atomic accesses need):
+//  * ws_publish: every thread waits until its partial stores have completed at the memory side
+//    (s_waitcnt vmcnt(0)) before the workgroup barrier that precedes the counter's fetch-add;
+//  * ws_acquire: the last arriver issues its partial loads only after the fetch-add has returned (and the
+//    barrier that broadcasts it); the statement keeps the compiler from hoisting them.
+// Both are compiler barriers ("memory" clobbers). The memory model's own fences (release: buffer_wbl2 sc1 +
+// s_waitcnt vmcnt(0), acquire: buffer_inv sc1, per arrival) were measured at 4.3x the headline call's time
+// (37.9 -> 164 us). tests/test_exchange_isa.py checks the emitted sequence on every build.
 
 __device__ __forceinline__ void ws_store(float* ptr, float v) {
   __hip_atomic_store(ptr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -43,6 +48,11 @@ __device__ __forceinline__ void ws_publish() { __asm__ volatile("s_waitcnt vmcnt
 
 // Keeps the compiler from hoisting the partial loads above the arrival that licenses them.
 __device__ __forceinline__ void ws_acquire() { __asm__ volatile("" ::: "memory"); }
+
+// Counts one arrival at a segment's counter (coherently, at the memory side); returns the count before it.
+__device__ __forceinline__ unsigned ws_arrive(unsigned* counter) {
+  return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // A load the whole wave makes from one address, through the scalar cache (the data is read-only here).
 template <typename T>
@@ -128,34 +138,14 @@ __device__ __forceinline__ void load_q(const DecodeParams& p, int64_t base, floa
 // at the segment's start, ahead of its chunks. With check_uniform set, a batch whose sequences all have
 // the same length gets no piece cost. Returns the piece cost the line was built with and whether the
 // lengths were found equal (the same in every thread). Params: any parameter block with B, lens (NULL:
-// every sequence is len_cap long), len_offset and len_cap. first_len: this thread's first length, read ahead
-// by line_first_len (or -1: read here).
+// every sequence is len_cap long), len_offset and len_cap.
 struct SegmentLine {
   int piece_cost;
   bool uniform;
 };
-
-// Sequence b's length as the segment line counts it: clamped to [0, len_cap] after the offset.
-template <typename Params>
-__device__ __forceinline__ int line_len(const Params& p, int b) {
-  const int len = (p.lens ? p.lens[b] : p.len_cap + p.len_offset) - p.len_offset;  // no lengths: all full
-  return len < 0 ? 0 : (len > p.len_cap ? p.len_cap : len);
-}
-
-// The first of the lengths this thread reads for build_segment_line (0 when it reads none). A kernel that
-// requests other data before building the line reads it ahead, so that waiting for it (vector loads complete
-// in order) does not wait for those requests as well.
-template <int NW, typename Params>
-__device__ __forceinline__ int line_first_len(const Params& p) {
-  constexpr int NT = NW * 64;
-  const int b = (int)threadIdx.x * ((p.B + NT - 1) / NT);
-  return b < p.B ? line_len(p, b) : 0;
-}
-
 template <int NW, int CH, typename Params>
 __device__ __forceinline__ SegmentLine build_segment_line(const Params& p, int* s_prefix, int* s_len, int* s_wsum,
-                                                          int piece_cost = 0, bool check_uniform = false,
-                                                          int first_len = -1) {
+                                                          int piece_cost = 0, bool check_uniform = false) {
   constexpr int NT = NW * 64;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -165,7 +155,8 @@ __device__ __forceinline__ SegmentLine build_segment_line(const Params& p, int* 
   const int hi = min(lo + per_thread, B);
   int sum = 0;
   for (int b = lo; b < hi; ++b) {
-    const int len = (b == lo && first_len >= 0) ? first_len : line_len(p, b);
+    int len = (p.lens ? p.lens[b] : p.len_cap + p.len_offset) - p.len_offset;  // no lengths: all full
+    len = len < 0 ? 0 : (len > p.len_cap ? p.len_cap : len);
     s_len[b] = len;
     sum += len > 0 ? (len + CH - 1) / CH + piece_cost : 0;
   }
@@ -234,50 +225,12 @@ __device__ __forceinline__ void write_out(const DecodeParams& p, int b, int qi, 
 // runs on XCD x % 8, each XCD with its own L2), and the line is numbered XCD-major: XCD k takes one
 // contiguous stretch of it. Neighbouring ranges then meet in one L2: the KV heads of a sequence (one page
 // holds all of them, and per-token scales share cache lines across them) and the ranges of one segment.
-// n: the workgroups that share the line (the first n of the launch); x: the workgroup (default: this one).
-__device__ __forceinline__ int64_t line_index(int n, int x) {
+// n: the workgroups that share the line (the first n of the launch).
+__device__ __forceinline__ int64_t line_index(int n) {
+  const int x = blockIdx.x;
   const int q = n >> 3, r = n & 7, k = x & 7;
   return (int64_t)k * q + min(k, r) + (x >> 3);
 }
-__device__ __forceinline__ int64_t line_index(int n) { return line_index(n, (int)blockIdx.x); }
-
-// How the segment line of C units is cut among n workgroups. The first n0 workgroups of the launch (one per
-// CU: dispatched first, their waves are the older ones on every SIMD, which the issue arbiter favours) take
-// ranges of per0 units and lie first on the line; the other n - n0 take ranges of per1 units after them. Each
-// block is numbered XCD-major (line_index). weight: per0 / per1 in 1/1024ths (1024: equal ranges); a fixed
-// partition size (the caller's split count) cuts equal ranges of exactly that size.
-struct LineCut {
-  int64_t n0, per0, per1;
-
-  __device__ __forceinline__ LineCut(int64_t C, int n, int first_block, int weight, int64_t per_forced) {
-    if (per_forced > 0) {
-      n0 = n;
-      per0 = per1 = per_forced;
-      return;
-    }
-    n0 = first_block > 0 && first_block < n ? first_block : n;
-    const int64_t n1 = n - n0;
-    if (n1 == 0 || weight == 1024) {
-      n0 = n;
-      per0 = per1 = (C + n - 1) / n;
-      return;
-    }
-    per1 = (C * 1024 + n0 * weight + n1 * 1024 - 1) / (n0 * weight + n1 * 1024);
-    per0 = (per1 * weight + 1023) / 1024;
-    if (per1 < 1) per1 = 1;
-    if (n0 * per0 + n1 * per1 < C) per1 = (C - n0 * per0 + n1 - 1) / n1;
-  }
-  // The line position of workgroup x of n.
-  __device__ __forceinline__ int64_t position(int x, int n) const {
-    return x < n0 ? line_index((int)n0, x) : n0 + line_index((int)(n - n0), (int)(x - n0));
-  }
-  __device__ __forceinline__ int64_t start(int64_t g) const { return g < n0 ? g * per0 : n0 * per0 + (g - n0) * per1; }
-  __device__ __forceinline__ int64_t size(int64_t g) const { return g < n0 ? per0 : per1; }
-  // The line position whose range holds unit c.
-  __device__ __forceinline__ int64_t owner(int64_t c) const {
-    return c < n0 * per0 ? c / per0 : n0 + (c - n0 * per0) / per1;
-  }
-};
 
 // Sequences with no tokens get zero output, or the caller's partial (workgroups take them round-robin).
 template <int NT>
@@ -379,8 +332,7 @@ template <int RG, int NT>
 __device__ __forceinline__ void arrive_and_combine(const DecodeParams& p, int seg, int b, int hr, int64_t first, int n,
                                                    int rows, int tid, int* s_flag) {
   if (tid == 0) {
-    const unsigned prev = __hip_atomic_fetch_add(p.counters + seg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *s_flag = prev == (unsigned)n - 1u;
+    *s_flag = ws_arrive(p.counters + seg) == (unsigned)n - 1u;
   }
   __syncthreads();
   if (*s_flag) combine_segment<RG, NT>(p, seg, b, hr, first, n, rows, tid);

@@ -515,8 +515,7 @@ __device__ __forceinline__ void arrive_and_combine(const KiviParams& p, int seg,
                                                    int per, int g_first, int n, int tid, int* s_flag) {
   constexpr int D = kHeadDim;
   if (tid == 0) {
-    const unsigned prev = __hip_atomic_fetch_add(p.counters + seg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *s_flag = prev == (unsigned)n - 1u;
+    *s_flag = ws_arrive(p.counters + seg) == (unsigned)n - 1u;
   }
   __syncthreads();
   if (!*s_flag) return;

@@ -488,6 +488,9 @@ void decode_kernel(const DecodeParams p) {
   ChunkRegs<CL> cr;
   ChunkPages<CL> gp;
   int len = sread(s_len[b]);
+  // The head's V scale is read with the piece, not at its merge (after a cold start, a full memory round
+  // trip between a workgroup's last chunk and its end).
+  float vscale = SK == kScaleHead ? load_uniform(p.vs + hr / p.n_rg) : 1.0f;
   {
     const int h = hr / p.n_rg;
     load_q_rows<KV, RG, QS>(p, q, rlen, b, h, hr - h * p.n_rg, rows, part, len,
@@ -533,6 +536,7 @@ void decode_kernel(const DecodeParams p) {
     // The next piece (if the range holds chunks of the next segment): its q rows and this wave's first
     // chunk go in flight now.
     const int b_cur = b, hr_cur = hr, nb_cur = nb;
+    const float vscale_head = vscale;
     const int64_t c_next = pe;
     bool more = false;
     if (c_next < c_end) {
@@ -554,6 +558,7 @@ void decode_kernel(const DecodeParams p) {
         const int hn = hr / p.n_rg;
         load_q_rows<KV, RG, QS>(p, q, rlen, b, hn, hr - hn * p.n_rg, rows, part, len,
                                 SK == kScaleHead ? load_uniform(p.ks + hn) : 1.0f);
+        vscale = SK == kScaleHead ? load_uniform(p.vs + hn) : 1.0f;
         if (wave < kn_end) {
           fetch_pages<KV, CL, PU>(p, b, wave, len, slot, gp);
           issue_chunk<KV, SK, CL, PU>(p, gp, hn, wave, len, slot, part, cr);
@@ -570,7 +575,6 @@ void decode_kernel(const DecodeParams p) {
     const int64_t g_last = (seg_c0 + X + nb_cur - 1) / per;
     const bool whole = g_first == g_last;
     const int64_t wslot = (int64_t)seg + g;
-    const float vscale_head = SK == kScaleHead ? load_uniform(p.vs + h) : 1.0f;
     for (int idx = tid; idx < RG * D; idx += NT) {
       const int r = idx / D;
       const int ch = idx - r * D;

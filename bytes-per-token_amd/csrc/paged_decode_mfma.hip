@@ -111,90 +111,46 @@ __device__ __forceinline__ void substitute(U4 (&rows)[2][2], const U4 (&x)[2], i
   }
 }
 
-// The new rows' stores, one row of K or V per wave: task t (t = the wave's launch-wide index, then every
-// launch-size-th) is row (b, qi, h) of K (t even) or V (t odd), stored only where the decode reads token
-// lens[b] - fuse_q + qi (slot_is_token's rule, as fused_in_place applies it). The work is split so that no
-// wait holds up the first chunk's loads: fused_row_begin (at entry, after the first
-// chunk is requested) requests the row (two bf16 channels per lane), and its slot, length and scale with
-// scalar loads; fused_row_check (after the prologue) requests the block-table entry of the token; fused_row_end
-// (before the chunk loop: the row was requested before or together with the first chunk) checks the slot,
-// quantizes and stores the 128 codes (two bytes per lane), then does any further tasks of the wave in one go.
-struct FusedRow {
-  int64_t task;
-  int b, qi, h, which;
-  uint32_t raw;   // this lane's two channels
-  int64_t blk, off;
-  int first_new;
-  float s;        // the head's scale
-  int e;          // the block-table entry of the token, or -1: no slot
-};
-
-__device__ __forceinline__ int64_t fused_tasks(const DecodeParams& p) { return (int64_t)p.B * p.fuse_q * p.Hkv * 2; }
-
-__device__ __forceinline__ void fused_row_begin(const DecodeParams& p, int64_t task, int lane, FusedRow& r) {
-  r.task = task;
-  r.e = -1;
-  if (task >= fused_tasks(p)) return;
-  r.which = (int)(task & 1);
-  const int64_t row = task >> 1;
-  r.h = (int)(row % p.Hkv);
-  const int64_t bq = row / p.Hkv;
-  r.qi = (int)(bq % p.fuse_q);
-  r.b = (int)(bq / p.fuse_q);
-  const uint16_t* src = (r.which ? p.nv : p.nk) + (int64_t)r.b * p.n_sb + (int64_t)r.qi * p.n_sq + (int64_t)r.h * p.n_sh;
-  r.raw = ((const uint32_t*)src)[lane];
-  const int64_t si = (int64_t)r.b * p.w_sb + (int64_t)r.qi * p.w_sq;
-  r.blk = p.w_i64 ? load_uniform((const int64_t*)p.w_blocks + si) : (int64_t)load_uniform((const int32_t*)p.w_blocks + si);
-  r.off = p.w_i64 ? load_uniform((const int64_t*)p.w_offsets + si) : (int64_t)load_uniform((const int32_t*)p.w_offsets + si);
-  r.first_new = load_uniform(p.lens + r.b) - p.fuse_q;
-  r.s = load_uniform((r.which ? p.vs : p.ks) + r.h);
-}
-
-__device__ __forceinline__ void fused_row_check(const DecodeParams& p, FusedRow& r) {
-  if (r.task >= fused_tasks(p)) return;
-  const int64_t tok = (int64_t)r.first_new + r.qi;
-  if (tok < 0 || (tok >> p.logP) >= p.max_blocks || r.blk < 0 || r.blk >= p.num_blocks) return;
-  r.e = load_uniform((const int32_t*)p.table + table_word(p, r.b, (int)(tok >> p.logP)));
-  r.e = r.e < 0 ? 0 : (r.e >= p.num_blocks ? p.num_blocks - 1 : r.e);
-}
-
-template <int KV>
-__device__ __forceinline__ uint32_t quantize2(uint32_t raw, float s) {
-  uint32_t w = 0u;
+// This launch's share of the new rows' writes: B x fuse_q x Hkv rows of K and of V, one per half-wave,
+// 32 lanes x 4 channels, to the caller's (block, offset) slots: the bytes quant_append_kernel stores.
+template <int KV, int NT>
+__device__ __forceinline__ void fused_append(const DecodeParams& p) {
+  const int lane = threadIdx.x & 31;
+  const int64_t ntask = (int64_t)p.B * p.fuse_q * p.Hkv * 2;
+  for (int64_t task = (int64_t)blockIdx.x * (NT / 32) + (threadIdx.x >> 5); task < ntask;
+       task += (int64_t)gridDim.x * (NT / 32)) {
+    const int which = (int)(task & 1);
+    const int64_t row = task >> 1;
+    const int h = (int)(row % p.Hkv);
+    const int64_t bq = row / p.Hkv;
+    const int qi = (int)(bq % p.fuse_q);
+    const int b = (int)(bq / p.fuse_q);
+    const int64_t si = (int64_t)b * p.w_sb + (int64_t)qi * p.w_sq;
+    const int64_t blk = load_index(p.w_blocks, si, p.w_i64 != 0);
+    const int64_t off = load_index(p.w_offsets, si, p.w_i64 != 0);
+    if (blk < 0 || blk >= p.num_blocks || off < 0 || off >= p.P) continue;
+    if (!slot_is_token(p.table, (int64_t)b * p.table_sb, p.table_i64 != 0, p.max_blocks, p.num_blocks, p.logP,
+                       (int64_t)p.lens[b] - p.fuse_q + qi, blk, off))
+      continue;
+    const uint16_t* src = (which ? p.nv : p.nk) + (int64_t)b * p.n_sb + (int64_t)qi * p.n_sq + (int64_t)h * p.n_sh + 4 * lane;
+    const float s = (which ? p.vs : p.ks)[h];
+    uint32_t w = 0u;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const float y = __fdiv_rn(__uint_as_float(i ? (raw & 0xffff0000u) : (raw << 16)), s);
-    uint32_t code;
-    if constexpr (KV == kKvFp8) {
-      code = f32_to_fp8(clamp_fp8_range(y));
-    } else {
-      float rr = rintf(y);
-      rr = rr > 127.0f ? 127.0f : (rr < -128.0f ? -128.0f : rr);
-      code = (uint32_t)(int32_t)rr & 0xffu;
+    for (int i = 0; i < 4; ++i) {
+      const float y = __fdiv_rn(__uint_as_float((uint32_t)src[i] << 16), s);
+      uint32_t code;
+      if constexpr (KV == kKvFp8) {
+        code = f32_to_fp8(clamp_fp8_range(y));
+      } else {
+        float r = rintf(y);
+        r = r > 127.0f ? 127.0f : (r < -128.0f ? -128.0f : r);
+        code = (uint32_t)(int32_t)r & 0xffu;
+      }
+      w |= code << (8 * i);
     }
-    w |= code << (8 * i);
+    uint8_t* dst = (uint8_t*)(which ? p.v : p.k) + blk * p.kv_sblk + off * p.kv_stok + (int64_t)h * p.kv_shead + 4 * lane;
+    *(uint32_t*)dst = w;
   }
-  return w;
-}
-
-template <int KV>
-__device__ __forceinline__ void fused_row_store(const DecodeParams& p, const FusedRow& r, int lane) {
-  if (r.task >= fused_tasks(p) || r.e < 0 || r.blk != r.e || r.off != ((r.first_new + r.qi) & (p.P - 1))) return;
-  const float s = r.s;
-  uint8_t* dst = (uint8_t*)(r.which ? p.v : p.k) + r.blk * p.kv_sblk + r.off * p.kv_stok + (int64_t)r.h * p.kv_shead;
-  ((uint16_t*)dst)[lane] = (uint16_t)quantize2<KV>(r.raw, s);
-}
-
-template <int KV>
-__device__ __forceinline__ void fused_row_end(const DecodeParams& p, FusedRow& r, int lane, int64_t stride) {
-  fused_row_store<KV>(p, r, lane);
-  for (int64_t t = r.task + stride; t < fused_tasks(p); t += stride) {  // more rows than waves: the rest now
-    FusedRow x;
-    fused_row_begin(p, t, lane, x);
-    fused_row_check(p, x);
-    fused_row_store<KV>(p, x, lane);
-  }
-  r.task = fused_tasks(p);
 }
 
 __device__ __forceinline__ int clamp_page(const DecodeParams& p, int e) {
@@ -224,20 +180,13 @@ __device__ __forceinline__ unsigned fused_in_place(const DecodeParams& p, int b,
 
 // Issue chunk kk's K loads (mfma_issue_k) or V loads and per-token scales (mfma_issue_v). Tokens at or past
 // len read the sequence's last token instead (valid memory, never weighted). PU: a 16-token tile lies
-// inside one page (page_size >= 16), whose id the caller has read (mfma_chunk_pages: pg[t] for tile t);
-// otherwise every token looks up its own page.
+// inside one page (page_size >= 16), whose id is read once per tile with a scalar load; otherwise every
+// token looks up its own page.
 template <bool PU>
-__device__ __forceinline__ int mfma_page(const DecodeParams& p, int b, int t, int tok, const int (&pg)[2]) {
-  if constexpr (PU) return pg[t];
-  return clamp_page(p, ((const int32_t*)p.table)[table_word(p, b, tok >> p.logP)]);
-}
-
-// The pages of chunk kk's two tiles when each lies inside one page (scalar loads of the block table).
-__device__ __forceinline__ void mfma_chunk_pages(const DecodeParams& p, int b, int kk, int len, int (&pg)[2]) {
+__device__ __forceinline__ int mfma_page(const DecodeParams& p, int b, int tile_first, int tok, int len) {
   const int32_t* table = (const int32_t*)p.table;
-#pragma unroll
-  for (int t = 0; t < 2; ++t)
-    pg[t] = clamp_page_u(p, load_uniform(table + table_word(p, b, min(kk * kMChunk + 16 * t, len - 1) >> p.logP)));
+  if constexpr (PU) return clamp_page(p, load_uniform(table + table_word(p, b, min(tile_first, len - 1) >> p.logP)));
+  return clamp_page(p, table[table_word(p, b, tok >> p.logP)]);
 }
 
 // K rows are loaded whole: each load instruction covers eight tokens' 128-byte rows (lane l: token
@@ -245,7 +194,7 @@ __device__ __forceinline__ void mfma_chunk_pages(const DecodeParams& p, int b, i
 // rows of sixteen tokens; mfma_k_operand then rearranges them through LDS.
 template <bool PU, bool FUSE>
 __device__ __forceinline__ void mfma_issue_k(const DecodeParams& p, int b, int h, int kk, int len, int lane, int first_new,
-                                             unsigned in_place, const int (&pg)[2], MChunk& c) {
+                                             unsigned in_place, MChunk& c) {
   const int T0 = kk * kMChunk;
   const int r = lane >> 3, sg = lane & 7;
   const int64_t head_off = (int64_t)h * p.kv_shead + 16 * sg;
@@ -254,7 +203,7 @@ __device__ __forceinline__ void mfma_issue_k(const DecodeParams& p, int b, int h
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int tok = min(T0 + 16 * t + 8 * j + r, len - 1);
-      const int e = mfma_page<PU>(p, b, t, tok, pg);
+      const int e = mfma_page<PU>(p, b, T0 + 16 * t, tok, len);
       c.k[t][j] = load16(p.k + (int64_t)e * p.kv_sblk + (int64_t)(tok & (p.P - 1)) * p.kv_stok + head_off);
     }
   }
@@ -291,7 +240,7 @@ __device__ __forceinline__ void mfma_k_operand(const MChunk& c, U4 (&sk)[2][16][
 
 template <int SK, bool PU, bool FUSE>
 __device__ __forceinline__ void mfma_issue_v(const DecodeParams& p, int b, int h, int kk, int len, int lane, int first_new,
-                                             unsigned in_place, const int (&pg)[2], MChunk& c) {
+                                             unsigned in_place, MChunk& c) {
   const int T0 = kk * kMChunk;
   {
     const int r = lane >> 3, sg = lane & 7;
@@ -301,7 +250,7 @@ __device__ __forceinline__ void mfma_issue_v(const DecodeParams& p, int b, int h
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int tok = min(T0 + 16 * t + 8 * j + r, len - 1);
-        const int e = mfma_page<PU>(p, b, t, tok, pg);
+        const int e = mfma_page<PU>(p, b, T0 + 16 * t, tok, len);
         c.v[t][j] = load16(p.v + (int64_t)e * p.kv_sblk + (int64_t)(tok & (p.P - 1)) * p.kv_stok + head_off);
       }
     }
@@ -310,7 +259,7 @@ __device__ __forceinline__ void mfma_issue_v(const DecodeParams& p, int b, int h
     // One scale per lane (32 tokens x K and V); mfma_compute spreads them through LDS.
     const int t = lane >> 5;
     const int tok = min(T0 + 16 * t + (lane & 15), len - 1);
-    const int e = mfma_page<PU>(p, b, t, tok, pg);
+    const int e = mfma_page<PU>(p, b, T0 + 16 * t, tok, len);
     const int64_t so = (int64_t)e * p.sc_sblk + (int64_t)(tok & (p.P - 1)) * p.sc_stok + (int64_t)h * p.sc_shead;
     c.sc1 = ((lane >> 4) & 1 ? p.vs : p.ks)[so];
   }
@@ -327,9 +276,9 @@ __device__ __forceinline__ void mfma_issue_v(const DecodeParams& p, int b, int h
 
 template <int SK, bool PU, bool FUSE>
 __device__ __forceinline__ void mfma_issue(const DecodeParams& p, int b, int h, int kk, int len, int lane, int first_new,
-                                           unsigned in_place, const int (&pg)[2], MChunk& c) {
-  mfma_issue_k<PU, FUSE>(p, b, h, kk, len, lane, first_new, in_place, pg, c);
-  mfma_issue_v<SK, PU, FUSE>(p, b, h, kk, len, lane, first_new, in_place, pg, c);
+                                           unsigned in_place, MChunk& c) {
+  mfma_issue_k<PU, FUSE>(p, b, h, kk, len, lane, first_new, in_place, c);
+  mfma_issue_v<SK, PU, FUSE>(p, b, h, kk, len, lane, first_new, in_place, c);
 }
 
 // 4 x 4 byte transpose: w[i] byte j -> out[j] byte i.
@@ -541,45 +490,6 @@ __device__ __forceinline__ void mfma_load_q(const DecodeParams& p, int b, int h,
   }
 }
 
-// The first piece of the range of workgroup x of ngroups on the segment line in s_prefix (cut by LineCut):
-// sequence b, segment h (the KV head), first chunk k and chunk end k_end inside the segment, the segment's
-// span of line units; the cut, the range's line position g and its end c_end. any is false when the range
-// holds no chunk (it lies past the line's end, or within one segment's piece-cost units). The decode kernel
-// and the hint kernel both place workgroups with it.
-struct MfmaRange {
-  LineCut cut;
-  int64_t g, c_end;
-  int b, h, k, span, k_end;
-  bool any;
-};
-template <bool HM>
-__device__ __forceinline__ MfmaRange mfma_range(const DecodeParams& p, const int* s_prefix, int x, int ngroups) {
-  const int B = p.B, HR = p.HR;
-  const int64_t SB = s_prefix[B];
-  const int64_t C = (int64_t)HR * SB;
-  MfmaRange r{LineCut(C, ngroups, p.slot_groups, p.slot_weight, p.per_forced), 0, 0, 0, 0, 0, 0, 0, false};
-  if (C == 0) return r;
-  r.g = r.cut.position(x, ngroups);
-  const int64_t c = r.cut.start(r.g);
-  if (c >= C) return r;
-  r.c_end = min(c + r.cut.size(r.g), C);
-  const int64_t hc = HM ? c / SB : 0;  // head-major: the KV head whose stretch holds c
-  const int64_t cb = HM ? c - hc * SB : c;
-  int lo = 0, hi = B - 1;  // largest b with prefix[b] <= cb (HM), HR * prefix[b] <= cb (sequence-major)
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if ((HM ? 1 : (int64_t)HR) * s_prefix[mid] <= cb) lo = mid; else hi = mid - 1;
-  }
-  r.b = lo;
-  r.span = s_prefix[lo + 1] - s_prefix[lo];
-  r.h = HM ? (int)hc : (int)((c - (int64_t)HR * s_prefix[lo]) / r.span);
-  const int64_t seg_c0 = HM ? (int64_t)r.h * SB + s_prefix[lo] : (int64_t)HR * s_prefix[lo] + (int64_t)r.h * r.span;
-  r.k = max((int)(c - seg_c0) - p.piece_cost, 0);
-  r.k_end = (int)(min(r.c_end, seg_c0 + r.span) - seg_c0 - p.piece_cost);
-  r.any = r.k_end > r.k;
-  return r;
-}
-
 template <int KV, int SK, bool PU, bool QS, int NW, bool FUSE>
 __global__ __launch_bounds__(NW * 64, kMfmaWavesPerSimd) void decode_mfma_kernel(const DecodeParams p) {
   constexpr int NT = NW * 64;
@@ -603,69 +513,8 @@ __global__ __launch_bounds__(NW * 64, kMfmaWavesPerSimd) void decode_mfma_kernel
   const int kq = lane >> 4, n = lane & 15;
   const int B = p.B;
 
-  const int len0 = line_first_len<NW>(p);  // read ahead of the hinted loads (see build_segment_line)
-  const int rows = p.Q * p.G;
-  typename MQ<KV, QS>::T qb[MQ<KV, QS>::kOps];
-  int rlen = 0;
-  MChunk cr;
-  // Fused writes: the sequence's first new token (its new rows are the last fuse_q of its length) and the
-  // head's scales, which quantize them.
-  int first_new = 0;
-  unsigned in_place = 0u;
-  float ks_new = 1.0f, vs_new = 1.0f, qscale = p.qscale;
-  int pg[2] = {0, 0};  // the pages of the chunk in flight (page_size >= 16)
-  // A piece's per-sequence and per-head values and its q rows.
-  auto start_piece = [&](int sb, int sh, int slen) {
-    if constexpr (FUSE) {
-      first_new = load_uniform(p.lens + sb) - p.fuse_q;
-      in_place = fused_in_place(p, sb, first_new);
-      ks_new = load_uniform(p.ks + sh);
-      vs_new = load_uniform(p.vs + sh);
-    }
-    qscale = p.qscale * (SK == kScaleHead ? load_uniform(p.ks + sh) : 1.0f);
-    mfma_load_q<KV, QS>(p, sb, sh, rows, slen, lane, qb, rlen);
-  };
-
-  // ---- launch hint: the first chunk's loads go out before the prologue -----------------------------------
-  // A hint (decode_mfma_hint_kernel, run once for the lengths and block table every layer of a forward pass
-  // shares) names this workgroup's first piece (sequence, KV head, first chunk, chunk end, length) and the
-  // pages of each wave's first chunk. Those q rows and that chunk are requested at entry, and the pages the
-  // block table holds for the chunk are read beside them. The prologue then computes the range itself;
-  // whatever the hint got wrong (a hint from other lengths, another table or another launch) is requested
-  // again, so results never depend on the hint, only the time to the first chunk does.
-  int hb = -1, hh = 0, hk = 0, hk_end = 0, hlen = 0;
-  int tpg[2] = {0, 0};
-  if constexpr (PU) {
-    if (p.hints) {
-      const int32_t* hp = p.hints + (int64_t)blockIdx.x * kHintInts;
-      if (load_uniform(hp) == 1 && p.len_cap > 0) {
-        hb = min(max(load_uniform(hp + 1), 0), B - 1);
-        hh = min(max(load_uniform(hp + 2), 0), p.Hkv - 1);
-        hk = min(max(load_uniform(hp + 3), 0), p.len_cap / kMChunk + 1);
-        hk_end = load_uniform(hp + 4);
-        hlen = min(max(load_uniform(hp + 5), 1), p.len_cap);
-        start_piece(hb, hh, hlen);
-        if (hk + wave < hk_end) {
-          pg[0] = clamp_page_u(p, load_uniform(hp + 8 + 2 * wave));
-          pg[1] = clamp_page_u(p, load_uniform(hp + 9 + 2 * wave));
-          mfma_issue<SK, PU, FUSE>(p, hb, hh, hk + wave, hlen, lane, first_new, in_place, pg, cr);
-          mfma_chunk_pages(p, hb, hk + wave, hlen, tpg);
-        }
-      }
-    }
-  }
-  // Fused writes: this wave's row is requested now and stored once the first chunk is in (fused_row_end).
-  FusedRow fr;
-  const int64_t fr_stride = (int64_t)gridDim.x * NW;
-  if constexpr (FUSE) fused_row_begin(p, (int64_t)blockIdx.x * NW + wave, lane, fr);
-  // A workgroup leaving early stores its rows and waits for any hinted loads still in flight.
-  auto leave = [&]() {
-    if constexpr (FUSE) fused_row_end<KV>(p, fr, lane, fr_stride);
-    if (hb >= 0) __asm__ volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-  };
-
-  build_segment_line<NW, kMChunk>(p, s_prefix, s_len, s_wsum, p.piece_cost, false, len0);
-  if constexpr (FUSE) fused_row_check(p, fr);
+  if constexpr (FUSE) fused_append<KV, NT>(p);
+  build_segment_line<NW, kMChunk>(p, s_prefix, s_len, s_wsum, p.piece_cost);
   zero_empty_sequences<NT>(p, s_prefix);
 
   // ---- this workgroup's range of chunks (segments are (sequence, KV head): HR = Hkv) ---------------------
@@ -678,41 +527,68 @@ __global__ __launch_bounds__(NW * 64, kMfmaWavesPerSimd) void decode_mfma_kernel
   constexpr bool HM = NW == kMfmaManyRowWaves;
   const int HR = p.HR;
   const int64_t SB = s_prefix[B];  // one KV head's line units
-  const MfmaRange r0 = mfma_range<HM>(p, s_prefix, (int)blockIdx.x, gridDim.x);
-  if (!r0.any) {  // no chunk in this range (past the line's end, or within one segment's piece-cost units)
-    leave();
-    return;
+  const int64_t C = (int64_t)HR * SB;
+  if (C == 0) return;
+  const int64_t per = p.per_forced > 0 ? p.per_forced : (C + gridDim.x - 1) / gridDim.x;
+  const int64_t g = line_index(gridDim.x);
+  const int64_t c_begin = g * per;
+  if (c_begin >= C) return;
+  const int64_t c_end = min(c_begin + per, C);
+  int64_t c = c_begin;
+
+  int b, h;
+  {
+    const int64_t hc = HM ? c / SB : 0;  // head-major: the KV head whose stretch holds c
+    const int64_t cb = HM ? c - hc * SB : c;
+    int lo = 0, hi = B - 1;  // largest b with prefix[b] <= cb (HM), HR * prefix[b] <= cb (sequence-major)
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if ((HM ? 1 : (int64_t)HR) * s_prefix[mid] <= cb) lo = mid; else hi = mid - 1;
+    }
+    b = sread(lo);
+    h = (int)hc;
   }
-  const LineCut cut = r0.cut;
-  const int64_t g = r0.g;
-  const int64_t c_end = r0.c_end;
-  int b = sread(r0.b), h = sread(r0.h), k = sread(r0.k);
   // A segment spans X line units, then its nb chunks; a range that starts among the X units starts with
   // the segment's first chunk.
   const int X = p.piece_cost;
-  int span = sread(r0.span);
+  int span = sread(s_prefix[b + 1] - s_prefix[b]);
   int nb = span - X;
   auto seg_start = [&](int sb, int sh, int sspan) -> int64_t {
     return HM ? (int64_t)sh * SB + s_prefix[sb] : (int64_t)HR * s_prefix[sb] + (int64_t)sh * sspan;
   };
-
-  // The first piece's q rows and first chunk are requested here unless the hint did so already; every later
-  // piece's while the previous piece's waves are merged.
-  int len = sread(s_len[b]);
-  if (!(hb == b && hh == h && hk == k && hlen == len && hk_end == r0.k_end)) {
-    start_piece(b, h, len);
-    if (k + wave < r0.k_end) {
-      if constexpr (PU) mfma_chunk_pages(p, b, k + wave, len, pg);
-      mfma_issue<SK, PU, FUSE>(p, b, h, k + wave, len, lane, first_new, in_place, pg, cr);
-    }
-  } else if (k + wave < r0.k_end && (tpg[0] != pg[0] || tpg[1] != pg[1])) {
-    pg[0] = tpg[0];
-    pg[1] = tpg[1];
-    mfma_issue<SK, PU, FUSE>(p, b, h, k + wave, len, lane, first_new, in_place, pg, cr);
+  int k;
+  {
+    if (!HM) h = sread((int)((c - (int64_t)HR * s_prefix[b]) / span));
+    k = sread(max((int)(c - seg_start(b, h, span)) - X, 0));
+  }
+  const int rows = p.Q * p.G;
+  {
+    // A range that holds no chunk (it lies within one segment's X units) has nothing to do.
+    const int64_t seg_c0 = seg_start(b, h, span);
+    if (min(c_end, seg_c0 + span) - seg_c0 - X <= k) return;
   }
 
-  // The wave's fused row is stored now: its data came in ahead of the first chunk or together with it.
-  if constexpr (FUSE) fused_row_end<KV>(p, fr, lane, fr_stride);
+  // The first piece's q rows and first chunk are requested before the loop; every later piece's while the
+  // previous piece's waves are merged.
+  typename MQ<KV, QS>::T qb[MQ<KV, QS>::kOps];
+  int rlen;
+  MChunk cr;
+  int len = sread(s_len[b]);
+  // Fused writes: the sequence's first new token (its new rows are the last fuse_q of its length) and the
+  // head's scales, which quantize them.
+  int first_new = FUSE ? load_uniform(p.lens + b) - p.fuse_q : 0;
+  unsigned in_place = FUSE ? fused_in_place(p, b, first_new) : 0u;
+  float ks_new = FUSE ? load_uniform(p.ks + h) : 1.0f, vs_new = FUSE ? load_uniform(p.vs + h) : 1.0f;
+  float qscale = p.qscale * (SK == kScaleHead ? load_uniform(p.ks + h) : 1.0f);
+  // The head's V scale is read with the piece, not at its merge: after a cold start that read is a full
+  // memory round trip, which at a workgroup's last merge would stand between its last chunk and its end.
+  float vscale = SK == kScaleHead ? load_uniform(p.vs + h) : 1.0f;
+  mfma_load_q<KV, QS>(p, b, h, rows, len, lane, qb, rlen);
+  {
+    const int64_t seg_c0 = seg_start(b, h, span);
+    const int k_end = (int)(min(c_end, seg_c0 + span) - seg_c0 - X);
+    if (k + wave < k_end) mfma_issue<SK, PU, FUSE>(p, b, h, k + wave, len, lane, first_new, in_place, cr);
+  }
 
   for (;;) {
     const int64_t seg_c0 = seg_start(b, h, span);
@@ -730,18 +606,17 @@ __global__ __launch_bounds__(NW * 64, kMfmaWavesPerSimd) void decode_mfma_kernel
       const int kn = kk + NW;
       mfma_compute<KV, SK, QS, FUSE>(cr, s_k[wave], s_sc[wave], kk, lane, qb, qscale, rlen, m, l, o, ks_new, vs_new,
                                      [&]() {
-                                       if (kn < k_end) {
-                                         if constexpr (PU) mfma_chunk_pages(p, b, kn, len, pg);
-                                         mfma_issue_k<PU, FUSE>(p, b, h, kn, len, lane, first_new, in_place, pg, cr);
-                                       }
+                                       if (kn < k_end)
+                                         mfma_issue_k<PU, FUSE>(p, b, h, kn, len, lane, first_new, in_place, cr);
                                      });
-      if (kn < k_end) mfma_issue_v<SK, PU, FUSE>(p, b, h, kn, len, lane, first_new, in_place, pg, cr);
+      if (kn < k_end) mfma_issue_v<SK, PU, FUSE>(p, b, h, kn, len, lane, first_new, in_place, cr);
       kk = kn;
     }
 
     // The next piece (if the range holds chunks of the next segment): its q rows and this wave's first
     // chunk go in flight now.
     const int b_cur = b, h_cur = h, nb_cur = nb;
+    const float vscale_head = vscale;
     const int64_t c_next = pe;
     bool more = false;
     if (c_next < c_end) {
@@ -774,11 +649,16 @@ __global__ __launch_bounds__(NW * 64, kMfmaWavesPerSimd) void decode_mfma_kernel
       more = kn_end > 0;
       if (more) {
         len = sread(s_len[b]);
-        start_piece(b, h, len);
-        if (wave < kn_end) {
-          if constexpr (PU) mfma_chunk_pages(p, b, wave, len, pg);
-          mfma_issue<SK, PU, FUSE>(p, b, h, wave, len, lane, first_new, in_place, pg, cr);
+        if constexpr (FUSE) {
+          first_new = load_uniform(p.lens + b) - p.fuse_q;
+          in_place = fused_in_place(p, b, first_new);
+          ks_new = load_uniform(p.ks + h);
+          vs_new = load_uniform(p.vs + h);
         }
+        qscale = p.qscale * (SK == kScaleHead ? load_uniform(p.ks + h) : 1.0f);
+        vscale = SK == kScaleHead ? load_uniform(p.vs + h) : 1.0f;
+        mfma_load_q<KV, QS>(p, b, h, rows, len, lane, qb, rlen);
+        if (wave < kn_end) mfma_issue<SK, PU, FUSE>(p, b, h, wave, len, lane, first_new, in_place, cr);
       }
     }
 
@@ -801,11 +681,10 @@ __global__ __launch_bounds__(NW * 64, kMfmaWavesPerSimd) void decode_mfma_kernel
     // The segment's number in line order: workspace slots seg + g stay distinct across segments only when
     // segments are numbered in the order the line holds them.
     const int seg = HM ? h_cur * B + b_cur : b_cur * HR + h_cur;
-    const int64_t g_first = cut.owner(seg_c0 + X);  // the line positions holding the segment's first and last chunks
-    const int64_t g_last = cut.owner(seg_c0 + X + nb_cur - 1);
+    const int64_t g_first = (seg_c0 + X) / per;  // the workgroups holding the segment's first and last chunks
+    const int64_t g_last = (seg_c0 + X + nb_cur - 1) / per;
     const bool whole = g_first == g_last;
     const int64_t wslot = (int64_t)seg + g;
-    const float vscale_head = SK == kScaleHead ? load_uniform(p.vs + h_cur) : 1.0f;
     // Four channels of one row per thread, rows < `rows` only.
     for (int idx = tid; idx < rows * (D / 4); idx += NT) {
       const int r = idx / (D / 4);
@@ -842,65 +721,9 @@ __global__ __launch_bounds__(NW * 64, kMfmaWavesPerSimd) void decode_mfma_kernel
       arrive_and_combine<RG, NT>(p, seg, b_cur, h_cur, g_first, (int)(g_last - g_first + 1), rows, tid, &s_last);
     }
     if (!more) break;
+    c = c_next;
     __syncthreads();  // the LDS merge buffers are rewritten by the next piece
   }
-}
-
-// Launch hints for decode_mfma_kernel with NW-wave workgroups (page size >= 16), one 32-int record per
-// workgroup of the launch: [0] 1 when its range holds a chunk, [1..5] its first piece's sequence, KV head,
-// first chunk, chunk end and length, [8 + 2 w + t] the page of tile t of wave w's first chunk. Computed by
-// one workgroup from the same segment line and range rule as the decode kernel (build_segment_line,
-// mfma_range), for the lengths and block table every layer of a forward pass shares.
-template <int NW>
-__global__ __launch_bounds__(1024) void decode_mfma_hint_kernel(const DecodeParams p, int32_t* hints) {
-  extern __shared__ int s_dyn[];
-  int* s_prefix = s_dyn;
-  int* s_len = s_dyn + p.B + 1;
-  __shared__ int s_wsum[16];
-  build_segment_line<16, kMChunk>(p, s_prefix, s_len, s_wsum, p.piece_cost);
-  constexpr bool HM = NW == kMfmaManyRowWaves;
-  const int32_t* table = (const int32_t*)p.table;
-  for (int x = threadIdx.x; x < p.grid; x += 1024) {
-    const MfmaRange r = mfma_range<HM>(p, s_prefix, x, p.grid);
-    int32_t* o = hints + (int64_t)x * kHintInts;
-    int4 rec[kHintInts / 4];
-#pragma unroll
-    for (int i = 0; i < kHintInts / 4; ++i) rec[i] = int4{0, 0, 0, 0};
-    if (r.any) {
-      const int len = s_len[r.b];
-      rec[0] = int4{1, r.b, r.h, r.k};
-      rec[1] = int4{r.k_end, len, 0, 0};
-#pragma unroll
-      for (int w = 0; w < NW; ++w) {
-        const int kk = r.k + w;
-        if (kk < r.k_end) {
-          int pgw[2];
-#pragma unroll
-          for (int t = 0; t < 2; ++t)
-            pgw[t] = clamp_page(p, table[table_word(p, r.b, min(kk * kMChunk + 16 * t, len - 1) >> p.logP)]);
-          int4& q = rec[2 + w / 2];
-          if (w & 1) {
-            q.z = pgw[0];
-            q.w = pgw[1];
-          } else {
-            q.x = pgw[0];
-            q.y = pgw[1];
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < kHintInts / 4; ++i) ((int4*)o)[i] = rec[i];
-  }
-}
-
-hipError_t launch_decode_mfma_hints(const DecodeParams& p, int32_t* hints, hipStream_t stream) {
-  const size_t lds = (size_t)(2 * p.B + 1) * sizeof(int);
-  if (mfma_waves(p.Q * p.G) == kMfmaManyRowWaves)
-    hipLaunchKernelGGL(decode_mfma_hint_kernel<kMfmaManyRowWaves>, dim3(1), dim3(1024), lds, stream, p, hints);
-  else
-    hipLaunchKernelGGL(decode_mfma_hint_kernel<kDecodeWaves>, dim3(1), dim3(1024), lds, stream, p, hints);
-  return hipGetLastError();
 }
 
 template <int KV, int SK, int NW, bool FUSE>

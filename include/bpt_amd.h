@@ -139,41 +139,21 @@ typedef struct {
   const float* merge_out;  /* optional contiguous float32 [B, Q, Hq, D]: a partial over other tokens ... */
   const float* merge_lse;  /* ... and its log-sum-exp [B, Q, Hq] (natural log, -inf if empty), merged into
                               out (and lse_out) exactly, as kernels/reference.py:205-211 merges parts */
-
-  /* Launch hints (optional, NULL for none): what bpt_decode_hints wrote for this launch. The kernel checks
-     every hint against what it computes and ignores any that differ, so a stale one costs time and never
-     changes a result. */
-  const void* hints;
-  size_t hints_bytes;
 } bpt_decode_args;
 
 #define BPT_DECODE_NONCAUSAL 1
-
-/*
- * Launch hints for bpt_paged_decode, written on the device from context_lens and block_table in one small
- * launch: where each workgroup's range of the batch starts and the pages of its waves' first chunks, so that
- * the decode's first KV loads go out at kernel entry instead of after its own planning. Build them once per
- * forward pass, after the per-forward metadata (bpt_paged_prepare), and pass them to every layer's decode:
- * the launch shape, lengths and block table are the same for all layers.
- *   hints == NULL: *hints_bytes receives the size the call needs (0: its kernel takes no hints); nothing
- *   is launched. Otherwise *hints_bytes is the buffer's size (16-byte aligned).
- * Replaces: the per-call planning of kernels/kv_attention.py:190-245 (split and grid, done there on the
- * host from `tokens=`), done here once per forward like engine/kv_cache.py:140-156 PagedKVCache.prepare.
- */
-int bpt_decode_hints(const bpt_decode_args* a, void* hints, size_t* hints_bytes, void* stream);
 
 /*
  * Plan constants for tuning sweeps, process-wide (bench.py --tune). A field at its neutral value keeps the
  * library's own choice; NULL restores every default. Calls planned on other threads meanwhile see either
  * setting. No counterpart in the reference's kernel interface: it is what fastserve's tuning sweep
  * (experiments/m7.py:292-335, over the launcher's split and num_warps arguments) varies, for the knobs this
- * launch has instead (workgroups per CU, the per-segment charge, the first workgroups' range weight).
+ * launch has instead (workgroups per CU, the per-segment charge, the minimum chunks per workgroup).
  */
 typedef struct {
   uint32_t struct_size;  /* sizeof(bpt_tuning) */
   int32_t groups_per_cu; /* workgroups per CU of the auto plan (0: built-in) */
   int32_t piece_cost;    /* line units charged per segment start (-1: built-in) */
-  int32_t slot_weight;   /* range size of the first workgroup on each CU over the others', x1024 (0: built-in) */
   int32_t min_chunks;    /* chunks per workgroup below which the auto plan launches fewer (0: built-in) */
 } bpt_tuning;
 int bpt_set_tuning(const bpt_tuning* t);

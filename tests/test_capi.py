@@ -291,16 +291,20 @@ def test_append_decode_refuses_a_bad_decode_block_before_storing(built_lib, fmt)
         _lib.check(built_lib.bpt_paged_append_decode(ctypes.byref(a), ctypes.byref(d), None))
 
 
-def test_hint_size_query_is_host_only(built_lib):
-    """bpt_decode_hints with no buffer reports the size a call's hints take (one 128-byte record per workgroup of
-    the matrix-core kernel; none for the vector kernel) without launching anything."""
-    from bpt_amd.paged_attention import _plan
-
-    for fmt, hq, want_records in (("fp8", 16, True), ("bf16", 16, False), ("fp8", 8, False)):
-        q, k, v, table, lens, ks, vs = cpu_case(fmt=fmt, b=6, hq=hq, max_blocks=64, nb=512)
-        a, _, _ = _plan(q, k, v, table, lens, ks, vs, 0.1, 1024, None)
-        size = ctypes.c_size_t(123)
-        assert built_lib.bpt_decode_hints(ctypes.byref(a), None, ctypes.byref(size), None) == 0
-        assert size.value == (a.grid_groups * 128 if want_records else 0), (fmt, hq)
-    assert built_lib.bpt_decode_hints(ctypes.byref(a), None, None, None) == _lib.BPT_ERR_INVALID_ARGUMENT
-    assert b"hints_bytes" in built_lib.bpt_last_error()
+def test_tuning_overrides_the_plan_and_resets(built_lib):
+    """bpt_set_tuning changes what the auto plan launches (the sweep's knobs) and NULL restores the built-in plan;
+    out-of-range values are refused."""
+    q, k, v, table, lens, ks, vs = cpu_case(b=32, max_blocks=256, nb=4096)
+    base = decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=4096)
+    try:
+        _lib.set_tuning(groups_per_cu=3)
+        grid, _, _, _ = decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=4096)
+        assert grid == 256 * 3
+        _lib.set_tuning(min_chunks=64)
+        grid, _, _, _ = decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=4096)
+        assert grid == (32 * 128 * 8 + 63) // 64
+        with pytest.raises(ValueError, match="out of range"):
+            _lib.set_tuning(groups_per_cu=99)
+    finally:
+        _lib.set_tuning()
+    assert decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=4096) == base
