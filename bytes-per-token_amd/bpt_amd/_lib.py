@@ -185,6 +185,13 @@ class KiviArgs(ctypes.Structure):
         ("workspace_bytes", ctypes.c_size_t),
         ("counters", _vp),
         ("counters_bytes", ctypes.c_size_t),
+        ("tail_k", _vp),
+        ("tail_v", _vp),
+        ("tail_stride_b", _i64),
+        ("tail_stride_h", _i64),
+        ("tail_stride_t", _i64),
+        ("tail_dtype", _i32),
+        ("tail_len", _i32),
     ]
 
 

@@ -188,7 +188,7 @@ def _format(kv: Any) -> int:
     raise ValueError(f"bits must be 4, 8 or 16, got {kv.bits}")
 
 
-def _launch(q, kv, lengths, scale, split, n_splits, out, lse) -> None:
+def _launch(q, kv, lengths, scale, split, n_splits, out, lse, tail=None) -> None:
     fmt = _format(kv)
     b, hq, d = q.shape
     kc, vc = kv.k_codes, kv.v_codes
@@ -240,6 +240,16 @@ def _launch(q, kv, lengths, scale, split, n_splits, out, lse) -> None:
     a.out_stride_b, a.out_stride_h, a.out_stride_s = out.stride(0), out.stride(1), out.stride(2)
     a.lse = lse.data_ptr()
     a.lse_stride_b, a.lse_stride_h, a.lse_stride_s = lse.stride(0), lse.stride(1), lse.stride(2)
+    if tail is not None:
+        tk, tv = tail
+        _require(tk.dim() == 4 and tk.shape == tv.shape and tuple(tk.shape[:2]) == (b, hkv) and tk.shape[3] == d,
+                 f"tail keys and values must be [{b}, {hkv}, tail_len, {d}]")
+        _require(tk.dtype == tv.dtype and tk.dtype in _Q_CODES, "tail keys and values must share a bf16/f16/f32 dtype")
+        _require(tk.stride() == tv.stride() and tk.stride(-1) == 1, "tail keys and values must share strides, channels contiguous")
+        _require(tk.device == dev and tv.device == dev, f"the tail must be on {dev}")
+        a.tail_k, a.tail_v = tk.data_ptr(), tv.data_ptr()
+        a.tail_stride_b, a.tail_stride_h, a.tail_stride_t = tk.stride(0), tk.stride(1), tk.stride(2)
+        a.tail_dtype, a.tail_len = _Q_CODES[tk.dtype], tk.shape[2]
     lib = _lib.lib()
     ws_bytes, cnt_bytes = ctypes.c_size_t(0), ctypes.c_size_t(0)
     _lib.check(lib.bpt_kivi_plan(ctypes.byref(a), ctypes.byref(ws_bytes), ctypes.byref(cnt_bytes)))
@@ -282,11 +292,18 @@ def decode_attention(
     return out, lse
 
 
-def attend(q: torch.Tensor, kv: Any, lengths: torch.Tensor, scale: float, **launch: int | None) -> torch.Tensor:
+def attend(q: torch.Tensor, kv: Any, lengths: torch.Tensor, scale: float, *,
+           tail: tuple[torch.Tensor, torch.Tensor] | None = None, **launch: int | None) -> torch.Tensor:
     """Decode attention over a KIVI cache: [B, Hq, D] float32 (kv_attention.py:248-252).
 
     The result does not depend on the split; a given `split` is still checked against the key group. The
     tokens past `tokens` (when given) are not read, as in decode_attention.
+
+    tail: the cache's full-precision tail (tail_k, tail_v) [B, Hkv, n, D], n <= 64 tokens every row sees in
+    full (the tokens whose key group is not complete yet). Its attention is merged into the result in the same
+    launch: what QuantizedKVCache.attend's decode branch computes with three (integration/kv_cache.py:172-185:
+    decode over the codes, partial_attention over the tail, merge_partials). A row with no codes gets the
+    tail's attention alone.
     """
     b, hq, d = q.shape
     t_max = kv.k_codes.shape[2]
@@ -302,5 +319,7 @@ def attend(q: torch.Tensor, kv: Any, lengths: torch.Tensor, scale: float, **laun
     whole = max(-(-reach // step), 1) * step  # one split covering all of them
     out = torch.empty((b, hq, 1, d), dtype=torch.float32, device=q.device)
     lse = torch.empty((b, hq, 1), dtype=torch.float32, device=q.device)
-    _launch(q, kv, lengths, scale, whole, 1, out, lse)
+    if tail is not None and tail[0].shape[2] == 0:
+        tail = None
+    _launch(q, kv, lengths, scale, whole, 1, out, lse, tail)
     return out[:, :, 0]

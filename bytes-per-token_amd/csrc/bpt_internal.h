@@ -231,7 +231,15 @@ struct KiviParams {
   int q_dtype;
   int D, split;       // head dim; tokens per split
   int gshift_tokens;  // log2(tokens per key group)
+  // Full-precision tail merged into the (single) split's result: [B, Hkv, tail_len, D], strides in elements.
+  const void* tk;
+  const void* tv;
+  int64_t tk_sb, tk_sh, tk_st;
+  int tail_dtype, tail_len;
 };
+
+// The most tail tokens a KIVI call takes (a tail is shorter than a key group).
+constexpr int kKiviMaxTail = 64;
 
 // Launch-ready form of bpt_kivi_quant_args: KIVI quantize-on-write of keys and values [B, Hkv, T, D].
 struct KiviQuantParams {

@@ -445,9 +445,11 @@ int bpt_set_tuning(const bpt_tuning* t) {
 //
 // `scratch` holds, on every GPU the library runs on, kScratchWorkspace bytes of partials followed by
 // kScratchCounters bytes of arrival counters. The counters sit at a fixed offset, so the invariant that every
-// completed call leaves them zero holds across calls of any shape; they are cleared once per device, by a
-// fill kernel on the first call's stream. In host code `scratch` names a host-side stand-in: its device
-// address, different on each GPU, comes from hipGetSymbolAddress and is the only form passed to kernels.
+// completed call leaves them zero holds across calls of any shape. They start at zero: the array has static
+// storage and no initializer, so the code object's loader zero-fills it on every GPU (no clear is queued, so
+// a first call made under stream capture records nothing extra into the graph). In host code `scratch` names
+// a host-side stand-in: its device address, different on each GPU, comes from hipGetSymbolAddress and is the
+// only form passed to kernels.
 namespace {
 
 constexpr size_t kScratchWorkspace = (size_t)30 << 20;
@@ -460,15 +462,10 @@ static __device__ __align__(256) uint8_t scratch[kScratchWorkspace + kScratchCou
 
 namespace {
 
-__global__ void zero_words_kernel(uint32_t* p, size_t n) {
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0u;
-}
-
 std::mutex g_scratch_mutex;
 uint8_t* g_scratch[kMaxDevices];  // device address of `scratch` on each GPU, once set up
 
-// This device's scratch address; on the device's first call, looks it up (with the device current) and queues
-// the counters' clear on `stream`.
+// This device's scratch address; on the device's first call, looks it up (with the device current).
 int scratch_for(hipStream_t stream, uint8_t** out, const char* fn) {
   hipDevice_t dev = 0;
   hipError_t e = hipStreamGetDevice(stream, &dev);
@@ -485,10 +482,6 @@ int scratch_for(hipStream_t stream, uint8_t** out, const char* fn) {
       const hipError_t e2 = hipSetDevice(cur);
       if (e == hipSuccess) e = e2;
     }
-    if (e != hipSuccess) return hip_fail(fn, e);
-    uint32_t* counters = (uint32_t*)((uint8_t*)ptr + kScratchWorkspace);
-    hipLaunchKernelGGL(zero_words_kernel, dim3(256), dim3(256), 0, stream, counters, kScratchCounters / 4);
-    e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(fn, e);
     g_scratch[dev] = (uint8_t*)ptr;
   }
@@ -548,6 +541,16 @@ int bpt_kivi_decode(const bpt_kivi_args* a, void* stream) {
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: q, codes, lengths, out and lse must be non-NULL", fn);
   if (quant && (!a->k_scale || !a->k_zero || !a->v_scale || !a->v_zero))
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: 4- and 8-bit codes need their key and value grids", fn);
+  if (a->tail_len < 0 || a->tail_len > bpt::kKiviMaxTail)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: tail_len %d must be in [0, %d]", fn, a->tail_len, bpt::kKiviMaxTail);
+  if (a->tail_len > 0) {
+    if (!a->tail_k || !a->tail_v)
+      return fail(BPT_ERR_INVALID_ARGUMENT, "%s: a tail needs tail_k and tail_v", fn);
+    if (a->num_splits != 1)
+      return fail(BPT_ERR_INVALID_ARGUMENT, "%s: a tail is merged into one split's result (num_splits 1)", fn);
+    if (a->tail_dtype < BPT_F_BF16 || a->tail_dtype > BPT_F_F32)
+      return fail(BPT_ERR_INVALID_ARGUMENT, "%s: tail_dtype must be bf16, f16 or f32", fn);
+  }
   if (pl.any) {  // element-aligned tensors are enough for the float32 kernel
     if (((uintptr_t)a->k_codes | (uintptr_t)a->v_codes) % pl.eb)
       return fail(BPT_ERR_INVALID_ARGUMENT, "%s: code tensors must be aligned to their element size", fn);
@@ -617,6 +620,13 @@ int bpt_kivi_decode(const bpt_kivi_args* a, void* stream) {
   p.D = a->head_dim;
   p.split = a->split;
   p.gshift_tokens = quant ? log2i(a->group) : 0;
+  p.tk = a->tail_k;
+  p.tv = a->tail_v;
+  p.tk_sb = a->tail_stride_b;
+  p.tk_sh = a->tail_stride_h;
+  p.tk_st = a->tail_stride_t;
+  p.tail_dtype = a->tail_dtype;
+  p.tail_len = a->tail_len;
   hipError_t e = pl.any ? bpt::launch_kivi_any(p, a->format, (hipStream_t)stream)
                         : bpt::launch_kivi(p, a->format, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(fn, e);

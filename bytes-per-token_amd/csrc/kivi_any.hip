@@ -78,19 +78,16 @@ __global__ __launch_bounds__(kAnyThreads) void kivi_any_kernel(const KiviParams 
   const uint16_t* vs = kQuant ? p.vs + (int64_t)b * p.t_sb + (int64_t)h * p.t_sh : nullptr;
   const uint16_t* vz = kQuant ? p.vz + (int64_t)b * p.t_sb + (int64_t)h * p.t_sh : nullptr;
 
-  for (int t0 = lo; t0 < hi; t0 += kAnyThreads) {
-    const int n = min(kAnyThreads, hi - t0);
+  // One block of n <= 256 tokens: key(i, c) and value(i, c) give channel c of the block's token i.
+  auto block = [&](int n, auto key, auto value) {
     // ---- scores of this thread's token for every head ---------------------------------------------------
     {
-      const int t = t0 + tid;
       float sc[kAnyMaxG];
 #pragma unroll
       for (int g = 0; g < kAnyMaxG; ++g) sc[g] = 0.0f;
       if (tid < n) {
-        const int64_t go = (int64_t)(t >> p.gshift_tokens) * p.g_sg;
         for (int c = 0; c < D; ++c) {
-          const float x = kivi_element<FMT>(kc, c_st, t, c, D, kQuant ? half_at(ks, go + c) : 1.0f,
-                                            kQuant ? half_at(kz, go + c) : 0.0f);
+          const float x = key(tid, c);
 #pragma unroll
           for (int g = 0; g < kAnyMaxG; ++g) sc[g] = g < G ? fmaf(s_q[g][c], x, sc[g]) : sc[g];
         }
@@ -130,16 +127,34 @@ __global__ __launch_bounds__(kAnyThreads) void kivi_any_kernel(const KiviParams 
       if (e < G * D) {
         const int g = e / D, c = e - g * D;
         float a = acc[k] * s_alpha[g];
-        for (int i = 0; i < n; ++i) {
-          const int t = t0 + i;
-          const float x = kivi_element<FMT>(vc, c_st, t, c, D, kQuant ? half_at(vs, t) : 1.0f,
-                                            kQuant ? half_at(vz, t) : 0.0f);
-          a = fmaf(s_p[g][i], x, a);
-        }
+        for (int i = 0; i < n; ++i) a = fmaf(s_p[g][i], value(i, c), a);
         acc[k] = a;
       }
     }
     __syncthreads();
+  };
+
+  for (int t0 = lo; t0 < hi; t0 += kAnyThreads) {
+    block(
+        min(kAnyThreads, hi - t0),
+        [&](int i, int c) {
+          const int t = t0 + i;
+          const int64_t go = (int64_t)(t >> p.gshift_tokens) * p.g_sg;
+          return kivi_element<FMT>(kc, c_st, t, c, D, kQuant ? half_at(ks, go + c) : 1.0f,
+                                   kQuant ? half_at(kz, go + c) : 0.0f);
+        },
+        [&](int i, int c) {
+          const int t = t0 + i;
+          return kivi_element<FMT>(vc, c_st, t, c, D, kQuant ? half_at(vs, t) : 1.0f, kQuant ? half_at(vz, t) : 0.0f);
+        });
+  }
+  // The full-precision tail (one split: it goes with the last), one more block (fastserve
+  // integration/kv_cache.py:172-185 attends it separately and merges; the online softmax is that merge).
+  if (p.tail_len > 0 && s == p.S - 1) {
+    const int64_t t0 = (int64_t)b * p.tk_sb + (int64_t)h * p.tk_sh;
+    block(
+        p.tail_len, [&](int i, int c) { return load_float(p.tk, t0 + (int64_t)i * p.tk_st + c, p.tail_dtype); },
+        [&](int i, int c) { return load_float(p.tv, t0 + (int64_t)i * p.tk_st + c, p.tail_dtype); });
   }
 
   // ---- the split's output and log-sum-exp (natural log) -----------------------------------------------

@@ -489,11 +489,68 @@ __device__ __forceinline__ int64_t lse_index(const KiviParams& p, int b, int hq,
 }
 
 // Splits past a row's length: out 0, lse -inf (workgroups take the rows round-robin).
+// The attention state of the full-precision tail for the G query heads of (b, h), in the wave states' form
+// (base 2, reference point m, bias kBias): s_tm[r] = m_r = max_t s_rt, s_tl[r] = sum_t 2^(s_rt - m_r + kBias),
+// s_to[r D + ch] = sum_t 2^(s_rt - m_r + kBias) v_t[ch], where s_rt = sm_scale log2(e) q_r . k_t over the
+// tail_len tokens (fastserve integration/kv_cache.py:179-182: partial_attention over the tail, in float32).
+// s_tp: G x kKiviMaxTail floats of scratch. The whole workgroup calls it; it ends with a barrier.
 template <int NT>
-__device__ __forceinline__ void zero_empty_splits(const KiviParams& p, const int* s_prefix) {
+__device__ __forceinline__ void tail_state(const KiviParams& p, int b, int h, float* s_tp, float* s_tm, float* s_tl,
+                                           float* s_to) {
+  constexpr int D = kHeadDim;
+  const int T = p.tail_len, G = p.G;
+  const int64_t kv0 = (int64_t)b * p.tk_sb + (int64_t)h * p.tk_sh;
+  for (int i = threadIdx.x; i < G * T; i += NT) {
+    const int r = i / T, t = i - r * T;
+    const int64_t qo = (int64_t)b * p.q_sb + (int64_t)(h * G + r) * p.q_sh;
+    const int64_t ko = kv0 + (int64_t)t * p.tk_st;
+    float acc = 0.0f;
+#pragma unroll 8
+    for (int c = 0; c < D; ++c) acc = fmaf(load_float(p.q, qo + c, p.q_dtype), load_float(p.tk, ko + c, p.tail_dtype), acc);
+    s_tp[r * kKiviMaxTail + t] = acc * p.qscale;
+  }
+  __syncthreads();
+  for (int r = threadIdx.x; r < G; r += NT) {
+    float m = kNegInf;
+    for (int t = 0; t < T; ++t) m = fmaxf(m, s_tp[r * kKiviMaxTail + t]);
+    float l = 0.0f;
+    for (int t = 0; t < T; ++t) {
+      const float w = fast_exp2(s_tp[r * kKiviMaxTail + t] - m + kBias);
+      s_tp[r * kKiviMaxTail + t] = w;
+      l += w;
+    }
+    s_tm[r] = m;
+    s_tl[r] = l;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < G * D; i += NT) {
+    const int r = i / D, ch = i - r * D;
+    float o = 0.0f;
+    for (int t = 0; t < T; ++t) o = fmaf(s_tp[r * kKiviMaxTail + t], load_float(p.tv, kv0 + (int64_t)t * p.tk_st + ch, p.tail_dtype), o);
+    s_to[r * D + ch] = o;
+  }
+  __syncthreads();
+}
+
+template <int NT, bool TAIL>
+__device__ __forceinline__ void zero_empty_splits(const KiviParams& p, const int* s_prefix, float* s_tp, float* s_tm,
+                                                  float* s_tl, float* s_to) {
   constexpr int D = kHeadDim;
   for (int b = blockIdx.x; b < p.B; b += gridDim.x) {
     const int nb = s_prefix[b + 1] - s_prefix[b];
+    if (TAIL && nb == 0) {  // no codes: the result is the tail's attention alone (one split)
+      for (int h = 0; h < p.Hkv; ++h) {
+        tail_state<NT>(p, b, h, s_tp, s_tm, s_tl, s_to);
+        for (int i = threadIdx.x; i < p.G * D; i += NT) {
+          const int r = i / D, ch = i - r * D;
+          const int hq = h * p.G + r;
+          p.out[out_index(p, b, hq, 0) + ch] = s_to[r * D + ch] / s_tl[r];
+          if (ch == 0) p.lse[lse_index(p, b, hq, 0)] = (s_tm[r] - kBias + __log2f(s_tl[r])) * kLn2;
+        }
+        __syncthreads();  // the tail buffers are rewritten by the next head
+      }
+      continue;
+    }
     const int active = (nb + p.cps - 1) / p.cps;
     const int per_head = (p.S - active) * D;
     for (int i = threadIdx.x; i < p.Hq * per_head; i += NT) {
@@ -562,7 +619,7 @@ __device__ __forceinline__ void arrive_and_combine(const KiviParams& p, int seg,
 
 }  // namespace
 
-template <int FMT, int RP>
+template <int FMT, int RP, bool TAIL>
 __global__ __launch_bounds__(kDecodeWaves * 64, 2) void kivi_decode_kernel(const KiviParams p) {
   constexpr int NW = kDecodeWaves;
   constexpr int NT = NW * 64;
@@ -584,6 +641,11 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void kivi_decode_kernel(const
   __shared__ float s_m[NW][RP];
   __shared__ float s_l[NW][RP];
   __shared__ float s_o[NW][RP][D];
+  __shared__ float s_tm[RP], s_tl[RP];  // the tail's state (tail_state); its scratch and sums reuse the fold buffers
+  static_assert(sizeof(s_qh) >= RP * kKiviMaxTail * sizeof(float) && sizeof(s_ql) >= RP * D * sizeof(float),
+                "the fold buffers hold the tail's scratch");
+  float* const s_tp = (float*)&s_qh[0][0][0];
+  float* const s_to = (float*)&s_ql[0][0][0];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -594,7 +656,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void kivi_decode_kernel(const
   const int G = p.G;
 
   build_segment_line<NW, kChunk>(p, s_prefix, s_len, s_wsum);
-  zero_empty_splits<NT>(p, s_prefix);
+  zero_empty_splits<NT, TAIL>(p, s_prefix, s_tp, s_tm, s_tl, s_to);
 
   // ---- this workgroup's range of chunks on the line of (sequence, KV head) segments ---------------------
   const int C = HR * s_prefix[B];  // < 2^31, checked on the host
@@ -667,6 +729,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void kivi_decode_kernel(const
 
   for (;;) {
     const int j_cur = k / p.cps;
+    const int k_first = k;
     const int k_end = piece_end(k, c);
     const int seg_c0 = HR * s_prefix[b] + h * nb;
     const int split_end = min((j_cur + 1) * p.cps, nb);
@@ -778,6 +841,9 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void kivi_decode_kernel(const
       }
     }
     __syncthreads();
+    // The piece that starts the segment also holds the tail's tokens (one split: the tail goes with it).
+    const bool with_tail = TAIL && k_first == 0;
+    if (with_tail) tail_state<NT>(p, b_cur, h_cur, s_tp, s_tm, s_tl, s_to);
 
     // ---- merge the waves; write the split's result, or this piece's partial ---------------------------
     const int seg = (b_cur * HR + h_cur) * p.S + j_cur;
@@ -793,6 +859,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void kivi_decode_kernel(const
       float M = kNegInf;
 #pragma unroll
       for (int w = 0; w < NW; ++w) M = fmaxf(M, s_m[w][r]);
+      if (with_tail) M = fmaxf(M, s_tm[r]);
       const float mu = M == kNegInf ? 0.0f : M;
       float L = 0.0f, A = 0.0f;
 #pragma unroll
@@ -801,6 +868,11 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void kivi_decode_kernel(const
         const float e = lw > 0.0f ? fast_exp2(s_m[w][r] - mu) : 0.0f;
         L += lw * e;
         A += lw > 0.0f ? s_o[w][r][ch] * e : 0.0f;
+      }
+      if (with_tail) {
+        const float e = fast_exp2(s_tm[r] - mu);
+        L += s_tl[r] * e;
+        A += s_to[r * D + ch] * e;
       }
       const float out = L > 0.0f ? A / L : 0.0f;
       const float lse2 = L > 0.0f ? M - kBias + __log2f(L) : kNegInf;
@@ -824,15 +896,21 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void kivi_decode_kernel(const
   }
 }
 
-template <int FMT>
+template <int FMT, bool TAIL>
 static hipError_t launch_fmt(const KiviParams& p, hipStream_t stream) {
   dim3 grid(p.grid), block(kDecodeWaves * 64);
   const size_t lds = (size_t)(2 * p.B + 1) * sizeof(int);
-  if (p.G <= 2) hipLaunchKernelGGL((kivi_decode_kernel<FMT, 2>), grid, block, lds, stream, p);
-  else if (p.G <= 4) hipLaunchKernelGGL((kivi_decode_kernel<FMT, 4>), grid, block, lds, stream, p);
-  else if (p.G <= 8) hipLaunchKernelGGL((kivi_decode_kernel<FMT, 8>), grid, block, lds, stream, p);
-  else hipLaunchKernelGGL((kivi_decode_kernel<FMT, 16>), grid, block, lds, stream, p);
+  if (p.G <= 2) hipLaunchKernelGGL((kivi_decode_kernel<FMT, 2, TAIL>), grid, block, lds, stream, p);
+  else if (p.G <= 4) hipLaunchKernelGGL((kivi_decode_kernel<FMT, 4, TAIL>), grid, block, lds, stream, p);
+  else if (p.G <= 8) hipLaunchKernelGGL((kivi_decode_kernel<FMT, 8, TAIL>), grid, block, lds, stream, p);
+  else hipLaunchKernelGGL((kivi_decode_kernel<FMT, 16, TAIL>), grid, block, lds, stream, p);
   return hipGetLastError();
+}
+
+// Calls with a full-precision tail run their own instantiation: the tail's merge costs the others nothing.
+template <int FMT>
+static hipError_t launch_fmt(const KiviParams& p, hipStream_t stream) {
+  return p.tail_len > 0 ? launch_fmt<FMT, true>(p, stream) : launch_fmt<FMT, false>(p, stream);
 }
 
 hipError_t launch_kivi(const KiviParams& p, int fmt, hipStream_t stream) {

@@ -257,6 +257,18 @@ typedef struct {
   size_t workspace_bytes;
   void* counters;
   size_t counters_bytes;
+
+  /* Full-precision tail (optional; tail_len = 0 for none): the tokens whose key group is not complete yet,
+     as fastserve's QuantizedKVCache keeps them (integration/kv_cache.py:139-158), attended in the same launch
+     and merged into the result (its :172-185: partial_attention over the tail, then merge_partials). Every
+     row sees all tail_len tokens; a row with no codes gets the tail's attention alone. num_splits must be 1.
+       tail_k, tail_v  [B, Hkv, tail_len, D] (strides tail_stride_{b,h,t} in elements; channel stride 1),
+                       BF16 / F16 / F32 (tail_dtype); at most 64 tokens. */
+  const void* tail_k;
+  const void* tail_v;
+  int64_t tail_stride_b, tail_stride_h, tail_stride_t;
+  int32_t tail_dtype; /* bpt_float_dtype */
+  int32_t tail_len;
 } bpt_kivi_args;
 
 /*
