@@ -291,6 +291,9 @@ def measure_workload(name: str, flush, iters: int, warmup: int) -> dict:
             "unique_gbps": round(ub / (cmed * 1e-3) / 1e9, 1),
             "logical_gbps": round(nbytes / (cmed * 1e-3) / 1e9, 1),
         }
+    log(f"{name}: {row['us_per_call']} us/call, {row['gbps']} GB/s ({row['pct_of_peak']}% of 8 TB/s); read floors "
+        f"{row['read_floor_us']} us contiguous, {row['page_read_floor_us']} us through its pages"
+        + (f"; unique {row['unique_gbps']} GB/s" if "unique_gbps" in row else ""))
     if name == "qwen3-1.7b-int8":
         write, row["append_bytes"] = append_call(w)
         wt, _ = timed_calls(write, flush, iters, warmup)
@@ -475,6 +478,101 @@ def measure_norm_quant(flush, iters: int, warmup: int) -> dict:
     return table
 
 
+TUNE_PAGED = {  # workload -> batch / length cap (None: the full workload)
+    "qwen3-1.7b-fp8": [(None, None), (1, 2943), (4, None)],
+    "qwen3-1.7b-int8": [(None, None), (1, None), (16, 2048)],
+    "qwen3-8b-fp8-long": [(None, None)],
+    "qwen3-1.7b-verify": [(None, None), (2, None)],
+    "qwen3-0.6b-bf16": [(None, None)],
+}
+TUNE_KIVI_SHAPES = [(1, 32768), (1, 2048), (16, 2048), (64, 8192)]  # fastserve benchmarks/configs/m7_kernels.yaml:33-38
+TUNE_KIVI_SPLITS = [32, 64, 128, 256, 512, 1024, 2048, 4096, 8192]
+
+
+def tune(args) -> int:
+    """Sweep the decode plans' knobs (bpt_set_tuning: workgroups per CU, the per-segment charge, the fewest
+    chunks per workgroup) on the paged workloads and the KIVI kernel at fastserve's tuning shapes, and the
+    KIVI split (fastserve experiments/m7.py:292-335 sweeps split x num_warps for its Triton kernel). Cold calls
+    (1 GiB read between calls), event-timed; each shape is warmed up before its first point and its built-in
+    point measured again after the last (the lower of the two is reported), since the first calls on a freshly
+    built workload run slower. One JSON line with every point, the best of each shape on stderr."""
+    import torch
+
+    from bpt_amd import _lib, decode_plan, kivi, measure, paged_decode_attention, workloads
+
+    torch.cuda.set_device(0)
+    flush = measure.ReadProbe(args.flush_bytes)
+    points = []
+
+    def timed(call, iters=args.tune_iters):
+        total, _ = timed_calls(call, flush, iters, 3)
+        return round(statistics.median(total) * 1e3, 2)
+
+    for name, cases in TUNE_PAGED.items():
+        for batch, cap in cases:
+            w = workloads.make(name, device="cuda:0", seed=0, batch=batch, length_cap=cap)
+            out = torch.empty(tuple(w.q.shape), dtype=torch.bfloat16, device="cuda:0")
+            label = f"{name}" + (f" batch {batch}" if batch else "") + (f" cap {cap}" if cap else "")
+            timed(lambda: paged_decode_attention(*w.args(), **w.kwargs(), out=out), iters=30)  # warm-up
+            best = None
+            for gpc in (0, 1, 2, 3, 4):
+                for cost in (-1, 0, 4, 8, 12, 16):
+                    for mc in ((0, 1, 2, 4, 8, 16) if batch else (0,)):
+                        _lib.set_tuning(groups_per_cu=gpc, piece_cost=cost, min_chunks=mc)
+                        grid = decode_plan(*w.args(), **w.kwargs())[0]
+                        us = timed(lambda: paged_decode_attention(*w.args(), **w.kwargs(), out=out))
+                        pt = {"plan": "paged", "shape": label, "groups_per_cu": gpc, "piece_cost": cost,
+                              "min_chunks": mc, "grid": grid, "us": us}
+                        points.append(pt)
+                        if best is None or us < best["us"]:
+                            best = pt
+            _lib.set_tuning()
+            default = next(p for p in points if p["shape"] == label and p["groups_per_cu"] == 0
+                           and p["piece_cost"] == -1 and p["min_chunks"] == 0)
+            default["us"] = min(default["us"], timed(lambda: paged_decode_attention(*w.args(), **w.kwargs(), out=out)))
+            best = default if default["us"] <= best["us"] else best
+            log(f"tune {label}: built-in {default['us']} us (grid {default['grid']}); best {best['us']} us at "
+                f"groups/CU {best['groups_per_cu'] or 'built-in'}, piece cost "
+                f"{best['piece_cost'] if best['piece_cost'] >= 0 else 'built-in'}, min chunks {best['min_chunks'] or 'built-in'}"
+                f" (grid {best['grid']})")
+            del w, out
+            torch.cuda.empty_cache()
+
+    for batch, context in TUNE_KIVI_SHAPES:
+        for bits in (4, 8, 16):
+            w = workloads.make_kivi(batch, context, bits, device="cuda:0", seed=batch + context)
+            scale = workloads.HEAD_DIM**-0.5
+            label = workloads.kivi_name(batch, context, bits)
+            timed(lambda: kivi.attend(w.q, w, w.lengths, scale, tokens=context), iters=30)  # warm-up
+            best = None
+            for gpc in (0, 1, 2, 3, 4):
+                for mc in (0, 2, 4, 8, 16):
+                    _lib.set_tuning(groups_per_cu=gpc, min_chunks=mc)
+                    us = timed(lambda: kivi.attend(w.q, w, w.lengths, scale, tokens=context))
+                    pt = {"plan": "kivi", "shape": label, "groups_per_cu": gpc, "min_chunks": mc, "us": us}
+                    points.append(pt)
+                    if best is None or us < best["us"]:
+                        best = pt
+            _lib.set_tuning()
+            for split in [s for s in TUNE_KIVI_SPLITS if s < context] + [context]:
+                us = timed(lambda: kivi.decode_attention(w.q, w, w.lengths, scale, tokens=context, split=split))
+                points.append({"plan": "kivi-split", "shape": label, "split": split, "us": us})
+            default = next(p for p in points if p["shape"] == label and p["plan"] == "kivi"
+                           and p["groups_per_cu"] == 0 and p["min_chunks"] == 0)
+            default["us"] = min(default["us"], timed(lambda: kivi.attend(w.q, w, w.lengths, scale, tokens=context)))
+            best = default if default["us"] <= best["us"] else best
+            splits = [p for p in points if p["shape"] == label and p["plan"] == "kivi-split"]
+            bs = min(splits, key=lambda p: p["us"])
+            log(f"tune {label}: attend built-in {default['us']} us; best {best['us']} us at groups/CU "
+                f"{best['groups_per_cu'] or 'built-in'}, min chunks {best['min_chunks'] or 'built-in'}; "
+                f"decode_attention splits {min(p['us'] for p in splits)}-{max(p['us'] for p in splits)} us "
+                f"(best split {bs['split']})")
+            del w
+            torch.cuda.empty_cache()
+    print(json.dumps({"tune": points}), flush=True)
+    return 0
+
+
 def cpu_model() -> str:
     """The host CPU as /proc/cpuinfo names it: model name, family / model / stepping, cache size."""
     fields = {}
@@ -572,6 +670,8 @@ def main() -> int:
     ap.add_argument("--profile", action="store_true", help="short run for rocprofv3 (no JSON line)")
     ap.add_argument("--cascade", action="store_true", help="with --profile: the shared-prefix cascade call")
     ap.add_argument("--append", action="store_true", help="with --profile: the step's quantize-on-write call")
+    ap.add_argument("--tune", action="store_true", help="sweep the plan constants (one JSON line of points)")
+    ap.add_argument("--tune-iters", type=int, default=10, help="with --tune: timed calls per point")
     ap.add_argument("--fused", action="store_true",
                     help="with --profile: the decode call with the last token's store in the same launch")
     args = ap.parse_args()
@@ -587,6 +687,8 @@ def main() -> int:
 
     if args.profile:
         return profile_pass(args)
+    if args.tune:
+        return tune(args)
 
     import torch
 

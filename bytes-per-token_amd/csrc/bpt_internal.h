@@ -325,8 +325,8 @@ hipError_t launch_fp8_encode(const float* x, float scale, uint8_t* out, int64_t 
 int64_t read_probe_groups(uint64_t bytes);
 hipError_t launch_read_probe(const void* buf, uint64_t bytes, float* partial, hipStream_t stream,
                              const LaunchEvents& ev = {});
-int64_t page_read_probe_groups(int B, int Hkv, int len_cap);
-hipError_t launch_page_read_probe(const DecodeParams& p, int row_bytes, bool with_scales, float* partial,
+// The decode's ranges read only (p.grid workgroups, p.HR segments per sequence, `chunk`-token chunks).
+hipError_t launch_page_read_probe(const DecodeParams& p, int row_bytes, int chunk, bool with_scales, float* partial,
                                   hipStream_t stream, const LaunchEvents& ev = {});
 hipError_t launch_copy_probe(void* dst, const void* src, uint64_t bytes, hipStream_t stream);
 

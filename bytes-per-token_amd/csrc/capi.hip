@@ -106,16 +106,17 @@ int make_plan(const bpt_decode_args* a, Plan* pl) {
   const int64_t table_cap = (int64_t)a->max_blocks_per_seq * a->page_size;
   pl->len_cap = (int)(a->max_context < table_cap ? a->max_context : table_cap);
   const int64_t max_nb = (pl->len_cap + pl->chunk - 1) / pl->chunk;
-  const int64_t seq_chunks = (int64_t)a->batch * max_nb;  // bound on the chunk prefix sum
-  const int64_t seq_cost = (int64_t)a->batch * (max_nb + bpt::kMaxPieceCost);  // and on the line's
-  if (seq_cost > 0x7fffffffLL / (hr > 0 ? hr : 1))
-    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: batch x context x heads too large", fn);
-  const int64_t bound_c = seq_chunks * hr;
   bpt_tuning tune;
   {
     std::lock_guard<std::mutex> lock(g_tuning_mutex);
     tune = g_tuning;
   }
+  const int64_t seq_chunks = (int64_t)a->batch * max_nb;  // bound on the chunk prefix sum
+  const int64_t max_cost = tune.piece_cost > bpt::kMaxPieceCost ? tune.piece_cost : bpt::kMaxPieceCost;
+  const int64_t seq_cost = (int64_t)a->batch * (max_nb + max_cost);  // and on the line's
+  if (seq_cost > 0x7fffffffLL / (hr > 0 ? hr : 1))
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: batch x context x heads too large", fn);
+  const int64_t bound_c = seq_chunks * hr;
   const int groups_per_cu =
       tune.groups_per_cu > 0 ? tune.groups_per_cu
       : pl->mfma ? bpt::mfma_groups_per_cu(pl->rows)
@@ -248,9 +249,14 @@ int make_kivi_plan(const bpt_kivi_args* a, KiviPlan* pl) {
   const int64_t seq_chunks = (int64_t)a->batch * max_nb;
   if (seq_chunks > 0x7fffffffLL / a->num_kv_heads)
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: batch x tokens x heads too large", fn);
-  int64_t grid = (int64_t)bpt::kComputeUnits * bpt::kDecodeGroupsPerCu;
+  bpt_tuning tune;
+  {
+    std::lock_guard<std::mutex> lock(g_tuning_mutex);
+    tune = g_tuning;
+  }
+  int64_t grid = (int64_t)bpt::kComputeUnits * (tune.groups_per_cu > 0 ? tune.groups_per_cu : bpt::kDecodeGroupsPerCu);
   const int64_t bound_c = seq_chunks * a->num_kv_heads;
-  const int64_t min_chunks = bpt::kivi_min_chunks(bound_c, grid);
+  const int64_t min_chunks = tune.min_chunks > 0 ? tune.min_chunks : bpt::kivi_min_chunks(bound_c, grid);
   const int64_t by_chunks = (bound_c + min_chunks - 1) / min_chunks;
   if (by_chunks < grid) grid = by_chunks;
   pl->grid = (int)(grid < 1 ? 1 : grid);
@@ -947,7 +953,7 @@ int bpt_page_read_probe(const bpt_decode_args* a, float* partial_sums, int64_t* 
   Plan pl;
   int rc = make_plan(a, &pl);
   if (rc) return rc;
-  const int64_t g = bpt::page_read_probe_groups(a->batch, a->num_kv_heads, pl.len_cap);
+  const int64_t g = a->batch > 0 ? pl.grid : 0;  // the decode's workgroups
   if (num_groups) *num_groups = g;
   if (!partial_sums) return BPT_OK;
   if (!a->k_cache || !a->v_cache || !a->block_table)
@@ -983,6 +989,9 @@ int bpt_page_read_probe(const bpt_decode_args* a, float* partial_sums, int64_t* 
   p.num_blocks = a->num_blocks;
   p.len_cap = pl.len_cap;
   p.len_offset = a->len_offset;
+  p.HR = pl.HR;
+  p.n_rg = pl.n_rg;
+  p.grid = (int)g;
   bpt::LaunchEvents ev;
   ev.start = (hipEvent_t)start_event;
   ev.stop = (hipEvent_t)stop_event;
@@ -991,7 +1000,15 @@ int bpt_page_read_probe(const bpt_decode_args* a, float* partial_sums, int64_t* 
     if (e == hipSuccess) e = hipEventRecord(ev.stop, (hipStream_t)stream);
     return e == hipSuccess ? BPT_OK : hip_fail(fn, e);
   }
-  hipError_t e = bpt::launch_page_read_probe(p, a->head_dim * eb, per_token, partial_sums, (hipStream_t)stream, ev);
+  // A chunk is read as whole 16-byte loads over 64 lanes: rows per load divide it, 1, 2, 4 or 8 loads per
+  // lane, and one lane per token for the scales.
+  const int rows_per_load = 64 / (a->head_dim * eb / 16);
+  const int loads = pl.chunk / rows_per_load;
+  if (pl.chunk % rows_per_load || loads > 8 || (loads & (loads - 1)) || pl.chunk > 64)
+    return fail(BPT_ERR_INVALID_ARGUMENT, "%s: %d-token chunks of %d-byte rows are not read by this probe", fn,
+                pl.chunk, a->head_dim * eb);
+  hipError_t e = bpt::launch_page_read_probe(p, a->head_dim * eb, pl.chunk, per_token, partial_sums,
+                                             (hipStream_t)stream, ev);
   return e == hipSuccess ? BPT_OK : hip_fail(fn, e);
 }
 

@@ -152,9 +152,10 @@ typedef struct {
  */
 typedef struct {
   uint32_t struct_size;  /* sizeof(bpt_tuning) */
-  int32_t groups_per_cu; /* workgroups per CU of the auto plan (0: built-in) */
+  int32_t groups_per_cu; /* workgroups per CU of the auto plan, paged and KIVI (0: built-in) */
   int32_t piece_cost;    /* line units charged per segment start (-1: built-in) */
-  int32_t min_chunks;    /* chunks per workgroup below which the auto plan launches fewer (0: built-in) */
+  int32_t min_chunks;    /* chunks per workgroup below which the auto plan launches fewer, paged and KIVI
+                            (0: built-in) */
 } bpt_tuning;
 int bpt_set_tuning(const bpt_tuning* t);
 
@@ -444,10 +445,11 @@ int bpt_read_probe_timed(const void* buf, uint64_t bytes, float* partial_sums, v
                          void* stop_event);
 
 /* The page-read probe: every K and V row (and per-token scale) that bpt_paged_decode over the same args
- * reads, fetched through the same block table and context lengths with no attention math (one float per
- * workgroup into partial_sums). It is the read floor of a decode call's own access pattern. Call with
+ * reads, fetched through the same block table and context lengths, in the decode's own order (its segments,
+ * workgroup ranges and chunks, the same number of workgroups) with no attention math and no merges (one float
+ * per workgroup into partial_sums). It is the read floor of a decode call's own access pattern. Call with
  * partial_sums = NULL to get the workgroup count in *num_groups. Optional events as bpt_read_probe_timed
- * (both or neither). Uses only the cache, scale, table and length fields of args. No reference
+ * (both or neither). Uses the shape, cache, scale, table and length fields of args. No reference
  * counterpart. */
 int bpt_page_read_probe(const bpt_decode_args* args, float* partial_sums, int64_t* num_groups, void* stream,
                         void* start_event, void* stop_event);
