@@ -44,6 +44,10 @@ constexpr int kChunk = 32;  // tokens per chunk: two 16-token tiles
 template <int FMT>
 struct KF {
   static constexpr bool kQuant = FMT == kKivi4 || FMT == kKivi8;
+  // Value products over offset codes with the zero points taken out afterwards (compute, value_zero_out):
+  // always for 4-bit codes; for 8-bit codes but at 16 rows, where the extra accumulator would spill.
+  template <int CPL>
+  static constexpr bool kZeroFold = FMT == kKivi4 || (FMT == kKivi8 && CPL < 32);
   static constexpr bool kBf16 = FMT == kKiviBf16;
   static constexpr int kKU4 = FMT == kKivi4 ? 1 : (FMT == kKivi8 ? 2 : 4);  // 16-byte K loads per lane per tile
   static constexpr int kVWords = FMT == kKivi4 ? 1 : (FMT == kKivi8 ? 2 : 4);  // V dwords per lane per token
@@ -102,6 +106,44 @@ __device__ __forceinline__ f16x8 bytes8_minus(uint32_t w0, uint32_t w1, const ui
   const u32x4 r = {sub_h2(pair_lo(w0), z[0]), sub_h2(pair_hi(w0), z[1]), sub_h2(pair_lo(w1), z[2]),
                    sub_h2(pair_hi(w1), z[3])};
   return __builtin_bit_cast(f16x8, r);
+}
+
+// The f16 pair (1024 + b0, 1024 + b1) from bytes 0 and 1 (pair_lo) or 2 and 3 (pair_hi), for the value
+// product, which takes codes with the 1024 left in (the zero points are taken out after it).
+__device__ __forceinline__ f16x8 bytes8(uint32_t w0, uint32_t w1) {
+  const u32x4 r = {pair_lo(w0), pair_hi(w0), pair_lo(w1), pair_hi(w1)};
+  return __builtin_bit_cast(f16x8, r);
+}
+
+// Byte j of token words a (first) and b as the low half and the high half of one dword, the other bytes 0:
+// 4-bit codes of one channel pair for two tokens, split into f16 pairs by nib_lo / nib_hi.
+__device__ __forceinline__ uint32_t byte_pair(uint32_t a, uint32_t b, int j) {
+  return __builtin_amdgcn_perm(b, a, 0x0c000c00u | ((uint32_t)(4 + j) << 16) | (uint32_t)j);
+}
+// (1024 + low nibble) and (1024 + 16 * high nibble) of both halves, as f16 pairs: one v_and_or_b32 each,
+// the mask from a scalar register and 0x64006400 (f16 1024, 1024) from a vector register `k` that the caller
+// keeps (a VOP3 instruction takes no literal here, and reads one scalar register at most; left to itself
+// the compiler splits the AND and the OR into two instructions with literals).
+__device__ __forceinline__ uint32_t and_or_k(uint32_t x, uint32_t mask, uint32_t k) {
+  uint32_t r;
+  __asm__("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(mask), "v"(k));
+  return r;
+}
+__device__ __forceinline__ uint32_t nib_lo(uint32_t x, uint32_t k) { return and_or_k(x, 0x000F000Fu, k); }
+__device__ __forceinline__ uint32_t nib_hi(uint32_t x, uint32_t k) { return and_or_k(x, 0x00F000F0u, k); }
+
+// x = hi + lo with hi, lo f16 (hi rounded toward zero, lo the rounded remainder, which x - hi holds
+// exactly): 22 significant bits of each of two floats, as two f16 pairs.
+__device__ __forceinline__ void split_pair(float x0, float x1, uint32_t& hi, uint32_t& lo) {
+  const auto h = __builtin_amdgcn_cvt_pkrtz(x0, x1);
+  hi = __builtin_bit_cast(uint32_t, h);
+  lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x0 - (float)h[0], x1 - (float)h[1]));
+}
+
+// Bytes 0, 1 (HI false) or 2, 3 of x, each 0 .. 15, as the f16 pair (b0, b1): FP8 e4m3 times 2^9.
+template <bool HI>
+__device__ __forceinline__ uint32_t codes_f16(uint32_t x) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x, 512.0f, HI));
 }
 
 // 4 x 4 byte transpose: w[i] byte j -> o[j] byte i.
@@ -218,12 +260,13 @@ __device__ __forceinline__ void issue_v(const KiviParams& p, const Head& hd, con
 
 // The compact fold: lane l covers row fr = l / LPR, channels fc .. fc + CPL - 1 (fc = (l % LPR) * CPL).
 // x = q * key scale (1 for the unquantized formats); the row's largest |x| picks the power of two f; the
-// f-scaled x goes to LDS as high part + remainder at its contraction position, 1024 + key zero goes to
-// s_kz (row 0's lanes), qscale / f to s_inv.
+// f-scaled x goes to LDS as high part + remainder at its contraction position, qscale / f to s_inv; for
+// 8-bit codes 1024 + key zero goes to s_kz (row 0's lanes), for 4-bit codes the row's sum of key zero x
+// f-scaled x to s_zc (the scores start from minus it).
 template <int FMT, int RP, int CPL>
 __device__ __forceinline__ void fold(const float (&qf)[CPL], const uint32_t (&gs)[CPL / 2], const uint32_t (&gz)[CPL / 2],
                                      float qscale, int lane, uint16_t (*s_qh)[kHeadDim], uint16_t (*s_ql)[kHeadDim],
-                                     uint16_t* s_kz, float* s_inv) {
+                                     uint16_t* s_kz, float* s_inv, float* s_zc) {
   typedef KF<FMT> F;
   typedef typename F::E E;
   constexpr int LPR = 64 / RP;
@@ -253,21 +296,44 @@ __device__ __forceinline__ void fold(const float (&qf)[CPL], const uint32_t (&gs
   if (mx > 0.0f) (void)frexpf(mx, &e);
   e = e < -100 ? -100 : e;
   const float f = ldexpf(1.0f, 14 - e);
+  float zc = 0.0f;  // 4-bit codes: this lane's share of the row's sum of key zero x f-scaled x
+  if constexpr (FMT == kKivi4) {
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const uint32_t w = gz[c >> 1];
+      zc += (float)__builtin_bit_cast(_Float16, (uint16_t)((c & 1) ? (w >> 16) : (w & 0xffffu))) * (x[c] * f);
+    }
+    zc += dpp_mov<kDppXor1>(zc);
+    zc += dpp_mov<kDppXor2>(zc);
+    if constexpr (LPR >= 8) zc += dpp_mov<kDppHalfMirror>(zc);
+    if constexpr (LPR >= 16) zc += dpp_mov<kDppRowMirror>(zc);
+    if constexpr (LPR >= 32) zc = sum_xor<16>(zc);
+  }
 #pragma unroll
   for (int c0 = 0; c0 < CPL; c0 += 4) {
-    uint16_t hb[4], lb[4];
+    uint32_t hw[2], lw[2];
+    if constexpr (std::is_same<E, _Float16>::value) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const float y = x[c0 + c] * f;
-      const E hi = (E)y;
-      const E lo = (E)(y - (float)hi);
-      hb[c] = __builtin_bit_cast(uint16_t, hi);
-      lb[c] = __builtin_bit_cast(uint16_t, lo);
+      for (int c = 0; c < 4; c += 2) split_pair(x[c0 + c] * f, x[c0 + c + 1] * f, hw[c >> 1], lw[c >> 1]);
+    } else {
+      uint16_t hb[4], lb[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float y = x[c0 + c] * f;
+        const E hi = (E)y;
+        const E lo = (E)(y - (float)hi);
+        hb[c] = __builtin_bit_cast(uint16_t, hi);
+        lb[c] = __builtin_bit_cast(uint16_t, lo);
+      }
+      hw[0] = hb[0] | ((uint32_t)hb[1] << 16);
+      hw[1] = hb[2] | ((uint32_t)hb[3] << 16);
+      lw[0] = lb[0] | ((uint32_t)lb[1] << 16);
+      lw[1] = lb[2] | ((uint32_t)lb[3] << 16);
     }
     const int pos = kpos<FMT>(fc + c0);  // four consecutive channels stay consecutive
-    *(u32x2*)&s_qh[fr][pos] = u32x2{hb[0] | ((uint32_t)hb[1] << 16), hb[2] | ((uint32_t)hb[3] << 16)};
-    *(u32x2*)&s_ql[fr][pos] = u32x2{lb[0] | ((uint32_t)lb[1] << 16), lb[2] | ((uint32_t)lb[3] << 16)};
-    if constexpr (F::kQuant) {
+    *(u32x2*)&s_qh[fr][pos] = u32x2{hw[0], hw[1]};
+    *(u32x2*)&s_ql[fr][pos] = u32x2{lw[0], lw[1]};
+    if constexpr (FMT == kKivi8) {
       if (fr == 0) {
         typedef _Float16 h2 __attribute__((ext_vector_type(2)));
         const h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
@@ -277,16 +343,19 @@ __device__ __forceinline__ void fold(const float (&qf)[CPL], const uint32_t (&gs
       }
     }
   }
-  if ((lane % LPR) == 0) s_inv[fr] = qscale / f;
+  if ((lane % LPR) == 0) {
+    s_inv[fr] = ldexpf(qscale, e - 14);  // qscale / f
+    if constexpr (FMT == kKivi4) s_zc[fr] = zc;
+  }
 }
 
-// Row n's score operands for the four K-steps, its score factor (0 past the G rows) and, for codes,
-// 1024 + key zero in this lane's contraction order.
+// Row n's score operands for the four K-steps, its score factor (0 past the G rows) and, for 8-bit codes,
+// 1024 + key zero in this lane's contraction order, for 4-bit codes the row's zero term zc.
 template <int FMT, int RP>
 __device__ __forceinline__ void read_fold(int n, int kq, int G, const uint16_t (*s_qh)[kHeadDim],
                                           const uint16_t (*s_ql)[kHeadDim], const uint16_t* s_kz, const float* s_inv,
-                                          typename KF<FMT>::T (&qh)[4], typename KF<FMT>::T (&ql)[4],
-                                          uint32_t (&kzp)[4][4], float& inv) {
+                                          const float* s_zc, typename KF<FMT>::T (&qh)[4], typename KF<FMT>::T (&ql)[4],
+                                          uint32_t (&kzp)[4][4], float& inv, float& zc) {
   typedef typename KF<FMT>::T T;
   const bool in = n < G;
   const int r = in ? n : 0;  // padded rows compute row 0's scores, scaled by 0 and never stored
@@ -294,7 +363,7 @@ __device__ __forceinline__ void read_fold(int n, int kq, int G, const uint16_t (
   for (int s = 0; s < 4; ++s) {
     qh[s] = *(const T*)&s_qh[r][32 * kq + 8 * s];
     ql[s] = *(const T*)&s_ql[r][32 * kq + 8 * s];
-    if constexpr (KF<FMT>::kQuant) {
+    if constexpr (FMT == kKivi8) {
       const u32x4 z = *(const u32x4*)&s_kz[32 * kq + 8 * s];
       kzp[s][0] = z.x;
       kzp[s][1] = z.y;
@@ -303,6 +372,7 @@ __device__ __forceinline__ void read_fold(int n, int kq, int G, const uint16_t (
     }
   }
   inv = in ? s_inv[r] : 0.0f;
+  zc = FMT == kKivi4 ? s_zc[r] : 0.0f;
 }
 
 // Score operand A of K-step s, tile t: code - zero (quantized) or the stored halves.
@@ -315,20 +385,29 @@ __device__ __forceinline__ typename KF<FMT>::T k_operand(const KChunk<FMT, CPL>&
     const uint32_t w1 = (s & 1) ? q.w : q.y;
     return bytes8_minus(w0, w1, kz);
   } else if constexpr (FMT == kKivi4) {
+    // The codes themselves (the zero points go into the scores' starting value): a byte holding 0 .. 15,
+    // read as FP8 e4m3, is code x 2^-9 exactly (the subnormals and the first binade step by 2^-9), and the
+    // FP8 -> f16 conversion scaled by 2^9 gives the code.
     const U4 q = c.k[t][0];
     const uint32_t w = s == 0 ? q.x : (s == 1 ? q.y : (s == 2 ? q.z : q.w));
-    return bytes8_minus(w & 0x0F0F0F0Fu, (w >> 4) & 0x0F0F0F0Fu, kz);
+    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+    const u32x4 r = {codes_f16<false>(lo), codes_f16<true>(lo), codes_f16<false>(hi), codes_f16<true>(hi)};
+    return __builtin_bit_cast(T, r);
   } else {
     return __builtin_bit_cast(T, c.k[t][s]);
   }
 }
 
 // Fold chunk kk into this lane's state: m (row n's reference point, shared by its four lanes), l (this
-// lane's partial weight sum), o[mu] (row n, channels out_channel(kq, i, mu)).
+// lane's partial weight sum), o[mu] (row n, channels out_channel(kq, i, mu)) and, for codes, oz: the value
+// products take 1024 + code (4-bit high nibbles: 1024 + 16 code), and oz gathers what that adds, the sum
+// over tokens of weight x (1024 + value zero) (1024 + 16 zero in rows 8 .. 15 of its tile), which
+// value_zero_out takes out. The weights are positive, so the offset costs no precision that matters: the
+// products stay within 2^11 of their sum without it.
 template <int FMT, int CPL, typename AfterScores>
 __device__ __forceinline__ void compute(KChunk<FMT, CPL>& c, int kk, int len, int lane, const typename KF<FMT>::T (&qh)[4],
-                                        const typename KF<FMT>::T (&ql)[4], const uint32_t (&kzp)[4][4], float inv, float& m,
-                                        float& l, f32x4 (&o)[8], AfterScores after_scores) {
+                                        const typename KF<FMT>::T (&ql)[4], const uint32_t (&kzp)[4][4], float inv, float zc,
+                                        float& m, float& l, f32x4 (&o)[8], f32x4& oz, AfterScores after_scores) {
   typedef KF<FMT> F;
   typedef typename F::T T;
   typedef typename F::E E;
@@ -337,7 +416,7 @@ __device__ __forceinline__ void compute(KChunk<FMT, CPL>& c, int kk, int len, in
   float sc[8];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    f32x4 st = {0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 st = {-zc, -zc, -zc, -zc};  // 0 but for 4-bit codes
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const T a = k_operand<FMT, CPL>(c, t, s, kzp[s]);
@@ -372,7 +451,7 @@ __device__ __forceinline__ void compute(KChunk<FMT, CPL>& c, int kk, int len, in
   }
   float vsf[8];
   float ev = 0.0f;  // this lane's tokens have value scales below 2^ev
-  uint32_t vzp[4];  // 1024 + value zero of the lane's eight tokens, as f16 pairs
+  uint32_t vzp[4];  // 1024 + value zero of the lane's eight tokens (x 16 first in 4-bit rows 8 .. 15), f16 pairs
   if constexpr (F::kQuant) {
     typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
     const u16x2 m01 = __builtin_elementwise_max(__builtin_bit_cast(u16x2, sw[0]), __builtin_bit_cast(u16x2, sw[1]));
@@ -386,8 +465,15 @@ __device__ __forceinline__ void compute(KChunk<FMT, CPL>& c, int kk, int len, in
       const uint32_t bits = (j & 1) ? (sw[j >> 1] >> 16) : (sw[j >> 1] & 0xffffu);
       vsf[j] = (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
     }
+    if constexpr (FMT == kKivi4) {
+      const _Float16 z16 = (lane & 15) < 8 ? (_Float16)1.0f : (_Float16)16.0f;
+      const h2 zs = {z16, z16};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) vzp[j] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, zw[j]) + k1024);
+      for (int j = 0; j < 4; ++j) vzp[j] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, zw[j]) * zs + k1024);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) vzp[j] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, zw[j]) + k1024);
+    }
   } else {
 #pragma unroll
     for (int j = 0; j < 8; ++j) vsf[j] = 1.0f;
@@ -407,18 +493,35 @@ __device__ __forceinline__ void compute(KChunk<FMT, CPL>& c, int kk, int len, in
     l *= alpha;
 #pragma unroll
     for (int mu = 0; mu < 8; ++mu) o[mu] *= alpha;
+    if constexpr (F::template kZeroFold<CPL>) oz *= alpha;
     m = mn;
   }
   const float base = (m == kNegInf ? 0.0f : m) - kBias;
   T ph, pl;
+  if constexpr (std::is_same<E, _Float16>::value) {
+    u32x4 hw, lw;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const float e = fast_exp2(sc[j] - base);
-    l += e;
-    const float w = e * vsf[j];
-    const E hi = (E)w;
-    ph[j] = hi;
-    pl[j] = (E)(w - (float)hi);
+    for (int j = 0; j < 8; j += 2) {
+      const float e0 = fast_exp2(sc[j] - base), e1 = fast_exp2(sc[j + 1] - base);
+      l += e0;
+      l += e1;
+      uint32_t hi, lo;
+      split_pair(e0 * vsf[j], e1 * vsf[j + 1], hi, lo);
+      hw[j >> 1] = hi;
+      lw[j >> 1] = lo;
+    }
+    ph = __builtin_bit_cast(T, hw);
+    pl = __builtin_bit_cast(T, lw);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float e = fast_exp2(sc[j] - base);
+      l += e;
+      const float w = e * vsf[j];
+      const E hi = (E)w;
+      ph[j] = hi;
+      pl[j] = (E)(w - (float)hi);
+    }
   }
 
   // ---- O^T += V^T W^T: eight M-tiles -------------------------------------------------------------------
@@ -429,26 +532,44 @@ __device__ __forceinline__ void compute(KChunk<FMT, CPL>& c, int kk, int len, in
       transpose4(c.v[t][0][0], c.v[t][1][0], c.v[t][2][0], c.v[t][3][0], lo[t]);
       transpose4(c.v[t][0][1], c.v[t][1][1], c.v[t][2][1], c.v[t][3][1], hi[t]);
     }
+    constexpr bool ZF = F::template kZeroFold<CPL>;
 #pragma unroll
     for (int mu = 0; mu < 8; ++mu) {
       const uint32_t d0 = mu < 4 ? lo[0][mu & 3] : hi[0][mu & 3];
       const uint32_t d1 = mu < 4 ? lo[1][mu & 3] : hi[1][mu & 3];
-      const f16x8 a = bytes8_minus(d0, d1, vzp);
+      const f16x8 a = ZF ? bytes8(d0, d1) : bytes8_minus(d0, d1, vzp);
       o[mu] = mfma(a, ph, o[mu]);
       o[mu] = mfma(a, pl, o[mu]);
+    }
+    if constexpr (ZF) {
+      const f16x8 az = __builtin_bit_cast(f16x8, u32x4{vzp[0], vzp[1], vzp[2], vzp[3]});
+      oz = mfma(az, ph, oz);
+      oz = mfma(az, pl, oz);
     }
   } else if constexpr (FMT == kKivi4) {
-    uint32_t tr[2][4];  // [tile][j]: byte 4 n' + j of the tile's four tokens (channels 4 n' + j, 64 + 4 n' + j)
+    // Byte j of the lane's token words holds channels 4 n' + j (low nibble) and 64 + 4 n' + j (high):
+    // M-tiles j and 4 + j take it, for tokens (0, 1) and (2, 3) of each tile.
+    const uint32_t k1024 = 0x64006400u;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) transpose4(c.v[t][0][0], c.v[t][1][0], c.v[t][2][0], c.v[t][3][0], tr[t]);
+    for (int j = 0; j < 4; ++j) {
+      uint32_t pr[2][2];
 #pragma unroll
-    for (int mu = 0; mu < 8; ++mu) {
-      const uint32_t d0 = mu < 4 ? tr[0][mu] & 0x0F0F0F0Fu : (tr[0][mu & 3] >> 4) & 0x0F0F0F0Fu;
-      const uint32_t d1 = mu < 4 ? tr[1][mu] & 0x0F0F0F0Fu : (tr[1][mu & 3] >> 4) & 0x0F0F0F0Fu;
-      const f16x8 a = bytes8_minus(d0, d1, vzp);
-      o[mu] = mfma(a, ph, o[mu]);
-      o[mu] = mfma(a, pl, o[mu]);
+      for (int t = 0; t < 2; ++t) {
+        pr[t][0] = byte_pair(c.v[t][0][0], c.v[t][1][0], j);
+        pr[t][1] = byte_pair(c.v[t][2][0], c.v[t][3][0], j);
+      }
+      const f16x8 al = __builtin_bit_cast(
+          f16x8, u32x4{nib_lo(pr[0][0], k1024), nib_lo(pr[0][1], k1024), nib_lo(pr[1][0], k1024), nib_lo(pr[1][1], k1024)});
+      const f16x8 ah = __builtin_bit_cast(
+          f16x8, u32x4{nib_hi(pr[0][0], k1024), nib_hi(pr[0][1], k1024), nib_hi(pr[1][0], k1024), nib_hi(pr[1][1], k1024)});
+      o[j] = mfma(al, ph, o[j]);
+      o[j] = mfma(al, pl, o[j]);
+      o[4 + j] = mfma(ah, ph, o[4 + j]);
+      o[4 + j] = mfma(ah, pl, o[4 + j]);
     }
+    const f16x8 az = __builtin_bit_cast(f16x8, u32x4{vzp[0], vzp[1], vzp[2], vzp[3]});
+    oz = mfma(az, ph, oz);
+    oz = mfma(az, pl, oz);
   } else {
     // Halves: token pair (i, i + 1) of tile t at channel 8 n' + mu, as one dword.
 #pragma unroll
@@ -463,6 +584,25 @@ __device__ __forceinline__ void compute(KChunk<FMT, CPL>& c, int kk, int len, in
       o[mu] = mfma(a, ph, o[mu]);
       o[mu] = mfma(a, pl, o[mu]);
     }
+  }
+}
+
+// Takes out of o what the offset value codes added (oz: row n's sum of weight x (1024 + zero), the same in
+// every row of the lane's tile; for 4-bit codes rows 0 .. 7 hold the low channels' sum and rows 8 .. 15 the
+// high channels' (1024 + 16 zero), whose products also carry a factor 16).
+template <int FMT>
+__device__ __forceinline__ void value_zero_out(int kq, const f32x4& oz, f32x4 (&o)[8]) {
+  if constexpr (FMT == kKivi4) {
+    const float own = oz[0];
+    const float other = __shfl_xor(own, 32, 64);  // lanes kq and kq ^ 2: one holds each half
+    const float zl = kq < 2 ? own : other, zh = kq < 2 ? other : own;
+#pragma unroll
+    for (int mu = 0; mu < 4; ++mu) o[mu] -= zl;
+#pragma unroll
+    for (int mu = 4; mu < 8; ++mu) o[mu] = (o[mu] - zh) * 0.0625f;
+  } else {
+#pragma unroll
+    for (int mu = 0; mu < 8; ++mu) o[mu] -= oz[0];
   }
 }
 
@@ -638,6 +778,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void kivi_decode_kernel(const
   __shared__ __align__(16) uint16_t s_ql[NW][RP][D];  // and remainders
   __shared__ __align__(16) uint16_t s_kz[NW][D];      // 1024 + key zero (f16), contraction order
   __shared__ float s_inv[NW][RP];
+  __shared__ float s_zc[NW][RP];                      // 4-bit codes: each row's key zero term
   __shared__ float s_m[NW][RP];
   __shared__ float s_l[NW][RP];
   __shared__ float s_o[NW][RP][D];
@@ -735,19 +876,19 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void kivi_decode_kernel(const
     const int split_end = min((j_cur + 1) * p.cps, nb);
 
     float m = kNegInf, l = 0.0f;
-    f32x4 o[8];
+    f32x4 o[8], oz = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int mu = 0; mu < 8; ++mu) o[mu] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     T qh[4], ql[4];
     uint32_t kzp[4][4];
-    float inv = 0.0f;
+    float inv = 0.0f, zc = 0.0f;
     if constexpr (!F::kQuant) {  // unquantized: one fold serves the whole piece
       const uint32_t unit[CPL / 2] = {};
-      fold<FMT, RP, CPL>(qf, unit, unit, p.qscale, lane, s_qh[wave], s_ql[wave], s_kz[wave], s_inv[wave]);
+      fold<FMT, RP, CPL>(qf, unit, unit, p.qscale, lane, s_qh[wave], s_ql[wave], s_kz[wave], s_inv[wave], s_zc[wave]);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      read_fold<FMT, RP>(n, kq, G, s_qh[wave], s_ql[wave], s_kz[wave], s_inv[wave], qh, ql, kzp, inv);
+      read_fold<FMT, RP>(n, kq, G, s_qh[wave], s_ql[wave], s_kz[wave], s_inv[wave], s_zc[wave], qh, ql, kzp, inv, zc);
     }
 
     if constexpr (DEPTH == 1) {
@@ -756,13 +897,13 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void kivi_decode_kernel(const
       for (int kk = k + wave; kk < k_end;) {
         const int kn = kk + NW;
         if constexpr (F::kQuant) {
-          fold<FMT, RP, CPL>(qf, cr.gs, cr.gz, p.qscale, lane, s_qh[wave], s_ql[wave], s_kz[wave], s_inv[wave]);
+          fold<FMT, RP, CPL>(qf, cr.gs, cr.gz, p.qscale, lane, s_qh[wave], s_ql[wave], s_kz[wave], s_inv[wave], s_zc[wave]);
           __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
           __builtin_amdgcn_wave_barrier();
           __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-          read_fold<FMT, RP>(n, kq, G, s_qh[wave], s_ql[wave], s_kz[wave], s_inv[wave], qh, ql, kzp, inv);
+          read_fold<FMT, RP>(n, kq, G, s_qh[wave], s_ql[wave], s_kz[wave], s_inv[wave], s_zc[wave], qh, ql, kzp, inv, zc);
         }
-        compute<FMT, CPL>(cr, kk, len, lane, qh, ql, kzp, inv, m, l, o, [&]() {
+        compute<FMT, CPL>(cr, kk, len, lane, qh, ql, kzp, inv, zc, m, l, o, oz, [&]() {
           if (kn < k_end) issue_k<FMT, CPL>(p, hd, lo, kn, cr);
         });
         if (kn < k_end) issue_v<FMT, CPL>(p, hd, lo, kn, cr);
@@ -777,12 +918,12 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void kivi_decode_kernel(const
       auto step = [&](KChunk<FMT, CPL>& cur, int kk) __attribute__((always_inline)) {
         const int kn = kk + 2 * NW;
         const int kl = kn < k_end ? kn : kk;
-        fold<FMT, RP, CPL>(qf, cur.gs, cur.gz, p.qscale, lane, s_qh[wave], s_ql[wave], s_kz[wave], s_inv[wave]);
+        fold<FMT, RP, CPL>(qf, cur.gs, cur.gz, p.qscale, lane, s_qh[wave], s_ql[wave], s_kz[wave], s_inv[wave], s_zc[wave]);
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        read_fold<FMT, RP>(n, kq, G, s_qh[wave], s_ql[wave], s_kz[wave], s_inv[wave], qh, ql, kzp, inv);
-        compute<FMT, CPL>(cur, kk, len, lane, qh, ql, kzp, inv, m, l, o, [&]() { issue_k<FMT, CPL>(p, hd, lo, kl, cur); });
+        read_fold<FMT, RP>(n, kq, G, s_qh[wave], s_ql[wave], s_kz[wave], s_inv[wave], s_zc[wave], qh, ql, kzp, inv, zc);
+        compute<FMT, CPL>(cur, kk, len, lane, qh, ql, kzp, inv, zc, m, l, o, oz, [&]() { issue_k<FMT, CPL>(p, hd, lo, kl, cur); });
         issue_v<FMT, CPL>(p, hd, lo, kl, cur);
         __builtin_amdgcn_wave_barrier();  // the LDS fold buffers are rewritten next
       };
@@ -827,7 +968,9 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void kivi_decode_kernel(const
       }
     }
 
-    // This wave's state of row n: the four lanes' weight sums added, stored for the workgroup merge.
+    // This wave's state of row n: the value zero points taken out, the four lanes' weight sums added,
+    // stored for the workgroup merge.
+    if constexpr (F::template kZeroFold<CPL>) value_zero_out<FMT>(kq, oz, o);
     l = sum_xor<32>(sum_xor<16>(l));
     if (n < RP) {
       if (kq == 0) {
