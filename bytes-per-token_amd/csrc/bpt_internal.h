@@ -81,6 +81,12 @@ constexpr int64_t decode_min_chunks(bool mfma, int rows, bool int8, int64_t chun
                                                                                              : kDecodeMinChunksMfma))
               : (int8 ? kDecodeMinChunksInt8 : 1);
 }
+// KIVI calls with a few very long (sequence, KV head) segments launch one workgroup per CU: every segment
+// is then split over half as many workgroups, and the last one to finish combines half as many partials.
+// Measured (4-bit / 8-bit / bf16): 1 x 32768 tokens, 8 KV heads 26.0 -> 24.1, 28.3 -> 27.6, 41.7 -> 39.8 us;
+// with 32 segments (4 x 32768) or short ones (1 x 2048) the halved grid cost up to 10 us instead.
+constexpr int kKiviFewSegments = 8;
+constexpr int kKiviLongSegmentChunks = 512;
 // The KIVI kernel's fewest chunks per workgroup: one per wave while the call's chunks number no more than the
 // largest grid, two per wave beyond. Measured on INT8 caches: 1 x 2048 tokens 21.0 -> 14.0 us and 4 x 512
 // 16.1 -> 13.2 (4 instead of 1); 1 x 8192 22.8 -> 18.5, 4 x 2048 18.2 -> 16.0 and 16 x 512 16.3 -> 15.5 (8

@@ -254,7 +254,10 @@ int make_kivi_plan(const bpt_kivi_args* a, KiviPlan* pl) {
     std::lock_guard<std::mutex> lock(g_tuning_mutex);
     tune = g_tuning;
   }
-  int64_t grid = (int64_t)bpt::kComputeUnits * (tune.groups_per_cu > 0 ? tune.groups_per_cu : bpt::kDecodeGroupsPerCu);
+  const int64_t seq_heads = (int64_t)a->batch * a->num_kv_heads;
+  const bool few_long = seq_heads <= bpt::kKiviFewSegments && max_nb >= bpt::kKiviLongSegmentChunks;
+  const int default_gpc = few_long ? 1 : bpt::kDecodeGroupsPerCu;
+  int64_t grid = (int64_t)bpt::kComputeUnits * (tune.groups_per_cu > 0 ? tune.groups_per_cu : default_gpc);
   const int64_t bound_c = seq_chunks * a->num_kv_heads;
   const int64_t min_chunks = tune.min_chunks > 0 ? tune.min_chunks : bpt::kivi_min_chunks(bound_c, grid);
   const int64_t by_chunks = (bound_c + min_chunks - 1) / min_chunks;

@@ -781,7 +781,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void kivi_decode_kernel(const
   __shared__ float s_zc[NW][RP];                      // 4-bit codes: each row's key zero term
   __shared__ float s_m[NW][RP];
   __shared__ float s_l[NW][RP];
-  __shared__ float s_o[NW][RP][D];
+  __shared__ float s_o[NW][RP][D + 1];  // rows padded by one word: a merge store's rows land on distinct banks
   __shared__ float s_tm[RP], s_tl[RP];  // the tail's state (tail_state); its scratch and sums reuse the fold buffers
   static_assert(sizeof(s_qh) >= RP * kKiviMaxTail * sizeof(float) && sizeof(s_ql) >= RP * D * sizeof(float),
                 "the fold buffers hold the tail's scratch");

@@ -503,7 +503,9 @@ __global__ __launch_bounds__(NW * 64, kMfmaWavesPerSimd) void decode_mfma_kernel
   __shared__ int s_last;
   __shared__ float s_m[NW][RG];
   __shared__ float s_l[NW][RG];
-  __shared__ __attribute__((aligned(16))) float s_o[NW][RG][D];
+  // Rows padded by 16 bytes: the merge stores put lane (n, kq) at row n, byte 128 kq (+ 32 i), so unpadded
+  // 512-byte rows would send the 16 rows of one store to the same banks (many-row segments store them all).
+  __shared__ __attribute__((aligned(16))) float s_o[NW][RG][D + 4];
   __shared__ U4 s_k[NW][2][16][8];  // each wave's K rows of one chunk, on their way to the operand layout
   __shared__ float s_sc[NW][64];    // each wave's per-token scales of one chunk
 
