@@ -156,8 +156,11 @@ def test_larger_key_groups():
     check(q, qn, dev, ref, [256, 200], split=128)
 
 
-def test_max_context():
-    dev, ref = make_cache(1, 8, 32768, 4, seed=9)
+@pytest.mark.parametrize("bits", [4, 8, 16])
+def test_max_context(bits):
+    """One sequence of 32768 tokens: 8 segments of 1024 chunks, the plan's one-workgroup-per-CU case, each
+    segment split over 32 workgroups and combined by the last; and 32001 tokens over a caller's split."""
+    dev, ref = make_cache(1, 8, 32768, bits, seed=9)
     q, qn = make_q(1, 16, 9)
     check(q, qn, dev, ref, [32768])
     check(q, qn, dev, ref, [32001], split=2048)
