@@ -680,7 +680,7 @@ def main() -> int:
     if args.gpus != 1 or world != 1:
         print(
             "bench.py measures one GPU: the decode path is sharded by sequence or KV head with no exchange, "
-            "and multi-GPU runs are not part of this build (run with --gpus 1)",
+            "so each GPU runs this same single-GPU call on its own share; this benchmark takes --gpus 1",
             file=sys.stderr,
         )
         return 2
