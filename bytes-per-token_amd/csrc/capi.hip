@@ -168,8 +168,11 @@ int make_plan(const bpt_decode_args* a, Plan* pl) {
     }
     pl->grid = (int)(grid < 1 ? 1 : grid);
   }
+  // One sequence: its segments (one per KV head) are equally long, so the line's equal ranges need no charge
+  // for the merges (measured on the matrix-core kernel at 512 / 2943 tokens: 11.1 -> 9.5, 12.9 -> 12.0 us).
   pl->piece_cost = pl->per_forced > 0 ? 0
                    : tune.piece_cost >= 0 ? tune.piece_cost
+                   : a->batch == 1 ? 0
                    : (pl->mfma && pl->rows >= bpt::kManyRows ? bpt::kManyRowPieceCost : bpt::kDecodePieceCost);
   const size_t slots = (size_t)a->batch * pl->HR + pl->grid;
   pl->ws_out_floats = slots * pl->rows_per_group * a->head_dim;
