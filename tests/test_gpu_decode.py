@@ -142,6 +142,16 @@ def test_forced_split_counts(num_splits, fmt, scales):
     check(got, want, f"{fmt} num_splits={num_splits}")
 
 
+@pytest.mark.parametrize("nq", [1, 5])
+@pytest.mark.parametrize("length", [5, 31, 33, 512, 2943, 9000])
+def test_one_sequence_matrix_core(length, nq):
+    # One sequence on the matrix-core kernel (2-row and 10-row segments): the plan charges its equally long
+    # segments nothing, so the line's ranges fall anywhere inside them, across KV heads and chunk edges.
+    c = make_case("fp8", [length], nq=nq, seed=length)
+    got, want = run_case(c)
+    check(got, want, f"one sequence of {length}, Q={nq}")
+
+
 @pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 8), (32, 8), (64, 8), (12, 4), (40, 8)])
 def test_gqa_groups(hq, hkv):
     c = make_case("fp8", [300, 77, 1024], hq=hq, hkv=hkv)
