@@ -111,8 +111,8 @@ constexpr int64_t kAlignedMaxChunksBf16 = 32768;
 constexpr int64_t kAlignedMaxChunksInt8 = 16384;
 constexpr int64_t kAlignedMaxGrid = 512;
 
-// Waves per matrix-core workgroup for segments of `rows` rows, and workgroups per CU.
-constexpr int mfma_waves(int rows) { return rows >= kManyRows ? kMfmaManyRowWaves : kDecodeWaves; }
+// Matrix-core workgroups per CU for segments of `rows` rows (8-wave workgroups from kManyRows rows on, else
+// 4-wave ones; the plan picks 2-wave ones over many segments, kMfmaPairGroupsPerCu to a CU).
 constexpr int mfma_groups_per_cu(int rows) { return rows >= kManyRows ? 1 : kDecodeGroupsPerCu; }
 // Stream-K line units charged for each segment start, in chunks: the cost of merging one more piece (the
 // wave merge, the partial's round trip and, for one workgroup, the combine), so that a workgroup whose
@@ -121,6 +121,16 @@ constexpr int kDecodePieceCost = BPT_DECODE_PIECE_COST;
 // The same for matrix-core segments of kManyRows rows or more (8-wave workgroups; dearer merges).
 constexpr int kManyRowPieceCost = BPT_DECODE_MANY_ROW_PIECE_COST;
 constexpr int kMaxPieceCost = kDecodePieceCost > kManyRowPieceCost ? kDecodePieceCost : kManyRowPieceCost;
+// Few-row matrix-core calls over many segments (at least kMfmaPairMinSegments (sequence, KV head) pairs, an
+// automatic split) run in workgroups of kMfmaPairWaves waves, kMfmaPairGroupsPerCu to a CU (the same waves
+// per SIMD), charged kMfmaPairPieceCost per segment: with two waves dealing a piece's chunks, a range's last
+// round leaves at most one wave idle. Measured against four-wave workgroups: 128 to 1024 segments of ragged
+// lengths 1-6 % faster, equal lengths within 1 %; 64 or fewer segments, or a fixed split count over long
+// sequences, 2-20 % slower (those keep four waves).
+constexpr int kMfmaPairWaves = 2;
+constexpr int kMfmaPairGroupsPerCu = 4;
+constexpr int kMfmaPairPieceCost = 4;
+constexpr int kMfmaPairMinSegments = 128;
 
 // 16-byte K loads (and V loads) per lane per chunk: fewer for 4-row groups, whose q and accumulators take
 // twice the registers.
@@ -156,6 +166,7 @@ struct DecodeParams {
   unsigned* counters;  // [B * HR] arrivals per segment; zero between calls
   int B, Q, Hq, Hkv, G, P, logP, num_blocks, max_blocks, len_cap;
   int n_rg, HR;      // row groups per KV head; segments per sequence (Hkv * n_rg)
+  int waves;         // matrix-core kernel: waves per workgroup (kMfmaPairWaves, kDecodeWaves or kMfmaManyRowWaves)
   int grid;          // workgroups launched
   int64_t per_forced;  // chunks per workgroup when the caller fixed the split count, else 0
   int piece_cost;      // line units charged per segment start (0 with a fixed split count)

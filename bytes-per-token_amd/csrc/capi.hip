@@ -49,6 +49,7 @@ struct Plan {
   int64_t per_forced;
   int equal_grid;  // workgroups that take equal partitions when all lengths are equal (0: none)
   int piece_cost;  // line units charged per segment start
+  int waves;       // matrix-core kernel: waves per workgroup
   size_t ws_out_floats, ws_lse_floats, workspace, counters;
 };
 
@@ -117,8 +118,14 @@ int make_plan(const bpt_decode_args* a, Plan* pl) {
   if (seq_cost > 0x7fffffffLL / (hr > 0 ? hr : 1))
     return fail(BPT_ERR_INVALID_ARGUMENT, "%s: batch x context x heads too large", fn);
   const int64_t bound_c = seq_chunks * hr;
+  pl->waves = !pl->mfma ? bpt::kDecodeWaves
+              : pl->rows >= bpt::kManyRows ? bpt::kMfmaManyRowWaves
+              : a->num_splits == 0 && (int64_t)a->batch * hr >= bpt::kMfmaPairMinSegments ? bpt::kMfmaPairWaves
+                                                                                      : bpt::kDecodeWaves;
+  const bool pair = pl->waves == bpt::kMfmaPairWaves;
   const int groups_per_cu =
       tune.groups_per_cu > 0 ? tune.groups_per_cu
+      : pair ? bpt::kMfmaPairGroupsPerCu
       : pl->mfma ? bpt::mfma_groups_per_cu(pl->rows)
                  : bpt::decode_groups_per_cu(a->kv_dtype == BPT_KV_INT8, pl->rows_per_group,
                                              a->page_size >= bpt::decode_rows_per_load(a->kv_dtype),
@@ -173,6 +180,7 @@ int make_plan(const bpt_decode_args* a, Plan* pl) {
   pl->piece_cost = pl->per_forced > 0 ? 0
                    : tune.piece_cost >= 0 ? tune.piece_cost
                    : a->batch == 1 ? 0
+                   : pair ? bpt::kMfmaPairPieceCost
                    : (pl->mfma && pl->rows >= bpt::kManyRows ? bpt::kManyRowPieceCost : bpt::kDecodePieceCost);
   const size_t slots = (size_t)a->batch * pl->HR + pl->grid;
   pl->ws_out_floats = slots * pl->rows_per_group * a->head_dim;
@@ -385,6 +393,7 @@ int decode_setup(const bpt_decode_args* a, const char* fn, const Buffers* own, b
   p.max_blocks = a->max_blocks_per_seq;
   p.n_rg = pl.n_rg;
   p.HR = pl.HR;
+  p.waves = pl.waves;
   line_fields(pl, &p);
   p.len_cap = pl.len_cap;
   p.qscale = a->sm_scale * bpt::kLog2e;
@@ -997,6 +1006,7 @@ int bpt_page_read_probe(const bpt_decode_args* a, float* partial_sums, int64_t* 
   p.len_offset = a->len_offset;
   p.HR = pl.HR;
   p.n_rg = pl.n_rg;
+  p.waves = pl.waves;
   p.grid = (int)g;
   bpt::LaunchEvents ev;
   ev.start = (hipEvent_t)start_event;

@@ -741,16 +741,21 @@ static hipError_t launch_mfma_nw(const DecodeParams& p, bool pu, bool qs, hipStr
 
 template <int KV, int SK>
 static hipError_t launch_mfma_sk(const DecodeParams& p, bool pu, bool qs, hipStream_t stream, const LaunchEvents& ev) {
-  const bool many = mfma_waves(p.Q * p.G) == kMfmaManyRowWaves;
+  // The plan's waves per workgroup: 8 for many-row segments, 2 for few-row calls over many segments, else 4.
+  const bool many = p.waves == kMfmaManyRowWaves, pair = p.waves == kMfmaPairWaves;
+  if (!many && !pair && p.waves != kDecodeWaves) return hipErrorInvalidValue;
+  if (many != (p.Q * p.G >= kManyRows)) return hipErrorInvalidValue;
   if constexpr (SK == kScaleHead) {
     if (p.fuse_q > 0) {
       if (many) return launch_mfma_nw<KV, SK, kMfmaManyRowWaves, true>(p, pu, qs, stream, ev);
+      if (pair) return launch_mfma_nw<KV, SK, kMfmaPairWaves, true>(p, pu, qs, stream, ev);
       return launch_mfma_nw<KV, SK, kDecodeWaves, true>(p, pu, qs, stream, ev);
     }
   } else {
     if (p.fuse_q > 0) return hipErrorInvalidValue;  // fused writes take per-head scales
   }
   if (many) return launch_mfma_nw<KV, SK, kMfmaManyRowWaves, false>(p, pu, qs, stream, ev);
+  if (pair) return launch_mfma_nw<KV, SK, kMfmaPairWaves, false>(p, pu, qs, stream, ev);
   return launch_mfma_nw<KV, SK, kDecodeWaves, false>(p, pu, qs, stream, ev);
 }
 

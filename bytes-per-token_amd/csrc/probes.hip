@@ -68,10 +68,11 @@ __global__ __launch_bounds__(kProbeThreads) void read_probe_kernel(const U4* buf
 
 // The decode's own work split, read only: segments (sequence, KV head, row group) of `chunk`-token chunks laid
 // end to end (build_segment_line), equal contiguous ranges for the launched workgroups (numbered XCD-major, as
-// the decode numbers them), the four waves of a workgroup taking a range's chunks round-robin; a chunk is its
-// tokens' K and V rows (row_bytes each, 16 bytes per lane) and, with per-token scales, their scales. Page ids
-// are read as the decode reads them (one scalar load per load instruction when a load's rows lie in one page),
-// and each wave keeps two chunks' loads in flight. No attention math, no partials, no merges.
+// the decode numbers them), the waves of a workgroup (the decode's two or four) taking a range's chunks
+// round-robin; a chunk is its tokens' K and V rows (row_bytes each, 16 bytes per lane) and, with per-token
+// scales, their scales. Page ids are read as the decode reads them (one scalar load per load instruction when
+// a load's rows lie in one page), and each wave keeps two chunks' loads in flight. No attention math, no
+// partials, no merges.
 constexpr int kWalkWaves = 4;
 
 struct WalkChunk {
@@ -151,17 +152,17 @@ __device__ __forceinline__ uint32_t walk_fold(const WalkChunk& w) {
   return x;
 }
 
-template <bool PU, int LOADS, bool SC>
-__global__ __launch_bounds__(kWalkWaves * 64) void page_read_probe_kernel(const DecodeParams p, int chunk,
+template <bool PU, int LOADS, bool SC, int NWALK>
+__global__ __launch_bounds__(NWALK * 64) void page_read_probe_kernel(const DecodeParams p, int chunk,
                                                                          int lanes_per_row, float* partial) {
   extern __shared__ int s_dyn[];  // [B + 1] chunks per sequence (exclusive prefix sum), then [B] lengths
   int* s_prefix = s_dyn;
   int* s_len = s_dyn + p.B + 1;
-  __shared__ int s_wsum[kWalkWaves];
+  __shared__ int s_wsum[NWALK];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // The decode's segment line: `chunk`-token chunks per sequence (its prefix sum over the batch).
   {
-    const int per_thread = (p.B + kWalkWaves * 64 - 1) / (kWalkWaves * 64);
+    const int per_thread = (p.B + NWALK * 64 - 1) / (NWALK * 64);
     const int lo = min(tid * per_thread, p.B), hi = min(lo + per_thread, p.B);
     int sum = 0;
     for (int b = lo; b < hi; ++b) {
@@ -186,7 +187,7 @@ __global__ __launch_bounds__(kWalkWaves * 64) void page_read_probe_kernel(const 
     }
     if (tid == 0) {
       int total = 0;
-      for (int w = 0; w < kWalkWaves; ++w) total += s_wsum[w];
+      for (int w = 0; w < NWALK; ++w) total += s_wsum[w];
       s_prefix[p.B] = total;
     }
     __syncthreads();
@@ -196,10 +197,10 @@ __global__ __launch_bounds__(kWalkWaves * 64) void page_read_probe_kernel(const 
   const int64_t c0 = line_index(gridDim.x) * per;
   const int64_t c1 = min(c0 + per, C);
   uint32_t a = 0;
-  // This wave's chunks: c0 + wave + kWalkWaves i, i < n. The steady state issues unconditionally, so that
+  // This wave's chunks: c0 + wave + NWALK i, i < n. The steady state issues unconditionally, so that
   // each fold waits for its own chunk only (a conditional issue leaves the compiler a drain of every load).
   const int64_t first = c0 + wave;
-  const int n = first < c1 ? (int)((c1 - first + kWalkWaves - 1) / kWalkWaves) : 0;
+  const int n = first < c1 ? (int)((c1 - first + NWALK - 1) / NWALK) : 0;
   if (n > 0) {
     int lo = 0, hi = p.B - 1;  // the cursor: largest b with HR * prefix[b] <= first
     while (lo < hi) {
@@ -207,7 +208,7 @@ __global__ __launch_bounds__(kWalkWaves * 64) void page_read_probe_kernel(const 
       if ((int64_t)p.HR * s_prefix[mid] <= first) lo = mid; else hi = mid - 1;
     }
     int b = sread(lo);
-    auto at = [&](int i) { return first + (int64_t)kWalkWaves * i; };
+    auto at = [&](int i) { return first + (int64_t)NWALK * i; };
     WalkChunk A, B;
     walk_issue<PU, LOADS, SC>(p, s_prefix, s_len, at(0), b, chunk, lanes_per_row, lane, A);
     int i = 0;
@@ -227,12 +228,12 @@ __global__ __launch_bounds__(kWalkWaves * 64) void page_read_probe_kernel(const 
   }
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) a += (uint32_t)__shfl_xor((int)a, m, 64);
-  __shared__ uint32_t s[kWalkWaves];
+  __shared__ uint32_t s[NWALK];
   if (lane == 0) s[wave] = a;
   __syncthreads();
   if (tid == 0) {
     uint32_t t = 0;
-    for (int w = 0; w < kWalkWaves; ++w) t += s[w];
+    for (int w = 0; w < NWALK; ++w) t += s[w];
     partial[blockIdx.x] = (float)t;
   }
 }
@@ -242,13 +243,24 @@ hipError_t launch_page_read_probe(const DecodeParams& p, int row_bytes, int chun
   if (p.grid <= 0) return hipSuccess;
   const size_t lds = (size_t)(2 * p.B + 1) * sizeof(int);
   const int lanes_per_row = row_bytes / 16, rows = 64 / lanes_per_row;
+  // The decode's waves per workgroup: two for the matrix-core kernel's two-wave workgroups, else four.
+  const bool pair = p.waves == kMfmaPairWaves;
   auto go = [&](auto pu, auto loads) {
-    if (with_scales)
-      launch_kernel(page_read_probe_kernel<decltype(pu)::value, decltype(loads)::value, true>, dim3((unsigned)p.grid),
-                    dim3(kWalkWaves * 64), lds, stream, ev, p, chunk, lanes_per_row, partial);
+    constexpr bool PU = decltype(pu)::value;
+    constexpr int L = decltype(loads)::value;
+    const dim3 grid((unsigned)p.grid), block((pair ? kMfmaPairWaves : kWalkWaves) * 64);
+    if (pair && with_scales)
+      launch_kernel(page_read_probe_kernel<PU, L, true, kMfmaPairWaves>, grid, block, lds, stream, ev, p, chunk,
+                    lanes_per_row, partial);
+    else if (pair)
+      launch_kernel(page_read_probe_kernel<PU, L, false, kMfmaPairWaves>, grid, block, lds, stream, ev, p, chunk,
+                    lanes_per_row, partial);
+    else if (with_scales)
+      launch_kernel(page_read_probe_kernel<PU, L, true, kWalkWaves>, grid, block, lds, stream, ev, p, chunk,
+                    lanes_per_row, partial);
     else
-      launch_kernel(page_read_probe_kernel<decltype(pu)::value, decltype(loads)::value, false>, dim3((unsigned)p.grid),
-                    dim3(kWalkWaves * 64), lds, stream, ev, p, chunk, lanes_per_row, partial);
+      launch_kernel(page_read_probe_kernel<PU, L, false, kWalkWaves>, grid, block, lds, stream, ev, p, chunk,
+                    lanes_per_row, partial);
   };
   auto by_loads = [&](auto pu) {
     switch (chunk / rows) {

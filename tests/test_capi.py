@@ -78,10 +78,20 @@ def test_plan_honours_requested_splits(built_lib):
     assert grid == 4 * 8 * 8 and ws == expected_workspace(4, 8, 16, grid)
 
 
-def test_plan_auto_launches_two_groups_per_cu_at_most(built_lib):
-    q, k, v, table, lens, ks, vs = cpu_case("fp8", b=32, max_blocks=256, nb=8192)
-    grid, chunk, ws, cnt = decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=4096)
-    assert chunk == 32 and grid == 512 and ws == expected_workspace(32, 8, 16, 512) and cnt == expected_counters(32, 8)
+def test_plan_auto_groups_per_cu(built_lib):
+    """Few-row matrix-core calls over at least 128 (sequence, KV head) segments run two-wave workgroups, four to
+    a CU (1024); fewer segments, or a fixed split count, four-wave ones, two to a CU (512)."""
+    def plan(b, num_splits=None):
+        q, k, v, table, lens, ks, vs = cpu_case("fp8", b=b, max_blocks=256, nb=8192)
+        return decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=4096, num_splits=num_splits)
+
+    grid, chunk, ws, cnt = plan(32)  # 256 segments
+    assert chunk == 32 and grid == 1024 and ws == expected_workspace(32, 8, 16, 1024) and cnt == expected_counters(32, 8)
+    assert plan(16)[0] == 1024  # 128 segments
+    grid, _, ws, _ = plan(8)  # 64 segments
+    assert grid == 512 and ws == expected_workspace(8, 8, 16, 512)
+    # A fixed split count keeps four-wave workgroups: 1024 partitions over 512 of them, two partitions each.
+    assert plan(32, num_splits=4)[0] == 512
     qb, kb, vb, tb, lb, _, _ = cpu_case("bf16", b=1)
     grid, chunk_bf16, _, _ = decode_plan(qb, kb, vb, tb, lb, None, None, scale=0.1, max_context=64)
     assert chunk_bf16 == 16  # vector kernel: 4 loads of 4 rows (16 lanes per bf16 row)
@@ -131,7 +141,7 @@ def test_plan_workspace_grows_with_the_launch(built_lib, max_context):
     q, k, v, table, lens, ks, vs = cpu_case(b=32, max_blocks=4096, nb=8192)
     grid, chunk, ws, cnt = decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=max_context)
     bound = 32 * 8 * -(-min(max_context, 4096 * 16) // chunk)
-    assert 1 <= grid <= max(min(512, bound), 1)
+    assert 1 <= grid <= max(min(1024, bound), 1)  # 256 segments: two-wave workgroups, four to a CU
     assert ws == expected_workspace(32, 8, 16, grid) and cnt == expected_counters(32, 8)
 
 
@@ -156,12 +166,12 @@ def test_plan_gives_many_row_segments_fuller_workgroups(built_lib):
     q, k, v, table, lens, ks, vs = cpu_case("fp8", b=2, nq=5, max_blocks=256, nb=8192)
     grid, chunk, ws, _ = decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=3072)
     assert chunk == 32 and grid == 2 * 8 * 96 // 8 and ws == expected_workspace(2, 8, 16, grid)
-    # ... a full batch fills every CU with one 8-wave workgroup, and 2 rows per KV head keep two 4-wave
-    # workgroups per CU and one chunk per wave (4 per workgroup) as the floor.
+    # ... a full batch fills every CU with one 8-wave workgroup, and 2 rows per KV head over 128 segments run
+    # four 2-wave workgroups per CU.
     q, k, v, table, lens, ks, vs = cpu_case("fp8", b=16, nq=5, max_blocks=256, nb=8192)
     assert decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=3072)[0] == 256
     q, k, v, table, lens, ks, vs = cpu_case("fp8", b=16, max_blocks=256, nb=8192)
-    assert decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=3072)[0] == 512
+    assert decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=3072)[0] == 1024
     q, k, v, table, lens, ks, vs = cpu_case("fp8", b=1, max_blocks=64, nb=64)
     assert decode_plan(q, k, v, table, lens, ks, vs, scale=0.1, max_context=1024)[0] == 8 * 32 // 4
     # Two chunks per wave (8 per workgroup) once that still launches a workgroup per two CUs: 2 x 8 heads x

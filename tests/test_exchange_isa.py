@@ -25,6 +25,7 @@ CSRC = ROOT / "bytes-per-token_amd" / "csrc"
 # (source, mangled-name prefix of one instantiation that splits segments across workgroups)
 KERNELS = [
     ("paged_decode_mfma.hip", "_ZN3bpt18decode_mfma_kernelILi1ELi1ELb1ELb0ELi4ELb0EEEvNS_12DecodeParamsE"),
+    ("paged_decode_mfma.hip", "_ZN3bpt18decode_mfma_kernelILi1ELi1ELb1ELb0ELi2ELb0EEEvNS_12DecodeParamsE"),
     ("paged_decode.hip", "_ZN3bpt13decode_kernel"),
     ("kivi_decode.hip", "_ZN3bpt18kivi_decode_kernelILi0ELi2ELb0EE"),
 ]
