@@ -67,6 +67,17 @@ def test_fused_store_matches_store_then_decode(fmt, nq, hq, hkv, page):
     both_ways(c, k, v, blocks, offsets, max_context=max(lengths) + 700)
 
 
+@pytest.mark.parametrize("fmt,nq", [("fp8", 1), ("fp8", 2), ("int8", 3)])
+def test_fused_store_over_many_segments(fmt, nq):
+    """24 sequences x 8 KV heads = 192 segments: the plan's 2-wave workgroups, four to a CU (the shape of the
+    decode step's launches), storing and using the rows as the 4-wave ones do."""
+    lengths = [max(t, nq) for t in (1, 2, 31, 32, 33, 64, 95, 300, 513, 700, 1024, 1500, 2000, 2047, 2048, 2049,
+                                    2900, 3000, 47, 129, 255, 256, 257, 4000)]
+    c = make_case(fmt, lengths, nq=nq, scales="head", seed=40 + nq)
+    k, v, blocks, offsets = new_rows(c, nq, seed=9)
+    both_ways(c, k, v, blocks, offsets, max_context=max(lengths))
+
+
 @pytest.mark.parametrize("num_splits", [1, 7, 64])
 def test_fused_store_with_fixed_split_counts(num_splits):
     """A caller's split count (the partitions that hold a sequence's last chunk change with it)."""
