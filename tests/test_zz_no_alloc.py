@@ -51,6 +51,21 @@ def test_noalloc_matches_the_workspace_entry_point_on_two_calls(fmt, scales, nq)
         check(got, w2, f"{fmt} Q={nq} splits={splits} against the oracle")
 
 
+def test_noalloc_matches_on_two_wave_workgroups():
+    # 24 sequences x 8 KV heads = 192 segments: the plan's 2-wave workgroups (1024 of them, so twice the
+    # partial slots), then a call of 2 sequences on 4-wave ones, sharing the array.
+    lengths = [4096, 1000, 33, 1, 2500, 0, 700, 3000, 2048, 64, 95, 300, 513, 1500, 2, 31, 32, 2049, 129, 4000,
+               256, 257, 47, 1024]
+    big = make_case("fp8", lengths, seed=13)
+    small = make_case("fp8", [300, 17], seed=14)
+    for c in (big, small, big):
+        got = noalloc(c)
+        want = reference(c)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"{len(c['lens'])} sequences: differs from bpt_paged_decode"
+    check(got, run_case(big)[1], "192 segments against the oracle")
+
+
 def test_noalloc_refuses_a_call_larger_than_its_array():
     # 4096 sequences x 8 KV heads on the matrix cores need 16-row partial slots: far over 30 MiB.
     lengths = [40] * 4096
