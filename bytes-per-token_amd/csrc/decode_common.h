@@ -317,10 +317,12 @@ __device__ __forceinline__ void combine_segment(const DecodeParams& p, int seg, 
   const int hh = hr / p.n_rg;
   const int rg = hr - hh * p.n_rg;
   const int live = min(RG, rows - rg * RG);  // this row group's real rows
-  // CPC channels of one row per thread, every piece's loads issued before they are combined: four when that
-  // still keeps the whole workgroup busy, fewer for few rows.
-  if (live * (D / 4) >= NT) combine_rows<RG, NT, 4>(p, seg, b, hh, rg, first, n, live, tid);
-  else if (live * (D / 2) >= NT) combine_rows<RG, NT, 2>(p, seg, b, hh, rg, first, n, live, tid);
+  // CPC channels of one row per thread, every piece's loads issued before they are combined: the fewest that
+  // still cover the rows in one pass of the workgroup (four at most). A second pass would issue its loads
+  // only after the first pass's have returned: one more memory round trip at the end of the segment (3 rows
+  // over 128 threads with two channels each took 1 us longer than with four).
+  if (live * D > 2 * NT) combine_rows<RG, NT, 4>(p, seg, b, hh, rg, first, n, live, tid);
+  else if (live * D > NT) combine_rows<RG, NT, 2>(p, seg, b, hh, rg, first, n, live, tid);
   else combine_rows<RG, NT, 1>(p, seg, b, hh, rg, first, n, live, tid);
   if (tid == 0) __hip_atomic_store(p.counters + seg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
