@@ -164,12 +164,16 @@ __device__ __forceinline__ int clamp_page_u(const DecodeParams& p, int e) { retu
 // loads, once per piece.
 __device__ __forceinline__ unsigned fused_in_place(const DecodeParams& p, int b, int first_new) {
   unsigned mask = 0u;
+  const int ws = p.w_i64 != 0 ? 1 : 0;
   for (int qi = 0; qi < p.fuse_q; ++qi) {
+    // Both words of both slot fields at once (an int32 slot's second load repeats its first).
     const int64_t si = (int64_t)b * p.w_sb + (int64_t)qi * p.w_sq;
-    const int64_t blk = p.w_i64 ? load_uniform((const int64_t*)p.w_blocks + si)
-                                : (int64_t)load_uniform((const int32_t*)p.w_blocks + si);
-    const int64_t off = p.w_i64 ? load_uniform((const int64_t*)p.w_offsets + si)
-                                : (int64_t)load_uniform((const int32_t*)p.w_offsets + si);
+    const int32_t* wb = (const int32_t*)p.w_blocks + (si << ws);
+    const int32_t* wo = (const int32_t*)p.w_offsets + (si << ws);
+    const int32_t b_lo = load_uniform(wb), b_hi = load_uniform(wb + ws);
+    const int32_t o_lo = load_uniform(wo), o_hi = load_uniform(wo + ws);
+    const int64_t blk = ws ? (int64_t)(((uint64_t)(uint32_t)b_hi << 32) | (uint32_t)b_lo) : (int64_t)b_lo;
+    const int64_t off = ws ? (int64_t)(((uint64_t)(uint32_t)o_hi << 32) | (uint32_t)o_lo) : (int64_t)o_lo;
     const int64_t tok = (int64_t)first_new + qi;
     if (tok < 0 || (tok >> p.logP) >= p.max_blocks || blk < 0 || blk >= p.num_blocks) continue;
     const int e = clamp_page_u(p, load_uniform((const int32_t*)p.table + table_word(p, b, (int)(tok >> p.logP))));
@@ -271,6 +275,21 @@ __device__ __forceinline__ void mfma_issue_v(const DecodeParams& p, int b, int h
       c.nv[0] = load16((const uint8_t*)src);
       c.nv[1] = load16((const uint8_t*)(src + 8));
     }
+  }
+}
+
+// The new rows' loads of chunk kk (fused writes), after its K / V loads: which lanes hold a new token and
+// their bf16 channels, as mfma_issue_k / mfma_issue_v request them.
+__device__ __forceinline__ void mfma_issue_new(const DecodeParams& p, int b, int h, int kk, int len, int lane,
+                                               int first_new, unsigned in_place, MChunk& c) {
+  int qi;
+  c.nsel_k = c.nsel_v = new_row(kk, len, first_new, in_place, lane, qi);
+  if (c.nsel_k >= 0) {
+    const int64_t row = (int64_t)b * p.n_sb + (int64_t)qi * p.n_sq + (int64_t)h * p.n_sh + 16 * (lane & 7);
+    c.nk[0] = load16((const uint8_t*)(p.nk + row));
+    c.nk[1] = load16((const uint8_t*)(p.nk + row + 8));
+    c.nv[0] = load16((const uint8_t*)(p.nv + row));
+    c.nv[1] = load16((const uint8_t*)(p.nv + row + 8));
   }
 }
 
@@ -578,8 +597,8 @@ __global__ __launch_bounds__(NW * 64, kMfmaWavesPerSimd) void decode_mfma_kernel
   int len = sread(s_len[b]);
   // Fused writes: the sequence's first new token (its new rows are the last fuse_q of its length) and the
   // head's scales, which quantize them.
-  int first_new = FUSE ? load_uniform(p.lens + b) - p.fuse_q : 0;
-  unsigned in_place = FUSE ? fused_in_place(p, b, first_new) : 0u;
+  int first_new = 0;
+  unsigned in_place = 0u;
   float ks_new = FUSE ? load_uniform(p.ks + h) : 1.0f, vs_new = FUSE ? load_uniform(p.vs + h) : 1.0f;
   float qscale = p.qscale * (SK == kScaleHead ? load_uniform(p.ks + h) : 1.0f);
   // The head's V scale is read with the piece, not at its merge: after a cold start that read is a full
@@ -589,7 +608,15 @@ __global__ __launch_bounds__(NW * 64, kMfmaWavesPerSimd) void decode_mfma_kernel
   {
     const int64_t seg_c0 = seg_start(b, h, span);
     const int k_end = (int)(min(c_end, seg_c0 + span) - seg_c0 - X);
-    if (k + wave < k_end) mfma_issue<SK, PU, FUSE>(p, b, h, k + wave, len, lane, first_new, in_place, cr);
+    // Fused writes: the first chunk's K / V loads go out before the lookup of which new rows are stored in
+    // place (a chain of scalar loads), which then runs while they are in flight.
+    if (k + wave < k_end) mfma_issue<SK, PU, false>(p, b, h, k + wave, len, lane, 0, 0u, cr);
+    if constexpr (FUSE) {
+      first_new = load_uniform(p.lens + b) - p.fuse_q;
+      in_place = fused_in_place(p, b, first_new);
+      cr.nsel_k = cr.nsel_v = -1;
+      if (k + wave < k_end) mfma_issue_new(p, b, h, k + wave, len, lane, first_new, in_place, cr);
+    }
   }
 
   for (;;) {
@@ -652,15 +679,19 @@ __global__ __launch_bounds__(NW * 64, kMfmaWavesPerSimd) void decode_mfma_kernel
       if (more) {
         len = sread(s_len[b]);
         if constexpr (FUSE) {
-          first_new = load_uniform(p.lens + b) - p.fuse_q;
-          in_place = fused_in_place(p, b, first_new);
           ks_new = load_uniform(p.ks + h);
           vs_new = load_uniform(p.vs + h);
         }
         qscale = p.qscale * (SK == kScaleHead ? load_uniform(p.ks + h) : 1.0f);
         vscale = SK == kScaleHead ? load_uniform(p.vs + h) : 1.0f;
         mfma_load_q<KV, QS>(p, b, h, rows, len, lane, qb, rlen);
-        if (wave < kn_end) mfma_issue<SK, PU, FUSE>(p, b, h, wave, len, lane, first_new, in_place, cr);
+        if (wave < kn_end) mfma_issue<SK, PU, false>(p, b, h, wave, len, lane, 0, 0u, cr);
+        if constexpr (FUSE) {
+          first_new = load_uniform(p.lens + b) - p.fuse_q;
+          in_place = fused_in_place(p, b, first_new);
+          cr.nsel_k = cr.nsel_v = -1;
+          if (wave < kn_end) mfma_issue_new(p, b, h, wave, len, lane, first_new, in_place, cr);
+        }
       }
     }
 
