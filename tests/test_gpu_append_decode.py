@@ -169,3 +169,37 @@ def test_rows_aimed_elsewhere_are_neither_stored_nor_attended(fmt, scales, nq):
         assert torch.equal(a.view(torch.uint8) if a.dtype != torch.float32 else a,
                            b.view(torch.uint8) if b.dtype != torch.float32 else b), "the pools differ"
     assert torch.equal(got, want), f"outputs differ: max {(got.float() - want.float()).abs().max()}"
+
+
+def every_bf16_row_block(b, hkv, seed):
+    """Every bf16 bit pattern but the NaNs (65536 - 254 values, the rest zeros), shuffled into [b, 1, hkv, 128]."""
+    bits = torch.arange(65536, dtype=torch.int32)
+    exp_all_ones = (bits & 0x7F80) == 0x7F80
+    nan = exp_all_ones & ((bits & 0x007F) != 0)
+    bits = torch.where(nan, torch.zeros_like(bits), bits)
+    bits = bits[torch.randperm(65536, generator=torch.Generator().manual_seed(seed))]
+    u16 = (bits & 0xFFFF).to(torch.int16)[: b * hkv * 128].reshape(b, 1, hkv, 128)
+    return u16.view(torch.bfloat16).to(DEV)
+
+
+@pytest.mark.parametrize("fmt", ["fp8", "int8"])
+@pytest.mark.parametrize("length", [1, 2])
+def test_fused_codes_of_every_bf16_value_at_adversarial_scales(fmt, length):
+    """The fused call quantizes each new row twice, in registers for its own chunk and in its store task;
+    quantize_append quantizes it once. Every non-NaN bf16 value as a new K and V channel, at per-head scales
+    that put values exactly on e4m3 / integer rounding midpoints (1.0), just off them (1 +- 2^-20 ...), tiny
+    and large: the pools and the outputs must match the two calls bit for bit. With one token per sequence
+    the output is the new V row itself; with two it depends on the new K row's scores."""
+    b, hkv = 64, 8
+    nq = 1 if fmt == "fp8" else 5  # INT8 goes through the matrix-core store from 5 rows per KV head
+    hq = 16 if fmt == "fp8" else 8
+    c = make_case(fmt, [nq + length - 1] * b, hq=hq, hkv=hkv, nq=nq, scales="head", seed=30 + length)
+    scales = torch.tensor([1.0, 1.0 + 2**-20, 1.0 - 2**-21, 3.0, 0.1, 448.0 / 7, 2.0**-10, 1.5 + 2**-18],
+                          dtype=torch.float32, device=DEV)
+    c["ks"] = scales.clone()
+    c["vs"] = scales.flip(0).contiguous()
+    rows = every_bf16_row_block(b, hkv, seed=length)
+    k_rows = rows.expand(b, nq, hkv, 128).contiguous()
+    v_rows = rows.roll(1, dims=0).expand(b, nq, hkv, 128).contiguous()
+    _, _, blocks, offsets = new_rows(c, nq, seed=3)
+    both_ways(c, k_rows, v_rows, blocks, offsets, max_context=nq + length - 1)
